@@ -1,0 +1,415 @@
+// Paged decode attention for gfx950.
+//
+// Fast path (block_size 16, head_dim 64/128, fp32 or bf16 KV): one workgroup of NW wavefronts per
+// (request, head, split). The wavefronts of a workgroup take the split's KV blocks round-robin.
+// A (block, head) tile is block_size*head_dim contiguous elements (4 KiB for fp32/64 and
+// bf16/128), so one wave-wide 16-byte load reads 1 KiB of it: lane l reads 16-byte vector
+// (round*64 + l). A token row is LPR lanes wide; a lane holds EPL elements of TPL different rows
+// per round. Scores are reduced over the LPR lanes of a row with DPP, and each group of LPR lanes
+// keeps its own online-softmax state (max m, sum l, acc) for the rows it sees, so the inner loop
+// needs no cross-row exchange. Groups merge with shuffles after the loop; wavefronts merge in LDS.
+// The next block's K and V are loaded into a second register set while the current one is used.
+#include "pa_attention.h"
+
+namespace pa {
+
+template <typename KV, int HD, int BS>
+struct DecodeShape {
+  static constexpr int EPL = Vec16<KV>::EPL;   // elements per lane per 16-byte load
+  static constexpr int LPR = HD / EPL;          // lanes per token row
+  static constexpr int TPL = kWave / LPR;       // token rows per wave-wide load
+  static constexpr int ROUNDS = BS / TPL;       // wave-wide loads per tile
+  static_assert(LPR >= 4 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "row width");
+  static_assert(BS % TPL == 0, "block size must be a multiple of rows per load");
+};
+
+template <typename KV, int R>
+__device__ __forceinline__ void load_tile(uint4 (&kb)[R], uint4 (&vb)[R], const KV* kpool,
+                                          const KV* vpool, int64_t tile_off, int lane) {
+  const uint4* kt = reinterpret_cast<const uint4*>(kpool + tile_off);
+  const uint4* vt = reinterpret_cast<const uint4*>(vpool + tile_off);
+#pragma unroll
+  for (int r = 0; r < R; ++r) kb[r] = kt[r * kWave + lane];
+#pragma unroll
+  for (int r = 0; r < R; ++r) vb[r] = vt[r * kWave + lane];
+}
+
+// Fold one tile into the lane group's online-softmax state.
+template <typename KV, int HD, int BS, int R, int E>
+__device__ __forceinline__ void fold_tile(const uint4 (&kb)[R], const uint4 (&vb)[R],
+                                          const float (&qv)[E], int tok0, int n, bool valid,
+                                          float& m, float& l, float (&acc)[E]) {
+  using S = DecodeShape<KV, HD, BS>;
+  static_assert(S::ROUNDS == R && S::EPL == E, "tile shape");
+  float sc[S::ROUNDS];
+#pragma unroll
+  for (int r = 0; r < S::ROUNDS; ++r) {
+    float kf[S::EPL];
+    Vec16<KV>::unpack(kb[r], kf);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < S::EPL; ++e) d = fmaf(qv[e], kf[e], d);
+    d = group_sum<S::LPR>(d);
+    const int t = tok0 + r * S::TPL;
+    sc[r] = (valid && t < n) ? d : -INFINITY;
+  }
+  float mx = m;
+#pragma unroll
+  for (int r = 0; r < S::ROUNDS; ++r) mx = fmaxf(mx, sc[r]);
+  const float alpha = fast_exp2(m - mx);
+  l *= alpha;
+#pragma unroll
+  for (int e = 0; e < S::EPL; ++e) acc[e] *= alpha;
+#pragma unroll
+  for (int r = 0; r < S::ROUNDS; ++r) {
+    const float p = fast_exp2(sc[r] - mx);
+    l += p;
+    float vf[S::EPL];
+    Vec16<KV>::unpack(vb[r], vf);
+#pragma unroll
+    for (int e = 0; e < S::EPL; ++e) acc[e] = fmaf(p, vf[e], acc[e]);
+  }
+  m = mx;
+}
+
+template <typename KV, typename IO, int HD, int NW>
+__global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs a) {
+  constexpr int BS = 16;
+  using S = DecodeShape<KV, HD, BS>;
+  constexpr int EPL = S::EPL, LPR = S::LPR, R = S::ROUNDS;
+
+  __shared__ float sm_acc[NW][HD];
+  __shared__ float sm_m[NW];
+  __shared__ float sm_l[NW];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int nsplit = a.num_splits;
+  const int split = blockIdx.x % nsplit;
+  const int bh_ord = blockIdx.x / nsplit;
+  const int h = bh_ord % a.H;
+  const int bi = bh_ord / a.H;
+  const int b = a.order ? a.order[bi] : bi;
+
+  const int L = a.seq_lens[b];
+  const int C = a.cur_lens[b];
+  const int n = valid_keys(L, C, 0);
+  int nb = (n + BS - 1) / BS;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+  int jb = 0, je = nb;
+  if (nsplit > 1) {
+    jb = split * a.split_blocks;
+    je = jb + a.split_blocks < nb ? jb + a.split_blocks : nb;
+    if (jb > je) jb = je;
+  }
+
+  const int r = lane % LPR;
+  const int g = lane / LPR;
+
+  float qv[EPL];
+  {
+    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + r * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[e] = Elem<IO>::load(qp + e) * a.scale_log2;
+  }
+
+  float m = kNegBig, l = 0.f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+
+  const KV* kpool = static_cast<const KV*>(a.k_pool);
+  const KV* vpool = static_cast<const KV*>(a.v_pool);
+  const int64_t tile_elems = (int64_t)BS * HD;
+  const int64_t head_off = (int64_t)h * tile_elems;
+  const int64_t blk_stride = (int64_t)a.H * tile_elems;
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+  const int64_t nblk = a.num_blocks;
+
+  // This wave's blocks: j = jb + w + k*NW for k < mine.
+  const int span = je - jb;
+  const int mine = span > w ? (span - w + NW - 1) / NW : 0;
+
+  for (int c0 = 0; c0 < mine; c0 += kWave) {
+    const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
+    int my_blk = -1;
+    if (lane < cnt) my_blk = pt[jb + w + (c0 + lane) * NW];
+
+    uint4 k0[R], v0[R], k1[R], v1[R];
+    int blk0 = __builtin_amdgcn_readlane(my_blk, 0);
+    bool ok0 = blk0 >= 0 && blk0 < nblk;
+    load_tile<KV, R>(k0, v0, kpool, vpool, (ok0 ? blk0 : 0) * blk_stride + head_off, lane);
+    int i = 0;
+    for (; i + 1 < cnt; i += 2) {
+      const int blk1 = __builtin_amdgcn_readlane(my_blk, i + 1);
+      const bool ok1 = blk1 >= 0 && blk1 < nblk;
+      load_tile<KV, R>(k1, v1, kpool, vpool, (ok1 ? blk1 : 0) * blk_stride + head_off, lane);
+      fold_tile<KV, HD, BS>(k0, v0, qv, (jb + w + (c0 + i) * NW) * BS + g, n, ok0, m, l, acc);
+      if (i + 2 < cnt) {
+        blk0 = __builtin_amdgcn_readlane(my_blk, i + 2);
+        ok0 = blk0 >= 0 && blk0 < nblk;
+        load_tile<KV, R>(k0, v0, kpool, vpool, (ok0 ? blk0 : 0) * blk_stride + head_off, lane);
+      }
+      fold_tile<KV, HD, BS>(k1, v1, qv, (jb + w + (c0 + i + 1) * NW) * BS + g, n, ok1, m, l, acc);
+    }
+    if (i < cnt) fold_tile<KV, HD, BS>(k0, v0, qv, (jb + w + (c0 + i) * NW) * BS + g, n, ok0, m, l, acc);
+  }
+
+  // Merge the TPL lane groups of this wave (lanes with equal r hold the same head_dim slice).
+#pragma unroll
+  for (int off = LPR; off < kWave; off <<= 1) {
+    const float mo = __shfl_xor(m, off);
+    const float lo = __shfl_xor(l, off);
+    const float M = fmaxf(m, mo);
+    const float sa = fast_exp2(m - M), sb = fast_exp2(mo - M);
+    l = l * sa + lo * sb;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = acc[e] * sa + __shfl_xor(acc[e], off) * sb;
+    m = M;
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) sm_acc[w][r * EPL + e] = acc[e];
+  }
+  if (lane == 0) {
+    sm_m[w] = m;
+    sm_l[w] = l;
+  }
+  __syncthreads();
+
+  float M = kNegBig;
+#pragma unroll
+  for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_m[ww]);
+  for (int d = threadIdx.x; d < HD; d += NW * kWave) {
+    float lsum = 0.f, A = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float f = fast_exp2(sm_m[ww] - M);
+      lsum = fmaf(sm_l[ww], f, lsum);
+      A = fmaf(sm_acc[ww][d], f, A);
+    }
+    if (nsplit == 1) {
+      IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+      Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
+    } else {
+      float* rec = a.ws + (((int64_t)b * a.H + h) * nsplit + split) * (HD + 2);
+      if (d == 0) {
+        rec[0] = M;
+        rec[1] = lsum;
+      }
+      rec[2 + d] = A;
+    }
+  }
+}
+
+// Merge the num_splits partial records of each (request, head): one wavefront per pair.
+template <typename IO>
+__global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
+  const int bh = blockIdx.x;
+  const int b = bh / a.H, h = bh % a.H;
+  const int HD = a.head_dim;
+  const int S = a.num_splits;
+  const float* base = a.ws + (int64_t)bh * S * (HD + 2);
+  float M = kNegBig;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, base[(int64_t)s * (HD + 2)]);
+  IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+  for (int d = threadIdx.x; d < HD; d += kWave) {
+    float lsum = 0.f, A = 0.f;
+    for (int s = 0; s < S; ++s) {
+      const float* rec = base + (int64_t)s * (HD + 2);
+      const float f = fast_exp2(rec[0] - M);
+      lsum = fmaf(rec[1], f, lsum);
+      A = fmaf(rec[2 + d], f, A);
+    }
+    Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Generic kernel: one wavefront per (request, head, query row); lanes own head_dim elements and
+// the KV positions are walked one at a time. Serves any block_size and head_dim <= 512, decode
+// or prefill.
+// ---------------------------------------------------------------------------------------------
+constexpr int kGenericMaxHd = 512;
+
+template <typename KV, typename IO>
+__global__ __launch_bounds__(kWave) void attention_generic_kernel(const AttnArgs a) {
+  constexpr int ND = kGenericMaxHd / kWave;
+  const int lane = threadIdx.x;
+  const int unit = blockIdx.x;
+  const int i = unit % a.T;
+  const int bh = unit / a.T;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int HD = a.head_dim, BS = a.block_size;
+
+  const int L = a.seq_lens[b];
+  const int C = a.cur_lens[b];
+  const int n = valid_keys(L, C, i);
+
+  const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)i * a.q_st;
+  float qv[ND], acc[ND];
+#pragma unroll
+  for (int k = 0; k < ND; ++k) {
+    const int d = lane + k * kWave;
+    qv[k] = d < HD ? Elem<IO>::load(qp + d) * a.scale_log2 : 0.f;
+    acc[k] = 0.f;
+  }
+  float m = kNegBig, l = 0.f;
+  const KV* kpool = static_cast<const KV*>(a.k_pool);
+  const KV* vpool = static_cast<const KV*>(a.v_pool);
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+
+  for (int t = 0; t < n; ++t) {
+    const int p = t / BS;
+    if (p >= a.max_pages) break;
+    const int blk = pt[p];
+    if (blk < 0 || blk >= a.num_blocks) continue;
+    const int64_t row = (((int64_t)blk * a.H + h) * BS + (t % BS)) * HD;
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < ND; ++k) {
+      const int d = lane + k * kWave;
+      if (d < HD) dot = fmaf(qv[k], Elem<KV>::load(kpool + row + d), dot);
+    }
+    dot = wave_sum(dot);
+    const float mx = fmaxf(m, dot);
+    const float alpha = fast_exp2(m - mx);
+    const float pe = fast_exp2(dot - mx);
+    l = l * alpha + pe;
+#pragma unroll
+    for (int k = 0; k < ND; ++k) {
+      const int d = lane + k * kWave;
+      const float v = d < HD ? Elem<KV>::load(vpool + row + d) : 0.f;
+      acc[k] = fmaf(pe, v, acc[k] * alpha);
+    }
+    m = mx;
+  }
+  IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_st;
+#pragma unroll
+  for (int k = 0; k < ND; ++k) {
+    const int d = lane + k * kWave;
+    if (d < HD) Elem<IO>::store(op + d, l > 0.f ? acc[k] / l : 0.f);
+  }
+}
+
+int launch_generic_attention(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream) {
+  if (a.head_dim > kGenericMaxHd)
+    PA_FAIL(PA_ERR_UNSUPPORTED, "head_dim %d exceeds the generic kernel limit %d", a.head_dim, kGenericMaxHd);
+  const int64_t units = (int64_t)a.B * a.H * a.T;
+  if (units == 0) return PA_OK;
+  if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "too many (request, head, row) units");
+  const dim3 grid((unsigned)units), block(kWave);
+  if (io_dtype == PA_DTYPE_F32 && kv_dtype == PA_DTYPE_F32)
+    attention_generic_kernel<float, float><<<grid, block, 0, stream>>>(a);
+  else if (io_dtype == PA_DTYPE_F32 && kv_dtype == PA_DTYPE_BF16)
+    attention_generic_kernel<uint16_t, float><<<grid, block, 0, stream>>>(a);
+  else if (io_dtype == PA_DTYPE_BF16 && kv_dtype == PA_DTYPE_F32)
+    attention_generic_kernel<float, uint16_t><<<grid, block, 0, stream>>>(a);
+  else
+    attention_generic_kernel<uint16_t, uint16_t><<<grid, block, 0, stream>>>(a);
+  PA_CHECK_LAUNCH("generic attention kernel");
+  return PA_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Fast-path dispatch
+// ---------------------------------------------------------------------------------------------
+constexpr int kDecodeWaves = 8;
+
+template <typename KV, typename IO, int HD>
+static void launch_decode_fast(const AttnArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)a.B * a.H * a.num_splits)), block(kDecodeWaves * kWave);
+  decode_fast_kernel<KV, IO, HD, kDecodeWaves><<<grid, block, 0, stream>>>(a);
+}
+
+template <typename IO>
+static bool dispatch_decode_fast_io(const AttnArgs& a, int kv_dtype, hipStream_t stream) {
+  if (kv_dtype == PA_DTYPE_F32) {
+    if (a.head_dim == 64) { launch_decode_fast<float, IO, 64>(a, stream); return true; }
+    if (a.head_dim == 128) { launch_decode_fast<float, IO, 128>(a, stream); return true; }
+  } else {
+    if (a.head_dim == 64) { launch_decode_fast<uint16_t, IO, 64>(a, stream); return true; }
+    if (a.head_dim == 128) { launch_decode_fast<uint16_t, IO, 128>(a, stream); return true; }
+  }
+  return false;
+}
+
+static int num_splits_for(int32_t max_pages, int32_t split_blocks) {
+  if (split_blocks <= 0 || max_pages <= split_blocks) return 1;
+  return (int)((max_pages + split_blocks - 1) / split_blocks);
+}
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
+                                           int32_t max_pages, int32_t split_blocks) {
+  const int s = num_splits_for(max_pages, split_blocks);
+  if (s <= 1 || batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return (size_t)batch * num_heads * s * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                         void* out, int64_t out_stride_b, int64_t out_stride_h, int io_dtype,
+                         const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+                         const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+                         const int32_t* seq_lens, const int32_t* cur_lens, const int32_t* order,
+                         int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                         float scale, int32_t split_blocks,
+                         void* workspace, size_t workspace_bytes, void* stream_) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(batch >= 0 && num_heads > 0 && head_dim > 0 && block_size > 0,
+               "bad sizes: batch=%d heads=%d head_dim=%d block_size=%d", batch, num_heads, head_dim,
+               block_size);
+  PA_CHECK_ARG(io_dtype == PA_DTYPE_F32 || io_dtype == PA_DTYPE_BF16, "bad io dtype %d", io_dtype);
+  PA_CHECK_ARG(kv_dtype == PA_DTYPE_F32 || kv_dtype == PA_DTYPE_BF16, "bad kv dtype %d", kv_dtype);
+  if (batch == 0) return PA_OK;
+  PA_CHECK_ARG(q && out && seq_lens && cur_lens, "null q/out/seq_lens/cur_lens");
+  PA_CHECK_ARG(max_pages >= 0, "max_pages must be >= 0");
+  if (max_pages > 0) {
+    PA_CHECK_ARG(page_table != nullptr && pt_stride >= max_pages, "page table missing or stride < max_pages");
+    PA_CHECK_ARG(k_pool && v_pool && num_blocks > 0, "KV pool missing or empty");
+  }
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+
+  AttnArgs a{};
+  a.q = q; a.q_sb = q_stride_b; a.q_sh = q_stride_h; a.q_st = 0;
+  a.out = out; a.o_sb = out_stride_b; a.o_sh = out_stride_h; a.o_st = 0;
+  a.k_pool = k_pool; a.v_pool = v_pool; a.num_blocks = num_blocks;
+  a.page_table = page_table; a.pt_stride = pt_stride; a.max_pages = max_pages;
+  a.seq_lens = seq_lens; a.cur_lens = cur_lens; a.order = order;
+  a.B = batch; a.H = num_heads; a.T = 1; a.head_dim = head_dim; a.block_size = block_size;
+  a.scale_log2 = scale * kLog2e;
+  a.num_splits = 1; a.split_blocks = 0; a.ws = nullptr;
+
+  const bool fast = block_size == 16 && (head_dim == 64 || head_dim == 128);
+  if (!fast) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
+
+  const int nsplit = num_splits_for(max_pages, split_blocks);
+  if (nsplit > 1) {
+    const size_t need = pa_decode_workspace_size(batch, num_heads, head_dim, max_pages, split_blocks);
+    if (workspace == nullptr || workspace_bytes < need)
+      PA_FAIL(PA_ERR_WORKSPACE, "decode workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
+    a.num_splits = nsplit;
+    a.split_blocks = split_blocks;
+    a.ws = static_cast<float*>(workspace);
+  }
+  if ((int64_t)batch * num_heads * nsplit > 0x7fffffffLL)
+    PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
+
+  const bool ok = io_dtype == PA_DTYPE_F32 ? dispatch_decode_fast_io<float>(a, kv_dtype, stream)
+                                           : dispatch_decode_fast_io<uint16_t>(a, kv_dtype, stream);
+  if (!ok) PA_FAIL(PA_ERR_UNSUPPORTED, "no decode kernel for head_dim %d", head_dim);
+  PA_CHECK_LAUNCH("decode kernel");
+  if (nsplit > 1) {
+    const dim3 grid((unsigned)((int64_t)batch * num_heads)), block(kWave);
+    if (io_dtype == PA_DTYPE_F32)
+      decode_merge_kernel<float><<<grid, block, 0, stream>>>(a);
+    else
+      decode_merge_kernel<uint16_t><<<grid, block, 0, stream>>>(a);
+    PA_CHECK_LAUNCH("decode merge kernel");
+  }
+  return PA_OK;
+}

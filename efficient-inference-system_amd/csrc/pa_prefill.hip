@@ -1,0 +1,277 @@
+// Chunked causal prefill attention over paged KV for gfx950, on matrix cores.
+//
+// One workgroup of 4 wavefronts per (request, head, tile of 16 query rows); the wavefronts take
+// the tile's KV blocks round-robin and merge their online-softmax states in LDS at the end.
+// For each 16-token KV block a wavefront computes the transposed score tile S^T = K Q^T (16 keys x
+// 16 queries) and accumulates the transposed output O^T += V^T P^T. With the 16x16 MFMA output
+// layout (lane = 16*G + c holds rows 4G..4G+3 of column c), lane (G, c) then owns query c's
+// scores for keys 4G..4G+3, its output column, and its softmax state, so:
+//   - the row max / row sum over keys is 4 registers plus two cross-group shuffles;
+//   - the score registers ARE the B operand (P^T) of the next product, with no data movement;
+//   - rescaling the output by the new running max is a per-lane scalar.
+// The contraction index of each product is permuted so that every lane reads contiguous 16-byte
+// vectors: the QK^T contraction slot (G, s) is head_dim index G*HD/4 + s, the PV slot (G, i) is
+// key 4G + i, and output tile t, row r holds head_dim index r*HD/16 + t. A and B use the same
+// slot->index map, so the products are exact regardless of the hardware's k ordering.
+// fp32 KV uses v_mfma_f32_16x16x4_f32 (fp32 products, like the reference). bf16 KV uses
+// v_mfma_f32_16x16x32_bf16 for QK^T (q rounded to bf16) and v_mfma_f32_16x16x16_bf16 for PV
+// (softmax weights rounded to bf16), accumulating in fp32.
+#include <type_traits>
+
+#include "pa_attention.h"
+
+namespace pa {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Load NW 32-bit words (NW in {2, 4, 8, ...}) from a 8- or 16-byte aligned address.
+template <int NWORDS>
+__device__ __forceinline__ void load_words(const void* p, uint32_t (&w)[NWORDS]) {
+  if constexpr (NWORDS % 4 == 0) {
+    const u32x4* v = static_cast<const u32x4*>(p);
+#pragma unroll
+    for (int k = 0; k < NWORDS / 4; ++k) {
+      const u32x4 x = v[k];
+      w[4 * k + 0] = x[0]; w[4 * k + 1] = x[1]; w[4 * k + 2] = x[2]; w[4 * k + 3] = x[3];
+    }
+  } else {
+    static_assert(NWORDS == 2, "word count");
+    const u32x2 x = *static_cast<const u32x2*>(p);
+    w[0] = x[0]; w[1] = x[1];
+  }
+}
+
+template <typename KV, typename IO, int HD>
+__global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
+  constexpr int BS = 16;
+  constexpr int NW = 4;
+  constexpr int QD = HD / 4;   // head_dim values per lane in the QK^T operands
+  constexpr int DT = HD / 16;  // output tiles of 16 head_dim columns
+  constexpr bool kBf16 = std::is_same<KV, uint16_t>::value;
+
+  __shared__ float sm_o[NW][16][HD + 1];
+  __shared__ float sm_m[NW][16];
+  __shared__ float sm_l[NW][16];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int G = lane >> 4;
+  const int c = lane & 15;
+
+  const int ntiles = (a.T + 15) / 16;
+  const int qt = blockIdx.x % ntiles;
+  const int bh = blockIdx.x / ntiles;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int i0 = qt * 16;
+  const int i = i0 + c;
+
+  const int L = a.seq_lens[b];
+  const int C = a.cur_lens[b];
+  const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
+  const int i_last = (i0 + 15) < (a.T - 1) ? (i0 + 15) : (a.T - 1);
+  const int n_max = valid_keys(L, C, i_last);  // nondecreasing in the row index
+  int nb = (n_max + BS - 1) / BS;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+
+  // Q operand: row i, head_dim [G*QD, G*QD + QD), pre-scaled into the log2 domain.
+  float qv[QD];
+  {
+    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
+                   (int64_t)(i < a.T ? i : 0) * a.q_st + G * QD;
+#pragma unroll
+    for (int s = 0; s < QD; ++s) qv[s] = i < a.T ? Elem<IO>::load(qp + s) * a.scale_log2 : 0.f;
+  }
+  bf16x8 qb[kBf16 ? QD / 8 : 1];
+  if constexpr (kBf16) {
+#pragma unroll
+    for (int s = 0; s < QD / 8; ++s) {
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        wd[e] = (uint32_t)f32_to_bf16(qv[8 * s + 2 * e]) | ((uint32_t)f32_to_bf16(qv[8 * s + 2 * e + 1]) << 16);
+      const u32x4 x = {wd[0], wd[1], wd[2], wd[3]};
+      qb[s] = __builtin_bit_cast(bf16x8, x);
+    }
+  }
+
+  f32x4 oacc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = kNegBig, l = 0.f;
+
+  const KV* kpool = static_cast<const KV*>(a.k_pool);
+  const KV* vpool = static_cast<const KV*>(a.v_pool);
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+
+  for (int j = w; j < nb; j += NW) {
+    const int blk = pt[j];
+    const bool ok = blk >= 0 && blk < a.num_blocks;
+    const int64_t tile = ((int64_t)(ok ? blk : 0) * a.H + h) * (BS * HD);
+
+    // ---- S^T = K Q^T --------------------------------------------------------------------
+    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (!kBf16) {
+      uint32_t kw[QD];
+      load_words<QD>(kpool + tile + c * HD + G * QD, kw);
+#pragma unroll
+      for (int s = 0; s < QD; ++s)
+        sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kw[s]), qv[s], sacc, 0, 0, 0);
+    } else {
+      uint32_t kw[QD / 2];
+      load_words<QD / 2>(kpool + tile + c * HD + G * QD, kw);
+#pragma unroll
+      for (int s = 0; s < QD / 8; ++s) {
+        const u32x4 x = {kw[4 * s], kw[4 * s + 1], kw[4 * s + 2], kw[4 * s + 3]};
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x), qb[s], sacc, 0, 0, 0);
+      }
+    }
+
+    // ---- online softmax over this block's keys, per query column c ------------------------
+    float p[4];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = j * BS + 4 * G + r;
+      p[r] = (ok && t < n_c) ? sacc[r] : -INFINITY;
+      mloc = fmaxf(mloc, p[r]);
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const float mnew = fmaxf(m, mloc);
+    const float alpha = fast_exp2(m - mnew);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = fast_exp2(p[r] - mnew);
+      ps += p[r];
+    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l = l * alpha + ps;
+    m = mnew;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+
+    // ---- O^T += V^T P^T -------------------------------------------------------------------
+    if constexpr (!kBf16) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint32_t vw[DT];
+        load_words<DT>(vpool + tile + (4 * G + r) * HD + c * DT, vw);
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vw[t]), p[r], oacc[t], 0, 0, 0);
+      }
+    } else {
+      uint32_t vw[4][DT / 2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) load_words<DT / 2>(vpool + tile + (4 * G + r) * HD + c * DT, vw[r]);
+      const s16x4 pb = {(short)f32_to_bf16(p[0]), (short)f32_to_bf16(p[1]), (short)f32_to_bf16(p[2]),
+                        (short)f32_to_bf16(p[3])};
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const int sh = (t & 1) * 16;
+        const s16x4 av = {(short)(vw[0][t >> 1] >> sh), (short)(vw[1][t >> 1] >> sh),
+                          (short)(vw[2][t >> 1] >> sh), (short)(vw[3][t >> 1] >> sh)};
+        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb, oacc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- merge the wavefronts' states and write the tile -----------------------------------
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm_o[w][c][(4 * G + r) * DT + t] = oacc[t][r];
+  if (G == 0) {
+    sm_m[w][c] = m;
+    sm_l[w][c] = l;
+  }
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < 16 * HD; idx += NW * kWave) {
+    const int cc = idx / HD;
+    const int d = idx - cc * HD;
+    const int row = i0 + cc;
+    if (row >= a.T) continue;
+    float M = kNegBig;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_m[ww][cc]);
+    float lsum = 0.f, A = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float f = fast_exp2(sm_m[ww][cc] - M);
+      lsum = fmaf(sm_l[ww][cc], f, lsum);
+      A = fmaf(sm_o[ww][cc][d], f, A);
+    }
+    IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
+    Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
+  }
+}
+
+template <typename KV, typename IO>
+static bool dispatch_prefill_io(const AttnArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.head_dim == 64) { prefill_mfma_kernel<KV, IO, 64><<<grid, 256, 0, stream>>>(a); return true; }
+  if (a.head_dim == 128) { prefill_mfma_kernel<KV, IO, 128><<<grid, 256, 0, stream>>>(a); return true; }
+  return false;
+}
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                          void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
+                          int io_dtype,
+                          const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+                          const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+                          const int32_t* seq_lens, const int32_t* cur_lens,
+                          int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
+                          int32_t block_size, float scale, void* stream_) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(batch >= 0 && num_heads > 0 && query_len >= 0 && head_dim > 0 && block_size > 0,
+               "bad sizes: batch=%d heads=%d query_len=%d head_dim=%d block_size=%d", batch, num_heads,
+               query_len, head_dim, block_size);
+  PA_CHECK_ARG(io_dtype == PA_DTYPE_F32 || io_dtype == PA_DTYPE_BF16, "bad io dtype %d", io_dtype);
+  PA_CHECK_ARG(kv_dtype == PA_DTYPE_F32 || kv_dtype == PA_DTYPE_BF16, "bad kv dtype %d", kv_dtype);
+  if (batch == 0 || query_len == 0) return PA_OK;
+  PA_CHECK_ARG(q && out && seq_lens && cur_lens, "null q/out/seq_lens/cur_lens");
+  PA_CHECK_ARG(max_pages >= 0, "max_pages must be >= 0");
+  if (max_pages > 0) {
+    PA_CHECK_ARG(page_table != nullptr && pt_stride >= max_pages, "page table missing or stride < max_pages");
+    PA_CHECK_ARG(k_pool && v_pool && num_blocks > 0, "KV pool missing or empty");
+  }
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+
+  AttnArgs a{};
+  a.q = q; a.q_sb = q_stride_b; a.q_sh = q_stride_h; a.q_st = q_stride_t;
+  a.out = out; a.o_sb = out_stride_b; a.o_sh = out_stride_h; a.o_st = out_stride_t;
+  a.k_pool = k_pool; a.v_pool = v_pool; a.num_blocks = num_blocks;
+  a.page_table = page_table; a.pt_stride = pt_stride; a.max_pages = max_pages;
+  a.seq_lens = seq_lens; a.cur_lens = cur_lens; a.order = nullptr;
+  a.B = batch; a.H = num_heads; a.T = query_len; a.head_dim = head_dim; a.block_size = block_size;
+  a.scale_log2 = scale * kLog2e;
+  a.num_splits = 1; a.split_blocks = 0; a.ws = nullptr;
+
+  const bool fast = block_size == 16 && (head_dim == 64 || head_dim == 128);
+  if (!fast) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
+
+  const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);
+  if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
+  const dim3 grid((unsigned)units);
+  bool ok;
+  if (kv_dtype == PA_DTYPE_F32)
+    ok = io_dtype == PA_DTYPE_F32 ? dispatch_prefill_io<float, float>(a, grid, stream)
+                                  : dispatch_prefill_io<float, uint16_t>(a, grid, stream);
+  else
+    ok = io_dtype == PA_DTYPE_F32 ? dispatch_prefill_io<uint16_t, float>(a, grid, stream)
+                                  : dispatch_prefill_io<uint16_t, uint16_t>(a, grid, stream);
+  if (!ok) PA_FAIL(PA_ERR_UNSUPPORTED, "no prefill kernel for head_dim %d", head_dim);
+  PA_CHECK_LAUNCH("prefill kernel");
+  return PA_OK;
+}

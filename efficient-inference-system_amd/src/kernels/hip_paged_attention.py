@@ -1,0 +1,244 @@
+"""torch-facing wrappers over the libpaged_hip C ABI (HIP kernels for gfx950).
+
+These replace the reference's Triton launch wrappers with the same argument meaning:
+  paged_attention_decode_hip  <- paged_attention_decode_triton  (triton_paged_attention.py:179-217)
+  paged_attention_prefill_hip <- paged_attention_prefill_triton (triton_paged_attention.py:220-258)
+and add the device-side cache operations the reference does with per-request Python loops:
+  kv_append_hip      <- PagedKVCacheState.append slice copies   (src/cache/paged_kv.py:102-120)
+  pack_metadata_hip  <- page_table_tensor / seq_lens_tensor      (src/cache/paged_kv.py:174-197)
+  zero_blocks_hip    <- LayerBlockPool.release_block zero_()     (src/cache/paged_kv.py:80-85)
+
+All work is enqueued on torch's current stream; nothing here synchronises. Every tensor must live
+on a HIP device: there is no CPU path.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from src.kernels import _lib
+
+_workspaces: dict[int, torch.Tensor] = {}
+_cu_counts: dict[int, int] = {}
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(name: str, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError(f"{name}: the hip_paged backend needs tensors on a HIP device, got {t.device}")
+
+
+def _require_i32(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.int32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous int32 tensor (got {t.dtype}, contiguous={t.is_contiguous()})")
+
+
+def cu_count(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _cu_counts:
+        _cu_counts[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _cu_counts[idx]
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[idx] = ws
+    return ws
+
+
+def default_split_blocks(batch: int, num_heads: int, max_pages: int, device: torch.device) -> int:
+    """KV blocks per decode split: 0 (no split) when (request, head) pairs alone fill the GPU,
+    otherwise enough splits for about two workgroups per compute unit, never under 16 blocks."""
+    units = batch * num_heads
+    target = 2 * cu_count(device)
+    if units == 0 or units >= target or max_pages <= 32:
+        return 0
+    splits = math.ceil(target / units)
+    blocks = max(16, math.ceil(max_pages / splits))
+    return 0 if blocks >= max_pages else blocks
+
+
+def _check_pool(name: str, k_pool: torch.Tensor, v_pool: torch.Tensor) -> None:
+    if k_pool.dim() != 4 or k_pool.shape != v_pool.shape or k_pool.dtype != v_pool.dtype:
+        raise ValueError(f"{name}: K/V pools must share shape [num_blocks, H, block_size, head_dim] and dtype")
+    if not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError(f"{name}: K/V pools must be contiguous")
+
+
+def paged_attention_decode_hip(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    current_lengths: torch.Tensor,
+    *,
+    order: torch.Tensor | None = None,
+    split_blocks: int | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Decode attention for q [B, H, 1, Hd]; returns a tensor shaped and strided like q."""
+    _require_gpu("paged_attention_decode_hip", q, k_pool, v_pool, page_table, seq_lens, current_lengths)
+    _check_pool("paged_attention_decode_hip", k_pool, v_pool)
+    B, H, T, Hd = q.shape
+    if T != 1:
+        raise ValueError(f"decode expects query_len 1, got {T}")
+    if q.stride(3) != 1:
+        q = q.contiguous()
+    nblk, Hp, bs, Hdp = k_pool.shape
+    if (Hp, Hdp) != (H, Hd):
+        raise ValueError(f"pool heads/head_dim {Hp}/{Hdp} do not match q {H}/{Hd}")
+    _require_i32("page_table", page_table)
+    _require_i32("seq_lens", seq_lens)
+    _require_i32("current_lengths", current_lengths)
+    if order is not None:
+        _require_i32("order", order)
+    if out is None:
+        out = torch.empty_like(q)
+    if out.stride(3) != 1:
+        raise ValueError("out must have unit stride along head_dim")
+    max_pages = page_table.shape[1] if page_table.dim() == 2 else 0
+    pt_stride = page_table.stride(0) if page_table.dim() == 2 and B > 0 else max_pages
+    if split_blocks is None:
+        split_blocks = default_split_blocks(B, H, max_pages, q.device)
+    lib = _lib.load()
+    ws_bytes = lib.pa_decode_workspace_size(B, H, Hd, max_pages, split_blocks)
+    ws_ptr = _workspace(q.device, ws_bytes).data_ptr() if ws_bytes else None
+    status = lib.pa_decode(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1), _lib.dtype_code(q.dtype),
+        k_pool.data_ptr(), v_pool.data_ptr(), _lib.dtype_code(k_pool.dtype), nblk,
+        page_table.data_ptr() if max_pages else None, pt_stride, max_pages,
+        seq_lens.data_ptr(), current_lengths.data_ptr(), order.data_ptr() if order is not None else None,
+        B, H, Hd, bs,
+        1.0 / math.sqrt(Hd), split_blocks,
+        ws_ptr, ws_bytes, _stream_ptr(q.device),
+    )
+    _lib.check(status, "pa_decode")
+    return out
+
+
+def paged_attention_prefill_hip(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    current_lengths: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Chunked causal prefill attention for q [B, H, T, Hd]; returns a tensor shaped like q."""
+    _require_gpu("paged_attention_prefill_hip", q, k_pool, v_pool, page_table, seq_lens, current_lengths)
+    _check_pool("paged_attention_prefill_hip", k_pool, v_pool)
+    B, H, T, Hd = q.shape
+    if q.stride(3) != 1:
+        q = q.contiguous()
+    nblk, Hp, bs, Hdp = k_pool.shape
+    if (Hp, Hdp) != (H, Hd):
+        raise ValueError(f"pool heads/head_dim {Hp}/{Hdp} do not match q {H}/{Hd}")
+    _require_i32("page_table", page_table)
+    _require_i32("seq_lens", seq_lens)
+    _require_i32("current_lengths", current_lengths)
+    if out is None:
+        out = torch.empty_like(q)
+    max_pages = page_table.shape[1] if page_table.dim() == 2 else 0
+    pt_stride = page_table.stride(0) if page_table.dim() == 2 and B > 0 else max_pages
+    lib = _lib.load()
+    status = lib.pa_prefill(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _lib.dtype_code(q.dtype),
+        k_pool.data_ptr(), v_pool.data_ptr(), _lib.dtype_code(k_pool.dtype), nblk,
+        page_table.data_ptr() if max_pages else None, pt_stride, max_pages,
+        seq_lens.data_ptr(), current_lengths.data_ptr(),
+        B, H, T, Hd, bs,
+        1.0 / math.sqrt(Hd), _stream_ptr(q.device),
+    )
+    _lib.check(status, "pa_prefill")
+    return out
+
+
+def kv_append_hip(
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """Scatter k_new/v_new [B, H, T, Hd] rows into pool slots (slot_mapping int32 [B*T], -1 = skip)."""
+    _require_gpu("kv_append_hip", k_new, v_new, k_pool, v_pool, slot_mapping)
+    _check_pool("kv_append_hip", k_pool, v_pool)
+    _require_i32("slot_mapping", slot_mapping)
+    B, H, T, Hd = k_new.shape
+    if v_new.shape != k_new.shape or v_new.dtype != k_new.dtype:
+        raise ValueError("k_new and v_new must have the same shape and dtype")
+    if k_new.stride() != v_new.stride() or k_new.stride(3) != 1:
+        k_new = k_new.contiguous()
+        v_new = v_new.contiguous()
+    if slot_mapping.numel() != B * T:
+        raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries, expected {B * T}")
+    nblk, Hp, bs, Hdp = k_pool.shape
+    if (Hp, Hdp) != (H, Hd):
+        raise ValueError(f"pool heads/head_dim {Hp}/{Hdp} do not match new rows {H}/{Hd}")
+    status = _lib.load().pa_kv_append(
+        k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1), k_new.stride(2),
+        _lib.dtype_code(k_new.dtype),
+        k_pool.data_ptr(), v_pool.data_ptr(), _lib.dtype_code(k_pool.dtype), nblk,
+        slot_mapping.data_ptr(), B, H, T, Hd, bs, _stream_ptr(k_new.device),
+    )
+    _lib.check(status, "pa_kv_append")
+
+
+def pack_metadata_hip(
+    block_ids: torch.Tensor,
+    row_offsets: torch.Tensor,
+    prev_lens: torch.Tensor,
+    append_lens: torch.Tensor,
+    *,
+    query_len: int,
+    block_size: int,
+    max_pages: int,
+    with_slots: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """Build (page_table int32 [B, max_pages], seq_lens int32 [B], seq_lens int64 [B],
+    slot_mapping int32 [B*query_len] or None) on the device from CSR block lists."""
+    _require_gpu("pack_metadata_hip", block_ids, row_offsets, prev_lens, append_lens)
+    for name, t in (("block_ids", block_ids), ("row_offsets", row_offsets), ("prev_lens", prev_lens),
+                    ("append_lens", append_lens)):
+        _require_i32(name, t)
+    B = prev_lens.numel()
+    dev = prev_lens.device
+    page_table = torch.empty((B, max_pages), dtype=torch.int32, device=dev)
+    seq32 = torch.empty((B,), dtype=torch.int32, device=dev)
+    seq64 = torch.empty((B,), dtype=torch.int64, device=dev)
+    slots = torch.empty((B * query_len,), dtype=torch.int32, device=dev) if with_slots else None
+    status = _lib.load().pa_pack_metadata(
+        block_ids.data_ptr() if block_ids.numel() else None, row_offsets.data_ptr(),
+        prev_lens.data_ptr(), append_lens.data_ptr(),
+        B, query_len, block_size, max_pages,
+        page_table.data_ptr() if max_pages else None, max_pages, seq32.data_ptr(), seq64.data_ptr(),
+        slots.data_ptr() if slots is not None else None, _stream_ptr(dev),
+    )
+    _lib.check(status, "pa_pack_metadata")
+    return page_table, seq32, seq64, slots
+
+
+def zero_blocks_hip(k_pool: torch.Tensor, v_pool: torch.Tensor, block_ids: torch.Tensor) -> None:
+    """Zero the K and V tiles of the given pool blocks (int32 ids on device) in one launch."""
+    _require_gpu("zero_blocks_hip", k_pool, v_pool, block_ids)
+    _check_pool("zero_blocks_hip", k_pool, v_pool)
+    _require_i32("block_ids", block_ids)
+    nblk, H, bs, Hd = k_pool.shape
+    status = _lib.load().pa_zero_blocks(
+        k_pool.data_ptr(), v_pool.data_ptr(), _lib.dtype_code(k_pool.dtype), nblk, H, bs, Hd,
+        block_ids.data_ptr(), block_ids.numel(), _stream_ptr(k_pool.device),
+    )
+    _lib.check(status, "pa_zero_blocks")

@@ -1,0 +1,151 @@
+/*
+ * paged_hip.h — C ABI of libpaged_hip.so, the MI355X (gfx950) paged-attention backend.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, plus the HIP stream
+ * (as `void*`, a `hipStream_t`) to launch on. None of them allocates device memory, synchronises
+ * the stream or reads device memory on the host. All return PA_OK (0) or a PA_ERR_* code;
+ * pa_last_error_message() describes the most recent failure of the calling thread.
+ *
+ * Data layout contract (the reference's, jacobzhang22/efficient-inference-system):
+ *   - KV pool K and V:  [num_blocks, num_heads, block_size, head_dim], contiguous
+ *                        (src/cache/paged_kv.py:54-61 of the reference).
+ *   - q / out:           [B, H, T, head_dim] with arbitrary element strides for B, H, T and unit
+ *                        stride for head_dim (the reference passes a transposed view,
+ *                        src/model/attention.py:25-29).
+ *   - page_table:        int32 [B, max_pages] with row stride pt_stride, -1 padded
+ *                        (src/cache/paged_kv.py:174-193).
+ *   - seq_lens:          int32 [B], the cached length of each request AFTER the append
+ *                        (src/cache/paged_kv.py:195-197).
+ *   - cur_lens:          int32 [B], the request's current_lengths value
+ *                        (src/kernels/paged_attention.py:27-32).
+ *
+ * Attention semantics (src/kernels/reference_paged_attention.py:10-59): for request b, head h and
+ * query row i, with L = seq_lens[b] and C = cur_lens[b], the row attends key positions
+ * t < n_i = clamp(min(L, L - C + 1 + i), 0, L) with softmax(q.k * scale) weights; a row with no
+ * key (n_i == 0) is all zeros. Rows i >= C (padding) follow the same formula. Keys whose page-table
+ * entry is negative or >= num_blocks are skipped, like the reference Triton kernels skip -1 pages
+ * (src/kernels/triton_paged_attention.py:55).
+ */
+#ifndef PAGED_HIP_H_
+#define PAGED_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of q/out ("io") and of the KV pool. */
+enum pa_dtype {
+  PA_DTYPE_F32 = 0,
+  PA_DTYPE_BF16 = 1,
+};
+
+/* Status codes. */
+enum pa_status {
+  PA_OK = 0,
+  PA_ERR_INVALID_ARGUMENT = 1, /* a null pointer, negative size or inconsistent shape */
+  PA_ERR_UNSUPPORTED = 2,      /* a dtype / head_dim / block_size combination with no kernel */
+  PA_ERR_WORKSPACE = 3,        /* workspace missing or smaller than pa_decode_workspace_size() */
+  PA_ERR_HIP = 4,              /* a HIP runtime call failed (launch or attribute query) */
+};
+
+/* Library version, major*10000 + minor*100 + patch. */
+int pa_version(void);
+
+/* Human-readable message for the most recent failing call on this thread ("" if none). */
+const char* pa_last_error_message(void);
+
+/*
+ * Paged DECODE attention (query_len == 1).
+ * Replaces the reference's paged_attention_decode_triton
+ * (src/kernels/triton_paged_attention.py:179-217) behind paged_attention()
+ * (src/kernels/paged_attention.py:34-42).
+ *
+ * One workgroup of wavefronts per (request, head, split); the wavefronts split the request's KV
+ * blocks between them and merge their online-softmax states in LDS. When split_blocks > 0 and a
+ * request has more than split_blocks KV blocks, its blocks are also divided among several
+ * workgroups whose partial results are merged by a second kernel; that path needs a workspace of
+ * pa_decode_workspace_size() bytes (no zeroing needed). split_blocks <= 0 means one workgroup per
+ * (request, head) and no workspace.
+ *
+ * order: optional int32 [B] permutation giving the processing order of requests (e.g. longest
+ * first, for load balance); NULL means 0..B-1. Results do not depend on it.
+ */
+int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+              void* out, int64_t out_stride_b, int64_t out_stride_h, int io_dtype,
+              const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+              const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+              const int32_t* seq_lens, const int32_t* cur_lens, const int32_t* order,
+              int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
+              float scale, int32_t split_blocks,
+              void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace pa_decode needs for these sizes (0 when split_blocks <= 0 or no request can
+ * need more than one split). No reference counterpart: the Triton decode path has no split-K. */
+size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
+                                int32_t max_pages, int32_t split_blocks);
+
+/*
+ * Paged chunked-PREFILL attention (any query_len >= 1), causal over cached context plus the
+ * in-chunk prefix. Replaces paged_attention_prefill_triton
+ * (src/kernels/triton_paged_attention.py:220-258) behind paged_attention()
+ * (src/kernels/paged_attention.py:44-51). fp32 KV uses fp32 MFMA (16x16x4); bf16 KV uses bf16
+ * MFMA with fp32 accumulation (q and the softmax weights are rounded to bf16 for the products).
+ */
+int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+               void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
+               int io_dtype,
+               const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+               const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+               const int32_t* seq_lens, const int32_t* cur_lens,
+               int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
+               int32_t block_size, float scale, void* stream);
+
+/*
+ * KV append / scatter: writes k_new[b, :, j, :] and v_new[b, :, j, :] into pool slot
+ * slot_mapping[b * query_len + j] (slot = block_id * block_size + offset; a negative slot skips
+ * the row). Values are converted to the pool dtype (fp32 -> bf16 rounds to nearest even).
+ * Replaces the per-request slice copies of PagedKVCacheState.append
+ * (src/cache/paged_kv.py:102-120) driven by BatchedPagedKVCache.append_batch (:151-172).
+ * Slots whose block is outside [0, num_blocks) are skipped.
+ */
+int pa_kv_append(const void* k_new, const void* v_new, int64_t new_stride_b, int64_t new_stride_h,
+                 int64_t new_stride_t, int new_dtype,
+                 void* k_pool, void* v_pool, int pool_dtype, int64_t num_blocks,
+                 const int32_t* slot_mapping,
+                 int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
+                 int32_t block_size, void* stream);
+
+/*
+ * Ragged metadata packing for one batched append + attention call, from a CSR list of each
+ * request's block ids (block_ids[row_offsets[b] .. row_offsets[b+1]) ):
+ *   page_table[b, p]  = block id p of request b, or -1 past its end (p < max_pages);
+ *                       replaces BatchedPagedKVCache.page_table_tensor (src/cache/paged_kv.py:174-193)
+ *   seq_lens[b]       = prev_lens[b] + append_lens[b]   (int32; seq_lens64 gets the same as int64
+ *                       when non-NULL, the value append_batch returns, src/cache/paged_kv.py:172)
+ *   slot_mapping[b*query_len + j] = slot of the j-th appended token of request b for
+ *                       j < append_lens[b], else -1 (NULL skips it)
+ * append_lens must already be clamped to [0, query_len] (src/cache/paged_kv.py:169).
+ */
+int pa_pack_metadata(const int32_t* block_ids, const int32_t* row_offsets,
+                     const int32_t* prev_lens, const int32_t* append_lens,
+                     int32_t batch, int32_t query_len, int32_t block_size, int32_t max_pages,
+                     int32_t* page_table, int64_t pt_stride, int32_t* seq_lens,
+                     int64_t* seq_lens64, int32_t* slot_mapping, void* stream);
+
+/*
+ * Zero the K and V tiles of n_ids pool blocks (block_ids on device), the batched form of
+ * LayerBlockPool.release_block's per-block zero_() (src/cache/paged_kv.py:80-85).
+ * Ids outside [0, num_blocks) are skipped.
+ */
+int pa_zero_blocks(void* k_pool, void* v_pool, int pool_dtype, int64_t num_blocks,
+                   int32_t num_heads, int32_t block_size, int32_t head_dim,
+                   const int32_t* block_ids, int32_t n_ids, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGED_HIP_H_ */

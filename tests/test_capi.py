@@ -1,0 +1,66 @@
+"""The C-ABI library loads and exports exactly what include/paged_hip.h declares (no GPU needed:
+these tests only resolve symbols and call the pure host functions)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from src.kernels import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "paged_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("build_lib", _lib.LIB_PATH.parent / "build_lib.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return _lib.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == sorted([
+        "pa_decode", "pa_decode_workspace_size", "pa_kv_append", "pa_last_error_message",
+        "pa_pack_metadata", "pa_prefill", "pa_version", "pa_zero_blocks",
+    ])
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared_functions():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_ctypes_signatures_cover_the_header():
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_host_only_entry_points(lib):
+    assert lib.pa_version() == 100
+    # no split -> no workspace; a split of 16 blocks over 64 pages -> 4 partial records per (b, h)
+    assert lib.pa_decode_workspace_size(8, 8, 64, 64, 0) == 0
+    assert lib.pa_decode_workspace_size(8, 8, 64, 64, 16) == 8 * 8 * 4 * (64 + 2) * 4
+    assert lib.pa_decode_workspace_size(8, 8, 64, 16, 16) == 0
+
+
+def test_argument_errors_are_reported_without_a_device(lib):
+    # invalid sizes are rejected on the host before any HIP call
+    st = lib.pa_decode(None, 0, 0, None, 0, 0, 0, None, None, 0, 0, None, 0, 0, None, None, None,
+                       1, 0, 64, 16, 1.0, 0, None, 0, None)
+    assert st == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"bad sizes" in lib.pa_last_error_message()
+    st = lib.pa_kv_append(None, None, 0, 0, 0, 7, None, None, 0, 0, None, 1, 1, 1, 1, 1, None)
+    assert st == _lib.PA_ERR_INVALID_ARGUMENT
+    # zero-sized work is a no-op success
+    assert lib.pa_prefill(None, 0, 0, 0, None, 0, 0, 0, 0, None, None, 0, 0, None, 0, 0, None, None,
+                          0, 8, 4, 64, 16, 1.0, None) == _lib.PA_OK

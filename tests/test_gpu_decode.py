@@ -1,0 +1,173 @@
+"""HIP paged DECODE attention vs the oracle (fp32 within 1e-4; bf16 KV within 2e-2 of the fp32
+result on the unrounded values and within 1e-4 of the oracle on the same bf16 values)."""
+import math
+import os
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from src import workloads
+from src.kernels.hip_paged_attention import paged_attention_decode_hip
+
+pytestmark = pytest.mark.gpu
+NTHREADS = min(16, os.cpu_count() or 1)
+
+
+def run(batch, **kw):
+    return paged_attention_decode_hip(batch.q, batch.k_pool, batch.v_pool, batch.page_table, batch.seq_lens_t,
+                                      batch.cur_lens_t, **kw)
+
+
+def oracle_out(batch):
+    return oracle.paged_attention(batch.q.cpu(), batch.k_pool.cpu(), batch.v_pool.cpu(), batch.block_lists,
+                                  batch.seq_lens, batch.cur_lens, nthreads=NTHREADS)
+
+
+def make_batch(device, seed, lens, curs, H, Hd, bs=16, kv_dtype=torch.float32, io_dtype=torch.float32, spare=7):
+    g = torch.Generator().manual_seed(seed)
+    need = sum(math.ceil(L / bs) for L in lens)
+    N = need + spare
+    perm = torch.randperm(N, generator=g).tolist()
+    lists, pos = [], 0
+    for L in lens:
+        n = math.ceil(L / bs)
+        lists.append(perm[pos:pos + n])
+        pos += n
+    B = len(lens)
+    q = torch.randn(B, H, 1, Hd, generator=g).to(io_dtype).to(device)
+    k = torch.randn(N, H, bs, Hd, generator=g).to(kv_dtype).to(device)
+    v = torch.randn(N, H, bs, Hd, generator=g).to(kv_dtype).to(device)
+    return workloads._batch(q, k, v, lists, list(lens), list(curs), device)
+
+
+def max_err(got, want):
+    return float(np.abs(got.float().cpu().numpy() - want).max()) if want.size else 0.0
+
+
+def test_single_decode_config(device):
+    b = workloads.single_decode(seed=0, device=device)
+    print("single decode: B=1 H=8 Hd=64 L=128", flush=True)
+    assert max_err(run(b), oracle_out(b)) <= 1e-4
+
+
+@pytest.mark.parametrize("layer", range(6))
+def test_ragged_decode_config(device, layer):
+    b = workloads.ragged_decode(seed=0, layer=layer, device=device)
+    print(f"ragged decode layer {layer}: lens={b.seq_lens}", flush=True)
+    assert max_err(run(b), oracle_out(b)) <= 1e-4
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
+def test_decode_fast_kernel_variants(device, kv_dtype, head_dim, io_dtype):
+    lens = [1, 15, 16, 17, 100, 257, 700, 1500]
+    b = make_batch(device, 3, lens, [1] * len(lens), H=4, Hd=head_dim, kv_dtype=kv_dtype, io_dtype=io_dtype)
+    print(f"decode variant kv={kv_dtype} hd={head_dim} io={io_dtype}", flush=True)
+    got = run(b)
+    assert got.dtype == io_dtype
+    want = oracle.paged_attention(b.q.float().cpu(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists, b.seq_lens,
+                                  b.cur_lens, nthreads=NTHREADS)
+    tol = 1e-4 if io_dtype == torch.float32 else 1e-2  # bf16 output rounding: |out| <= ~4, ulp 2^-6
+    assert max_err(got, want) <= tol
+
+
+def test_bf16_kv_against_unrounded_fp32(device):
+    lens = [33, 400, 1024, 3000]
+    b32 = make_batch(device, 4, lens, [1] * 4, H=8, Hd=128, kv_dtype=torch.float32)
+    want = oracle_out(b32)
+    got = paged_attention_decode_hip(b32.q, b32.k_pool.to(torch.bfloat16), b32.v_pool.to(torch.bfloat16),
+                                     b32.page_table, b32.seq_lens_t, b32.cur_lens_t)
+    assert max_err(got, want) <= 2e-2
+
+
+@pytest.mark.parametrize("split_blocks", [1, 3, 16])
+def test_split_path_matches_oracle_and_unsplit(device, split_blocks):
+    lens = [5, 64, 200, 1000, 2049]
+    b = make_batch(device, 5, lens, [1] * 5, H=3, Hd=64)
+    print(f"split decode split_blocks={split_blocks}", flush=True)
+    got = run(b, split_blocks=split_blocks)
+    assert max_err(got, oracle_out(b)) <= 1e-4
+    assert max_err(got, run(b, split_blocks=0).cpu().numpy()) <= 1e-5
+
+
+@pytest.mark.parametrize("Hd,bs", [(16, 8), (32, 16), (96, 16), (64, 32), (80, 4)])
+def test_generic_kernel_shapes(device, Hd, bs):
+    lens = [1, 9, 40, 130]
+    b = make_batch(device, 6, lens, [1] * 4, H=2, Hd=Hd, bs=bs)
+    print(f"generic decode Hd={Hd} bs={bs}", flush=True)
+    assert max_err(run(b), oracle_out(b)) <= 1e-4
+
+
+def test_edge_lengths_and_current_lengths(device):
+    # empty request, single key, block edges; current_lengths 0 (attend all), >1 (fewer keys),
+    # > seq_len (no key -> zeros)
+    lens = [0, 1, 15, 16, 17, 33, 50, 64]
+    curs = [1, 1, 0, 2, 17, 40, 3, 1]
+    b = make_batch(device, 7, lens, curs, H=2, Hd=64)
+    got = run(b)
+    want = oracle_out(b)
+    assert max_err(got, want) <= 1e-4
+    assert torch.count_nonzero(got[0]).item() == 0 and torch.count_nonzero(got[5]).item() == 0
+
+
+def test_strided_views_like_the_model(device):
+    B, H, Hd = 4, 8, 64
+    base = make_batch(device, 8, [70, 16, 300, 5], [1] * 4, H=H, Hd=Hd)
+    x = torch.randn(B, 1, H * Hd, device=device)
+    q = x.view(B, 1, H, Hd).transpose(1, 2)  # the model's [B, H, T, Hd] view
+    assert not q.is_contiguous()
+    out = paged_attention_decode_hip(q, base.k_pool, base.v_pool, base.page_table, base.seq_lens_t, base.cur_lens_t)
+    assert out.stride() == q.stride()
+    want = oracle.paged_attention(q.cpu().contiguous(), base.k_pool.cpu(), base.v_pool.cpu(), base.block_lists,
+                                  base.seq_lens, base.cur_lens)
+    assert max_err(out, want) <= 1e-4
+
+
+def test_order_does_not_change_results(device):
+    lens = [300, 20, 1000, 64, 513]
+    b = make_batch(device, 9, lens, [1] * 5, H=4, Hd=128, kv_dtype=torch.bfloat16)
+    order = torch.tensor(sorted(range(5), key=lambda i: -lens[i]), dtype=torch.int32, device=device)
+    a1 = run(b)
+    a2 = run(b, order=order)
+    assert torch.equal(a1, a2)
+
+
+def test_negative_page_entries_are_skipped(device):
+    b = make_batch(device, 10, [64, 64], [1, 1], H=2, Hd=64)
+    pt = b.page_table.clone()
+    pt[0, 1] = -1  # keys 16..31 of request 0 are skipped, like the reference kernels skip -1 pages
+    got = paged_attention_decode_hip(b.q, b.k_pool, b.v_pool, pt, b.seq_lens_t, b.cur_lens_t)
+    # equivalent request: drop block 1 and shorten by 16 keys
+    k = b.k_pool.cpu()
+    want0 = oracle.paged_attention(b.q[:1].cpu(), k, b.v_pool.cpu(), [[b.block_lists[0][0]] + b.block_lists[0][2:]],
+                                   [48], [1])
+    assert max_err(got[:1], want0) <= 1e-4
+    assert max_err(got[1:], oracle_out(b)[1:]) <= 1e-4
+
+
+def test_large_ragged_decode_sampled_parity(device):
+    """Full large ragged decode (B=256, 32x128, bf16 KV); a seeded sample of requests, plus the
+    longest and shortest, is checked against the oracle on the same bf16 values."""
+    b = workloads.large_decode(seed=0, device=device)
+    print(f"large decode: B={b.batch} total tokens={sum(b.seq_lens)} pool={b.k_pool.shape[0]}", flush=True)
+    got = run(b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    rng = random.Random(0)
+    lens = b.seq_lens
+    picks = sorted(set(rng.sample(range(b.batch), 10) + [lens.index(max(lens)), lens.index(min(lens))]))
+    for r in picks:
+        ids = torch.tensor(b.block_lists[r], device=device, dtype=torch.long)
+        k = b.k_pool.index_select(0, ids).cpu()
+        v = b.v_pool.index_select(0, ids).cpu()
+        want = oracle.paged_attention(b.q[r:r + 1].cpu(), k, v, [list(range(len(ids)))], [lens[r]], [1],
+                                      nthreads=NTHREADS)
+        err = max_err(got[r:r + 1], want)
+        print(f"  request {r} L={lens[r]} max err {err:.2e}", flush=True)
+        assert err <= 1e-4
+    del b
+    torch.cuda.empty_cache()
