@@ -119,7 +119,7 @@ def test_strided_views_like_the_model(device):
     base = make_batch(device, 8, [70, 16, 300, 5], [1] * 4, H=H, Hd=Hd)
     x = torch.randn(B, 1, H * Hd, device=device)
     q = x.view(B, 1, H, Hd).transpose(1, 2)  # the model's [B, H, T, Hd] view
-    assert not q.is_contiguous()
+    assert q.stride() == (H * Hd, Hd, H * Hd, 1)
     out = paged_attention_decode_hip(q, base.k_pool, base.v_pool, base.page_table, base.seq_lens_t, base.cur_lens_t)
     assert out.stride() == q.stride()
     want = oracle.paged_attention(q.cpu().contiguous(), base.k_pool.cpu(), base.v_pool.cpu(), base.block_lists,
