@@ -39,20 +39,23 @@ template <> struct Elem<uint16_t> {
   __device__ static __forceinline__ void store(uint16_t* p, float v) { *p = f32_to_bf16(v); }
 };
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 // Unpack one 16-byte vector into EPL floats.
 template <typename T> struct Vec16;
 template <> struct Vec16<float> {
   static constexpr int EPL = 4;
-  __device__ static __forceinline__ void unpack(const uint4& v, float* f) {
-    f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
-    f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+  __device__ static __forceinline__ void unpack(const u32x4& v, float* f) {
+    f[0] = __uint_as_float(v[0]); f[1] = __uint_as_float(v[1]);
+    f[2] = __uint_as_float(v[2]); f[3] = __uint_as_float(v[3]);
   }
 };
 template <> struct Vec16<uint16_t> {
   static constexpr int EPL = 8;
-  __device__ static __forceinline__ void unpack(const uint4& v, float* f) {
-    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-    f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+  __device__ static __forceinline__ void unpack(const u32x4& v, float* f) {
+    f[0] = bf16_lo(v[0]); f[1] = bf16_hi(v[0]); f[2] = bf16_lo(v[1]); f[3] = bf16_hi(v[1]);
+    f[4] = bf16_lo(v[2]); f[5] = bf16_hi(v[2]); f[6] = bf16_lo(v[3]); f[7] = bf16_hi(v[3]);
   }
 };
 
