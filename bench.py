@@ -12,12 +12,16 @@ Also reported on the same line:
   roofline       the decode kernel against MI355X's 8 TB/s HBM peak (and HBM traffic per launch
                  when a counter summary is available under profiles/);
   cpu_baseline   the oracle (C restatement of the reference's paged attention, fp64
-                 accumulation) on a bounded sample of the same batch, on this host's cores;
+                 accumulation) over the same batch on this host's cores, plus the rate of the
+                 reference's own per-token torch loop on a small slice of it;
+  secondary      the ragged fp32 decode (8 requests x 6 layers) and the chunked prefill (4 requests,
+                 fp32 and bf16 KV; MFMA utilisation against the fp32 / bf16 matrix peaks);
   continuous_batching  the end-to-end run: decoder LM (vocab 5000, d_model 512, 8 heads,
                  6 layers, d_ff 2048, KV block 16, fp32, weights N(0, 0.02)), 200 Poisson requests
                  at 32 req/s, max batch 8, prefill chunk 256, 1536-token iteration budget, greedy;
                  tokens/s and p50 TTFT on the scheduler's virtual clock, plus wall time.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-e2e]
+                       [--no-secondary] [--calibrate-copy]
 """
 from __future__ import annotations
 
@@ -26,7 +30,6 @@ import json
 import math
 import os
 import re
-import statistics
 import sys
 import time
 from pathlib import Path
@@ -88,51 +91,146 @@ def time_decode(batch, steps: int, warmup: int):
     return start.elapsed_time(end) / steps, wall_ms / steps, out
 
 
-def cpu_baseline(batch, target_s: float = 6.0) -> dict:
-    """Oracle on the first n requests of the batch (n sized for ~target_s per run), median of 3."""
+def cpu_baseline(batch, chunk: int = 32) -> dict:
+    """The oracle over the whole batch on this host's cores: requests are copied to host memory
+    `chunk` at a time and only the oracle's compute is timed (one run per chunk)."""
     import torch
 
     import oracle
 
     nthreads = cpu_threads()
     lens = batch.seq_lens
-
-    def sample(n):
-        ks, vs, lists, pos = [], [], [], 0
-        for r in range(n):
-            ids = torch.tensor(batch.block_lists[r], device=batch.q.device, dtype=torch.long)
-            ks.append(batch.k_pool.index_select(0, ids).cpu())
-            vs.append(batch.v_pool.index_select(0, ids).cpu())
-            lists.append(list(range(pos, pos + len(ids))))
-            pos += len(ids)
-        return (batch.q[:n].cpu(), oracle._np(torch.cat(ks)), oracle._np(torch.cat(vs)), lists, lens[:n], [1] * n)
-
-    def run(args):
+    total_s = 0.0
+    for c0 in range(0, batch.batch, chunk):
+        rows = range(c0, min(c0 + chunk, batch.batch))
+        ids = torch.tensor([i for r in rows for i in batch.block_lists[r]], device=batch.q.device, dtype=torch.long)
+        k = oracle._np(batch.k_pool.index_select(0, ids).cpu())
+        v = oracle._np(batch.v_pool.index_select(0, ids).cpu())
+        lists, pos = [], 0
+        for r in rows:
+            lists.append(list(range(pos, pos + len(batch.block_lists[r]))))
+            pos += len(batch.block_lists[r])
+        q = batch.q[c0:c0 + len(rows)].cpu()
         t0 = time.perf_counter()
-        oracle.paged_attention(*args, nthreads=nthreads)
-        return time.perf_counter() - t0
-
-    probe = sample(2)
-    rate = sum(lens[:2]) / max(run(probe), 1e-6)  # tokens (x all heads) per second
-    n, tokens = 0, 0
-    while n < batch.batch and tokens < rate * target_s and n < 64:
-        tokens += lens[n]
-        n += 1
-    args = sample(n)
-    times = sorted(run(args) for _ in range(3))
-    t = statistics.median(times)
+        oracle.paged_attention(q, k, v, lists, lens[c0:c0 + len(rows)], [1] * len(rows), nthreads=nthreads)
+        total_s += time.perf_counter() - t0
+        del k, v
     H, Hd = batch.q.shape[1], batch.q.shape[3]
-    nbytes = sum(H * (2 * L * Hd * batch.k_pool.element_size() + 2 * Hd * 4) + 4 * math.ceil(L / 16) + 8 for L in lens[:n])
     return {
-        "value": nbytes / t / 1e9,
+        "value": batch.decode_bytes() / total_s / 1e9,
         "unit": "GB/s",
         "cores": nthreads,
         "kind": "port",
-        "sample": f"requests 0..{n - 1} of the same batch ({sum(lens[:n])} tokens x {H} heads x {Hd}, bf16 KV); "
-                  f"oracle C restatement, fp64 accumulation, OpenMP over (request, head); median of 3 runs "
-                  f"({t:.2f} s each)",
-        "seconds_per_run": t,
+        "sample": f"the whole batch ({batch.batch} requests, {sum(lens)} tokens x {H} heads x {Hd}, bf16 KV), "
+                  f"copied to host {chunk} requests at a time; oracle C restatement of the reference's paged "
+                  f"attention, fp64 accumulation, OpenMP over (request, head); compute time {total_s:.2f} s",
+        "seconds": total_s,
     }
+
+
+def reference_loop_rate(batch, tokens: int = 256) -> dict:
+    """The reference's own CPU path (its per-token torch loop, restated in oracle/reference_loop.py)
+    on one request cut to `tokens` keys, all heads: seconds per (key x head), and the time the whole
+    batch would take at that rate."""
+    import torch
+
+    from oracle.reference_loop import paged_attention_loop
+
+    torch.set_num_threads(cpu_threads())
+    nblk = (tokens + 15) // 16
+    ids = torch.tensor(batch.block_lists[0][:nblk], device=batch.q.device, dtype=torch.long)
+    k = batch.k_pool.index_select(0, ids).float().cpu()
+    v = batch.v_pool.index_select(0, ids).float().cpu()
+    q = batch.q[:1].cpu()
+    t0 = time.perf_counter()
+    paged_attention_loop(q, k, v, [list(range(nblk))], [tokens], [1])
+    dt = time.perf_counter() - t0
+    per = dt / (tokens * q.shape[1])
+    whole = per * sum(batch.seq_lens) * q.shape[1]
+    return {"seconds_per_key_head": per, "sample": f"request 0 cut to {tokens} keys x {q.shape[1]} heads ({dt:.2f} s)",
+            "extrapolated_batch_seconds": whole,
+            "extrapolated_GBps": batch.decode_bytes() / whole / 1e9, "threads": torch.get_num_threads()}
+
+
+def time_call(fn, steps: int, warmup: int = 2) -> float:
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def secondary_workloads(device, steps: int) -> dict:
+    """Ragged fp32 decode (8 requests x 6 layers) and chunked prefill (fp32 and bf16 KV)."""
+    import torch
+
+    from src import workloads
+    from src.kernels.hip_paged_attention import (
+        kv_append_hip, pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
+
+    res = {}
+    per_layer = []
+    for layer in range(6):
+        b = workloads.ragged_decode(seed=0, layer=layer, device=device)
+        ms = time_call(lambda: paged_attention_decode_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t,
+                                                          b.cur_lens_t), steps)
+        per_layer.append((ms, b.decode_bytes()))
+    ms_tot = sum(m for m, _ in per_layer)
+    by_tot = sum(x for _, x in per_layer)
+    res["ragged_decode_fp32_6_layers"] = {
+        "workload": "8 requests, 8 heads x 64, lengths U[128,1024], 4096-block pool, fp32, one call per layer",
+        "us_per_layer": round(1e3 * ms_tot / 6, 2), "GBps": round(by_tot / (ms_tot * 1e-3) / 1e9, 1),
+        "bytes_per_layer": by_tot // 6,
+    }
+    for kv_dtype, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16kv")):
+        w = workloads.chunked_prefill(seed=0, device=device, kv_dtype=kv_dtype)
+        B = len(w["prev_lens"])
+        T = w["q"].shape[2]
+        lists = w["block_lists"]
+        max_pages = max(len(x) for x in lists)
+        flat = [i for x in lists for i in x]
+        offs = [0]
+        for x in lists:
+            offs.append(offs[-1] + len(x))
+        i32 = lambda a: torch.tensor(a, dtype=torch.int32, device=device)
+        pt, s32, _, slots = pack_metadata_hip(i32(flat), i32(offs), i32(w["prev_lens"]), i32(w["chunk_lens"]),
+                                              query_len=T, block_size=16, max_pages=max_pages)
+        cur = i32(w["chunk_lens"])
+        append_ms = time_call(lambda: kv_append_hip(w["k_new"], w["v_new"], w["k_pool"], w["v_pool"], slots), steps)
+        attn_ms = time_call(lambda: paged_attention_prefill_hip(w["q"], w["k_pool"], w["v_pool"], pt, s32, cur), steps)
+        flops = workloads.prefill_flops(w["prev_lens"], w["chunk_lens"], 8, 64)
+        peak = 157.3 if tag == "fp32" else 2500.0
+        tfs = flops / (attn_ms * 1e-3) / 1e12
+        res[f"chunked_prefill_{tag}"] = {
+            "workload": f"4 requests, 8 heads x 64, context {w['prev_lens']} + chunk {w['chunk_lens']}, "
+                        f"{'fp32' if tag == 'fp32' else 'bf16'} KV",
+            "attention_us": round(1e3 * attn_ms, 2), "append_us": round(1e3 * append_ms, 2),
+            "useful_gflop": round(flops / 1e9, 4), "TFLOPs": round(tfs, 2),
+            "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
+        }
+    return res
+
+
+def calibration_copy(device, nbytes: int = 1 << 32) -> None:
+    """A plain device copy of known size (reads and writes nbytes), for scaling HBM counters."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calibration copy: 3 x {nbytes} bytes read and written")
 
 
 def init_weights_normal(model, std: float = 0.02) -> None:
@@ -203,6 +301,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true", help="also run a copy kernel of known size")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -257,10 +357,16 @@ def main() -> int:
         },
     }
     if not args.no_cpu_baseline:
-        log("CPU baseline (oracle on a sample of the batch)")
+        log("CPU baseline (oracle over the batch)")
         result["cpu_baseline"] = cpu_baseline(batch)
+        result["cpu_reference_loop"] = reference_loop_rate(batch)
     del batch
     torch.cuda.empty_cache()
+    if args.calibrate_copy:
+        calibration_copy(dev)
+    if not args.no_secondary:
+        log("secondary workloads (ragged fp32 decode, chunked prefill)")
+        result["secondary"] = secondary_workloads(dev, args.steps)
     if not args.no_e2e:
         log("end-to-end continuous batching (200 requests, 32 req/s)")
         result["continuous_batching"] = continuous_batching(dev)
