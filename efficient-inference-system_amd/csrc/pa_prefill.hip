@@ -81,8 +81,10 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
   {
     const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
                    (int64_t)(i < a.T ? i : 0) * a.q_st + G * QD;
+    // The row index is clamped in bounds, so load unconditionally and zero rows past T after.
+    const float qscale = i < a.T ? a.scale_log2 : 0.f;
 #pragma unroll
-    for (int s = 0; s < QD; ++s) qv[s] = i < a.T ? Elem<IO>::load(qp + s) * a.scale_log2 : 0.f;
+    for (int s = 0; s < QD; ++s) qv[s] = Elem<IO>::load(qp + s) * qscale;
   }
   bf16x8 qb[kBf16 ? QD / 8 : 1];
   if constexpr (kBf16) {
@@ -106,36 +108,43 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
   const KV* vpool = static_cast<const KV*>(a.v_pool);
   const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
 
-  for (int j = w; j < nb; j += NW) {
-    const int blk = pt[j];
-    const bool ok = blk >= 0 && blk < a.num_blocks;
-    const int64_t tile = ((int64_t)(ok ? blk : 0) * a.H + h) * (BS * HD);
-
-    // ---- S^T = K Q^T --------------------------------------------------------------------
+  // Registers of one KV tile as this lane needs them: K row c, head_dim [G*QD, G*QD + QD), and
+  // V rows 4G..4G+3, head_dim [c*DT, c*DT + DT).
+  constexpr int KW = kBf16 ? QD / 2 : QD;
+  constexpr int VW = kBf16 ? DT / 2 : DT;
+  struct Tile {
+    uint32_t k[KW];
+    uint32_t v[4][VW];
+    bool ok;
+  };
+  auto issue = [&](Tile& t, int blk) {
+    t.ok = blk >= 0 && blk < a.num_blocks;
+    const int64_t base = ((int64_t)(t.ok ? blk : 0) * a.H + h) * (BS * HD);
+    load_words<KW>(kpool + base + c * HD + G * QD, t.k);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) load_words<VW>(vpool + base + (4 * G + r) * HD + c * DT, t.v[r]);
+  };
+  auto fold = [&](const Tile& tl, int j) {
+    // ---- S^T = K Q^T ------------------------------------------------------------------------
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
     if constexpr (!kBf16) {
-      uint32_t kw[QD];
-      load_words<QD>(kpool + tile + c * HD + G * QD, kw);
 #pragma unroll
       for (int s = 0; s < QD; ++s)
-        sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kw[s]), qv[s], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(tl.k[s]), qv[s], sacc, 0, 0, 0);
     } else {
-      uint32_t kw[QD / 2];
-      load_words<QD / 2>(kpool + tile + c * HD + G * QD, kw);
 #pragma unroll
       for (int s = 0; s < QD / 8; ++s) {
-        const u32x4 x = {kw[4 * s], kw[4 * s + 1], kw[4 * s + 2], kw[4 * s + 3]};
+        const u32x4 x = {tl.k[4 * s], tl.k[4 * s + 1], tl.k[4 * s + 2], tl.k[4 * s + 3]};
         sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x), qb[s], sacc, 0, 0, 0);
       }
     }
-
-    // ---- online softmax over this block's keys, per query column c ------------------------
+    // ---- online softmax over this block's keys, per query column c ----------------------------
     float p[4];
     float mloc = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = j * BS + 4 * G + r;
-      p[r] = (ok && t < n_c) ? sacc[r] : -INFINITY;
+      p[r] = (tl.ok && t < n_c) ? sacc[r] : -INFINITY;
       mloc = fmaxf(mloc, p[r]);
     }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
@@ -154,30 +163,48 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
     m = mnew;
 #pragma unroll
     for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
-
-    // ---- O^T += V^T P^T -------------------------------------------------------------------
+    // ---- O^T += V^T P^T -----------------------------------------------------------------------
     if constexpr (!kBf16) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint32_t vw[DT];
-        load_words<DT>(vpool + tile + (4 * G + r) * HD + c * DT, vw);
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int t = 0; t < DT; ++t)
-          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vw[t]), p[r], oacc[t], 0, 0, 0);
-      }
+          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(tl.v[r][t]), p[r], oacc[t], 0, 0, 0);
     } else {
-      uint32_t vw[4][DT / 2];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) load_words<DT / 2>(vpool + tile + (4 * G + r) * HD + c * DT, vw[r]);
       const s16x4 pb = {(short)f32_to_bf16(p[0]), (short)f32_to_bf16(p[1]), (short)f32_to_bf16(p[2]),
                         (short)f32_to_bf16(p[3])};
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         const int sh = (t & 1) * 16;
-        const s16x4 av = {(short)(vw[0][t >> 1] >> sh), (short)(vw[1][t >> 1] >> sh),
-                          (short)(vw[2][t >> 1] >> sh), (short)(vw[3][t >> 1] >> sh)};
+        const s16x4 av = {(short)(tl.v[0][t >> 1] >> sh), (short)(tl.v[1][t >> 1] >> sh),
+                          (short)(tl.v[2][t >> 1] >> sh), (short)(tl.v[3][t >> 1] >> sh)};
         oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb, oacc[t], 0, 0, 0);
       }
+    }
+  };
+
+  // This wave's blocks j = w + k*NW, k < mine, in chunks of one page-table entry per lane; the
+  // next block's tile is loaded into the second register set while the current one is folded.
+  const int mine = nb > w ? (nb - w + NW - 1) / NW : 0;
+  for (int c0 = 0; c0 < mine; c0 += kWave) {
+    const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
+    int ids = -1;
+    if (lane < cnt) ids = pt[w + (c0 + lane) * NW];
+    Tile t0, t1;
+    issue(t0, __builtin_amdgcn_readlane(ids, 0));
+    int i = 0;
+    for (; i + 2 < cnt; i += 2) {
+      issue(t1, __builtin_amdgcn_readlane(ids, i + 1));
+      fold(t0, w + (c0 + i) * NW);
+      issue(t0, __builtin_amdgcn_readlane(ids, i + 2));
+      fold(t1, w + (c0 + i + 1) * NW);
+    }
+    if (i + 1 < cnt) {
+      issue(t1, __builtin_amdgcn_readlane(ids, i + 1));
+      fold(t0, w + (c0 + i) * NW);
+      fold(t1, w + (c0 + i + 1) * NW);
+    } else {
+      fold(t0, w + (c0 + i) * NW);
     }
   }
 
