@@ -247,7 +247,8 @@ def init_weights_normal(model, std: float = 0.02) -> None:
                 mod.bias.zero_()
 
 
-def continuous_batching(device) -> dict:
+def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True) -> dict:
+    """The end-to-end benchmark trace through the continuous scheduler on `device`."""
     import torch
 
     from src.config import benchmark_serving_request_mix
@@ -260,16 +261,17 @@ def continuous_batching(device) -> dict:
 
     torch.manual_seed(42)
     model = TinyTransformerLM(vocab_size=5000, d_model=512, num_heads=8, num_layers=6, d_ff=2048, max_seq_len=1024,
-                              attention_backend="hip_paged", kv_block_size=16, kv_pool_initial_blocks=64,
+                              attention_backend=backend, kv_block_size=16, kv_pool_initial_blocks=64,
                               kv_pool_growth_factor=2.0).to(device).eval()
     init_weights_normal(model)
-    # warm-up as the reference harness does: one batched generate, then fresh pools
-    generate_with_cache(model, torch.randint(0, 5000, (8, 512), device=device), max_new_tokens=[2] * 8)
-    torch.cuda.synchronize()
-    model.reset_paged_cache_pools()
+    if warmup:  # as the reference harness: one batched generate, then fresh pools
+        generate_with_cache(model, torch.randint(0, 5000, (8, 512), device=device), max_new_tokens=[2] * 8)
+        if device.type == "cuda":
+            torch.cuda.synchronize()
+        model.reset_paged_cache_pools()
     reqs = generate_requests(200, 32.0, 5000, workload_profiles=benchmark_serving_request_mix(), seed=42)
     sched = ContinuousBatchingScheduler(max_batch_size=8, prefill_chunk_size=256, max_tokens_per_iteration=1536)
-    dev = str(device)
+    dev = str(device) if device.type == "cuda" else "cpu"
     t0 = time.perf_counter()
     with torch.no_grad():
         done, events = sched.run(
@@ -288,10 +290,26 @@ def continuous_batching(device) -> dict:
         "requests": s["num_requests"],
         "generated_tokens": sum(r.max_new_tokens for r in done),
         "decode_ms_per_token": s["mean_decode_ms_per_token"],
+        "prefill_runtime_ms_total": s["prefill_runtime_ms_total"],
+        "decode_runtime_ms_total": s["decode_runtime_ms_total"],
         "events": s["num_batches"],
         "wall_s": wall,
-        "clock": "scheduler virtual clock (sum of measured forward times), as the reference",
     }
+
+
+def continuous_batching_pair(device) -> dict:
+    """GPU run (hip_paged) and the same-run CPU baseline (torch paged_reference on the host cores)."""
+    import torch
+
+    gpu = continuous_batching(device, "hip_paged")
+    torch.set_num_threads(cpu_threads())
+    log(f"continuous batching on the CPU ({torch.get_num_threads()} threads)")
+    cpu = continuous_batching(torch.device("cpu"), "paged_reference", warmup=False)
+    cpu["threads"] = torch.get_num_threads()
+    cpu["kind"] = "port: this package's paged_reference backend (vectorised torch) on the CPU, same trace and weights"
+    gpu["clock"] = "scheduler virtual clock (sum of measured forward times), as the reference"
+    gpu["cpu_baseline"] = cpu
+    return gpu
 
 
 def main() -> int:
@@ -369,7 +387,7 @@ def main() -> int:
         result["secondary"] = secondary_workloads(dev, args.steps)
     if not args.no_e2e:
         log("end-to-end continuous batching (200 requests, 32 req/s)")
-        result["continuous_batching"] = continuous_batching(dev)
+        result["continuous_batching"] = continuous_batching_pair(dev)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -113,7 +113,9 @@ class LayerBlockPool:
         if self.k_blocks.is_cuda:
             from src.kernels.hip_paged_attention import zero_blocks_hip
 
-            ids = torch.tensor(block_ids, dtype=torch.int32).pin_memory().to(self.k_blocks.device, non_blocking=True)
+            from src.kernels.staging import upload
+
+            ids = upload(np.asarray(block_ids, dtype=np.int32), self.k_blocks.device)
             zero_blocks_hip(self.k_blocks, self.v_blocks, ids)
         else:
             idx = torch.tensor(block_ids, dtype=torch.long)
@@ -223,23 +225,15 @@ class BatchedPagedKVCache:
         from src.kernels.hip_paged_attention import pack_metadata_hip
 
         B = len(self.states)
-        counts = [len(s.block_ids) for s in self.states]
-        max_pages = max(counts, default=0)
-        total = sum(counts)
-        buf = np.empty(3 * B + 1 + total, dtype=np.int32)
-        buf[0] = 0
-        np.cumsum(counts, out=buf[1:B + 1])
-        buf[B + 1:2 * B + 1] = prev
-        buf[2 * B + 1:3 * B + 1] = app
-        if total:
-            buf[3 * B + 1:] = np.fromiter((i for s in self.states for i in s.block_ids), dtype=np.int32, count=total)
+        buf, max_pages = self.csr_buffer(prev, app)
         dev_index = _device_index(device)
         key = (dev_index, buf.tobytes(), query_len, self.pool.block_size, max_pages, with_slots)
         hit = _last_pack.get(dev_index)
         if hit is not None and hit[0] == key:
             return hit[1]
-        host = torch.from_numpy(buf).pin_memory()
-        dev = host.to(device, non_blocking=True)
+        from src.kernels.staging import upload
+
+        dev = upload(buf, device)
         result = pack_metadata_hip(
             dev[3 * B + 1:], dev[0:B + 1], dev[B + 1:2 * B + 1], dev[2 * B + 1:3 * B + 1],
             query_len=query_len, block_size=self.pool.block_size, max_pages=max_pages, with_slots=with_slots,
@@ -284,15 +278,15 @@ class BatchedPagedKVCache:
             return torch.tensor(updated, dtype=torch.long, device=k_new.device)
         return self._append_batch_device(k_new, v_new, lengths)
 
-    def _append_batch_device(self, k_new: torch.Tensor, v_new: torch.Tensor, lengths: list[int]) -> torch.Tensor:
-        from src.kernels.hip_paged_attention import kv_append_hip
-
-        B, H, T, Hd = k_new.shape
+    def host_append(self, app: list[int], query_len: int, num_heads: int, head_dim: int, dtype: torch.dtype,
+                    device: torch.device) -> list[int]:
+        """Host half of a device append of app[b] (already clamped to [0, T]) new tokens per
+        request: initialises the pool if needed, allocates blocks in the reference's order and
+        advances seq_len. Returns the lengths before the append."""
         pool = self.pool
         bs = pool.block_size
-        app = [max(min(n, T), 0) for n in lengths]
         if any(app):
-            pool.ensure_initialized(H, Hd, k_new.dtype, k_new.device)
+            pool.ensure_initialized(num_heads, head_dim, dtype, device)
         prev = []
         for state, n in zip(self.states, app):
             p = state.seq_len
@@ -308,6 +302,29 @@ class BatchedPagedKVCache:
             for _ in range((p + n + bs - 1) // bs - len(state.block_ids)):
                 state.block_ids.append(pool.allocate_block())
             state.seq_len = p + n
+        return prev
+
+    def csr_buffer(self, prev: list[int], app: list[int]) -> tuple[np.ndarray, int]:
+        """int32 [row_offsets B+1 | prev B | app B | block ids] of the batch, and max_pages."""
+        B = len(self.states)
+        counts = [len(s.block_ids) for s in self.states]
+        total = sum(counts)
+        buf = np.empty(3 * B + 1 + total, dtype=np.int32)
+        buf[0] = 0
+        np.cumsum(counts, out=buf[1:B + 1])
+        buf[B + 1:2 * B + 1] = prev
+        buf[2 * B + 1:3 * B + 1] = app
+        if total:
+            buf[3 * B + 1:] = np.fromiter((i for s in self.states for i in s.block_ids), dtype=np.int32, count=total)
+        return buf, max(counts, default=0)
+
+    def _append_batch_device(self, k_new: torch.Tensor, v_new: torch.Tensor, lengths: list[int]) -> torch.Tensor:
+        from src.kernels.hip_paged_attention import kv_append_hip
+
+        B, H, T, Hd = k_new.shape
+        pool = self.pool
+        app = [max(min(n, T), 0) for n in lengths]
+        prev = self.host_append(app, T, H, Hd, k_new.dtype, k_new.device)
         page_table, seq32, seq64, slots = self._pack(k_new.device, T, prev, app, True)
         if any(app):
             kv_append_hip(k_new, v_new, pool.k_blocks, pool.v_blocks, slots)

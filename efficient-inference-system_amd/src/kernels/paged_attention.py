@@ -17,8 +17,10 @@ import torch
 from src.cache.paged_kv import BatchedPagedKVCache
 from src.config import ATTENTION_BACKENDS
 from src.kernels.reference_paged_attention import paged_attention_reference
+from src.kernels.staging import upload
 
 _const_lengths: dict[tuple, torch.Tensor] = {}
+_last_host_lengths: dict[str, tuple] = {}
 
 
 def _lengths_tensor(current_lengths, batch_size: int, query_len: int, device: torch.device) -> torch.Tensor:
@@ -31,8 +33,15 @@ def _lengths_tensor(current_lengths, batch_size: int, query_len: int, device: to
             _const_lengths[key] = t
         return t
     if not current_lengths.is_cuda:
-        # Host lengths (the model passes them this way): an asynchronous pinned copy.
-        return current_lengths.to(torch.int32).contiguous().pin_memory().to(device, non_blocking=True)
+        # Host lengths (the model passes them this way, the same tensor to every layer): one
+        # asynchronous upload per tensor version, reused by the following layers.
+        key = (id(current_lengths), current_lengths._version, device.index)
+        hit = _last_host_lengths.get("last")
+        if hit is not None and hit[0] == key and hit[1] is current_lengths:
+            return hit[2]
+        dev = upload(current_lengths.to(torch.int32).contiguous().numpy(), device)
+        _last_host_lengths["last"] = (key, current_lengths, dev)
+        return dev
     return current_lengths.to(device=device, dtype=torch.int32).contiguous()
 
 

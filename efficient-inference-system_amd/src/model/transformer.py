@@ -2,7 +2,9 @@
 
 TinyTransformerLM: token + learned position embeddings, pre-LayerNorm blocks (attention, GELU
 MLP), final LayerNorm, bias-free lm_head; one LayerBlockPool per layer, created lazily. Module
-and parameter names match the reference so state dicts load across the two.
+and parameter names match the reference so state dicts load across the two. On the "hip_paged"
+backend, one-token cached steps over per-layer batched caches replay a captured HIP graph
+(src/model/graph_decode.py); everything else runs eagerly.
 """
 import torch
 import torch.nn as nn
@@ -86,6 +88,16 @@ class TinyTransformerLM(nn.Module):
 
     def reset_paged_cache_pools(self) -> None:
         self.layer_block_pools = None
+        if getattr(self, "_graph_decode", None) is not None:
+            self._graph_decode.captured.clear()
+
+    def _graph_decode_runner(self):
+        """Lazily created HIP-graph runner for one-token decode steps (see graph_decode.py)."""
+        if getattr(self, "_graph_decode", None) is None:
+            from src.model.graph_decode import GraphedDecodeStep
+
+            self._graph_decode = GraphedDecodeStep(self)
+        return self._graph_decode
 
     def create_request_kv_caches(self, batch_size: int) -> list[list[PagedKVCacheState]]:
         pools = self._ensure_layer_block_pools()
@@ -135,6 +147,13 @@ class TinyTransformerLM(nn.Module):
     ):
         B, T = input_ids.shape
         device = input_ids.device
+        if (use_cache and T == 1 and kv_caches is not None and input_ids.is_cuda
+                and (current_lengths is None or (isinstance(current_lengths, int) and current_lengths == 1))):
+            runner = self._graph_decode_runner()
+            if runner.usable(input_ids, kv_caches):
+                if isinstance(position_offset, int):
+                    position_offset = torch.full((B,), position_offset, dtype=torch.long, device=device)
+                return runner(input_ids, position_offset.view(B), kv_caches), list(kv_caches)
         if isinstance(position_offset, int):
             positions = torch.arange(position_offset, position_offset + T, device=device).unsqueeze(0).expand(B, T)
         else:

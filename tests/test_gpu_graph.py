@@ -1,0 +1,66 @@
+"""The HIP-graph decode step against the eager forward: same logits (within 1e-5; the graph packs
+the page table at a fixed width, which can change the decode split) and bit-identical KV pools
+and block lists, across batch-size changes, pool growth (graph re-capture) and eager work and
+synchronisations between replays."""
+import pytest
+import torch
+
+from src.cache.paged_kv import BatchedPagedKVCache
+from src.model.transformer import TinyTransformerLM
+
+pytestmark = pytest.mark.gpu
+
+
+def make(device, seed=0):
+    torch.manual_seed(seed)
+    m = TinyTransformerLM(vocab_size=300, d_model=128, num_heads=2, num_layers=3, d_ff=256, max_seq_len=256,
+                          attention_backend="hip_paged", kv_block_size=16, kv_pool_initial_blocks=4,
+                          kv_pool_growth_factor=2.0).to(device).eval()
+    return m
+
+
+def stack(caches_per_request, rows):
+    layers = len(caches_per_request[0])
+    return [BatchedPagedKVCache([caches_per_request[r][l] for r in rows], caches_per_request[rows[0]][l].pool)
+            for l in range(layers)]
+
+
+def test_graph_decode_matches_eager(device, monkeypatch):
+    eager, graphed = make(device), make(device)
+    graphed.load_state_dict(eager.state_dict())
+    B = 3
+    prompt = torch.randint(0, 300, (B, 40), device=device)
+    lens = torch.tensor([40, 23, 31], device=device)
+    per = {}
+    with torch.no_grad():
+        for name, m in (("eager", eager), ("graph", graphed)):
+            _, caches = m(prompt, use_cache=True, position_offset=0, current_lengths=lens)
+            per[name] = [[c.states[r] for c in caches] for r in range(B)]
+    rows = [0, 1, 2]
+    pos = lens.clone()
+    tok = torch.randint(0, 300, (B, 1), device=device)
+    for step in range(60):
+        if step == 25:
+            rows = [0, 2]  # request 1 leaves the batch: a different batch size / graph
+        r = torch.tensor(rows, device=device)
+        outs = {}
+        with torch.no_grad():
+            for name, m in (("eager", eager), ("graph", graphed)):
+                monkeypatch.setenv("PAGED_HIP_GRAPHS", "0" if name == "eager" else "1")
+                logits, _ = m(tok[r], kv_caches=stack(per[name], rows), use_cache=True, position_offset=pos[r])
+                outs[name] = logits
+        torch.cuda.synchronize()
+        err = (outs["eager"] - outs["graph"]).abs().max().item()
+        assert err <= 1e-5, (step, err)
+        pos[r] += 1
+        tok = torch.randint(0, 300, (B, 1), device=device)  # eager work between replays
+        torch.cuda.synchronize()
+    runner = graphed._graph_decode
+    assert runner is not None and runner.captured, "the graph path was not used"
+    for le, lg in zip(eager.layer_block_pools, graphed.layer_block_pools):
+        assert le.capacity_blocks == lg.capacity_blocks > 4  # grew during decode
+        assert le.free_block_ids == lg.free_block_ids
+        assert torch.equal(le.k_blocks, lg.k_blocks) and torch.equal(le.v_blocks, lg.v_blocks)
+    for re_, rg in zip(per["eager"], per["graph"]):
+        for se, sg in zip(re_, rg):
+            assert se.block_ids == sg.block_ids and se.seq_len == sg.seq_len
