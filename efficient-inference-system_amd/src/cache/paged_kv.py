@@ -19,8 +19,10 @@ of a model sees the same allocation sequence, consecutive layers usually pack id
 the last packed result per device is reused when the host-side CSR buffer is byte-identical.
 
 Additions beyond the reference: LayerBlockPool(dtype=...) to store KV in another dtype than the
-model (bf16 under an fp32 model), LayerBlockPool.release_blocks (one zeroing launch for many
-blocks), LayerBlockPool.mutations (allocation/release counter) and
+model (bf16 under an fp32 model), LayerBlockPool(storage=KVStorage) to keep the pool's tensors as
+views of fixed physical storage (the logical capacity, growth steps, free list and zeroing are
+unchanged; only the device addresses stay put), LayerBlockPool.release_blocks (one zeroing launch
+for many blocks), LayerBlockPool.mutations (allocation/release counter) and
 BatchedPagedKVCache.device_metadata().
 """
 from __future__ import annotations
@@ -32,6 +34,40 @@ import numpy as np
 import torch
 
 
+class KVStorage:
+    """Physical K/V storage a pool's tensors are prefix views of, so their device addresses stay
+    fixed while the pool grows and across pools that reuse it (a model keeps one per layer).
+    Holds `blocks` physical blocks; replaced by a larger allocation only when a pool outgrows it."""
+
+    def __init__(self, reserve_blocks: int):
+        self.reserve_blocks = reserve_blocks
+        self.k: torch.Tensor | None = None
+        self.v: torch.Tensor | None = None
+
+    @property
+    def blocks(self) -> int:
+        return 0 if self.k is None else self.k.shape[0]
+
+    def fits(self, shape_tail: tuple, dtype: torch.dtype, device: torch.device, blocks: int) -> bool:
+        return (self.k is not None and tuple(self.k.shape[1:]) == shape_tail and self.k.dtype == dtype
+                and self.k.device == device and self.k.shape[0] >= blocks)
+
+    def ensure(self, shape_tail: tuple, dtype: torch.dtype, device: torch.device, blocks: int,
+               keep: int = 0) -> None:
+        """Make room for `blocks` blocks, keeping the first `keep` blocks' contents."""
+        if self.fits(shape_tail, dtype, device, blocks):
+            return
+        compatible = (self.k is not None and tuple(self.k.shape[1:]) == shape_tail and self.k.dtype == dtype
+                      and self.k.device == device)
+        n = max(blocks, self.reserve_blocks, 2 * self.blocks if compatible else 0)
+        new_k = torch.zeros((n, *shape_tail), dtype=dtype, device=device)
+        new_v = torch.zeros_like(new_k)
+        if compatible and keep:
+            new_k[:keep].copy_(self.k[:keep])
+            new_v[:keep].copy_(self.v[:keep])
+        self.k, self.v = new_k, new_v
+
+
 class LayerBlockPool:
     def __init__(
         self,
@@ -39,6 +75,7 @@ class LayerBlockPool:
         initial_blocks: int,
         growth_factor: float,
         dtype: torch.dtype | None = None,
+        storage: KVStorage | None = None,
     ):
         self.block_size = block_size
         self.initial_blocks = initial_blocks
@@ -53,6 +90,7 @@ class LayerBlockPool:
         self.capacity_blocks = 0
         self.kv_dtype = dtype
         self.mutations = 0
+        self.storage = storage
 
     def ensure_initialized(
         self,
@@ -79,14 +117,26 @@ class LayerBlockPool:
             else int(math.ceil(self.capacity_blocks * (self.growth_factor - 1.0))),
         )
         grow_by = max(grow_by, 1)
-        new_k = torch.zeros(grow_by, self.num_heads, self.block_size, self.head_dim, dtype=self.dtype, device=self.device)
-        new_v = torch.zeros_like(new_k)
-        if self.k_blocks is None:
-            self.k_blocks = new_k
-            self.v_blocks = new_v
+        if self.storage is not None:
+            # Same logical growth, as a longer view of fixed storage: the new blocks are zeroed
+            # (the storage may hold an earlier pool's data) and existing blocks keep their place.
+            tail = (self.num_heads, self.block_size, self.head_dim)
+            old_cap = self.capacity_blocks
+            self.storage.ensure(tail, self.dtype, self.device, old_cap + grow_by, keep=old_cap)
+            self.storage.k[old_cap:old_cap + grow_by].zero_()
+            self.storage.v[old_cap:old_cap + grow_by].zero_()
+            self.k_blocks = self.storage.k[: old_cap + grow_by]
+            self.v_blocks = self.storage.v[: old_cap + grow_by]
         else:
-            self.k_blocks = torch.cat([self.k_blocks, new_k], dim=0)
-            self.v_blocks = torch.cat([self.v_blocks, new_v], dim=0)
+            new_k = torch.zeros(grow_by, self.num_heads, self.block_size, self.head_dim, dtype=self.dtype,
+                                device=self.device)
+            new_v = torch.zeros_like(new_k)
+            if self.k_blocks is None:
+                self.k_blocks = new_k
+                self.v_blocks = new_v
+            else:
+                self.k_blocks = torch.cat([self.k_blocks, new_k], dim=0)
+                self.v_blocks = torch.cat([self.v_blocks, new_v], dim=0)
         start = self.capacity_blocks
         self.capacity_blocks += grow_by
         self.free_block_ids.extend(range(start, self.capacity_blocks))

@@ -1,15 +1,16 @@
 """Decoder-only LM with per-layer paged KV pools (src/model/transformer.py of the reference).
 
 TinyTransformerLM: token + learned position embeddings, pre-LayerNorm blocks (attention, GELU
-MLP), final LayerNorm, bias-free lm_head; one LayerBlockPool per layer, created lazily. Module
-and parameter names match the reference so state dicts load across the two. On the "hip_paged"
-backend, one-token cached steps over per-layer batched caches replay a captured HIP graph
-(src/model/graph_decode.py); everything else runs eagerly.
+MLP), final LayerNorm, bias-free lm_head; one LayerBlockPool per layer, created lazily, each a
+view of a per-layer KVStorage the model keeps (fixed device addresses). Module and parameter
+names match the reference so state dicts load across the two. On the "hip_paged" backend, cached
+steps over per-layer batched caches (decode steps and prefill chunks up to 256 tokens) replay
+captured HIP graphs (src/model/graph_decode.py); everything else runs eagerly.
 """
 import torch
 import torch.nn as nn
 
-from src.cache.paged_kv import BatchedPagedKVCache, LayerBlockPool, PagedKVCacheState
+from src.cache.paged_kv import BatchedPagedKVCache, KVStorage, LayerBlockPool, PagedKVCacheState
 from src.config import ATTENTION_BACKENDS
 from src.model.attention import CausalSelfAttention
 
@@ -50,6 +51,7 @@ class TinyTransformerLM(nn.Module):
         kv_pool_growth_factor: float = 2.0,
         enable_attention_correctness_checks: bool = False,
         kv_cache_dtype: torch.dtype | None = None,
+        kv_pool_reserve_blocks: int | None = None,
     ):
         super().__init__()
         if attention_backend not in ATTENTION_BACKENDS:
@@ -72,6 +74,12 @@ class TinyTransformerLM(nn.Module):
         self.ln_f = nn.LayerNorm(d_model)
         self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
         self.layer_block_pools: list[LayerBlockPool] | None = None
+        # Physical KV storage per layer, kept across pool resets (pools are prefix views of it):
+        # None = ceil(max_seq_len / block) * 32 blocks, 0 = plain pools that reallocate on growth.
+        if kv_pool_reserve_blocks is None:
+            kv_pool_reserve_blocks = max(kv_pool_initial_blocks, 32 * -(-max_seq_len // kv_block_size))
+        self._kv_storages = [KVStorage(kv_pool_reserve_blocks) for _ in range(num_layers)] if kv_pool_reserve_blocks else None
+        self._graph_step = None
 
     def _ensure_layer_block_pools(self) -> list[LayerBlockPool]:
         if self.layer_block_pools is None:
@@ -81,23 +89,55 @@ class TinyTransformerLM(nn.Module):
                     initial_blocks=self.kv_pool_initial_blocks,
                     growth_factor=self.kv_pool_growth_factor,
                     dtype=self.kv_cache_dtype,
+                    storage=self._kv_storages[i] if self._kv_storages else None,
                 )
-                for _ in self.blocks
+                for i in range(len(self.blocks))
             ]
         return self.layer_block_pools
 
     def reset_paged_cache_pools(self) -> None:
         self.layer_block_pools = None
-        if getattr(self, "_graph_decode", None) is not None:
-            self._graph_decode.captured.clear()
 
-    def _graph_decode_runner(self):
-        """Lazily created HIP-graph runner for one-token decode steps (see graph_decode.py)."""
-        if getattr(self, "_graph_decode", None) is None:
-            from src.model.graph_decode import GraphedDecodeStep
+    def _graph_runner(self):
+        """Lazily created HIP-graph runner for cached steps (see graph_decode.py)."""
+        if self._graph_step is None:
+            from src.model.graph_decode import GraphedStep
 
-            self._graph_decode = GraphedDecodeStep(self)
-        return self._graph_decode
+            self._graph_step = GraphedStep(self)
+        return self._graph_step
+
+    @torch.no_grad()
+    def prepare_graphs(self, max_batch: int, device) -> int:
+        """Capture the HIP graphs of cached steps ahead of time: for every batch size up to
+        max_batch, one prefill chunk per length bucket and one decode step, on throwaway
+        requests that are released afterwards. Leaves fresh pools; returns the captures made."""
+        from src.model.graph_decode import T_BUCKETS
+
+        device = torch.device(device)
+        if device.type != "cuda" or self.attention_backend != "hip_paged" or self._kv_storages is None:
+            return 0
+        runner = self._graph_runner()
+        before = runner.captures
+        for B in range(1, max_batch + 1):
+            per_request = self.create_request_kv_caches(B)
+            pools = self._ensure_layer_block_pools()
+
+            def stacked():
+                return [BatchedPagedKVCache([per_request[r][l] for r in range(B)], pools[l])
+                        for l in range(len(self.blocks))]
+
+            pos = 0
+            for T in (16,) + tuple(T_BUCKETS) + (1,):
+                if pos + T > self.max_seq_len:
+                    continue
+                ids = torch.zeros((B, T), dtype=torch.long, device=device)
+                self(ids, kv_caches=stacked(), use_cache=True, position_offset=pos, current_lengths=T)
+                pos += T
+            for r in range(B):
+                self.release_request_caches(per_request[r])
+        torch.cuda.synchronize(device)
+        self.reset_paged_cache_pools()
+        return runner.captures - before
 
     def create_request_kv_caches(self, batch_size: int) -> list[list[PagedKVCacheState]]:
         pools = self._ensure_layer_block_pools()
@@ -147,13 +187,16 @@ class TinyTransformerLM(nn.Module):
     ):
         B, T = input_ids.shape
         device = input_ids.device
-        if (use_cache and T == 1 and kv_caches is not None and input_ids.is_cuda
-                and (current_lengths is None or (isinstance(current_lengths, int) and current_lengths == 1))):
-            runner = self._graph_decode_runner()
+        if use_cache and kv_caches is not None and input_ids.is_cuda:
+            runner = self._graph_runner()
             if runner.usable(input_ids, kv_caches):
-                if isinstance(position_offset, int):
-                    position_offset = torch.full((B,), position_offset, dtype=torch.long, device=device)
-                return runner(input_ids, position_offset.view(B), kv_caches), list(kv_caches)
+                if current_lengths is None:
+                    cur = [T] * B
+                elif isinstance(current_lengths, int):
+                    cur = [current_lengths] * B
+                else:
+                    cur = [int(x) for x in current_lengths.reshape(-1).tolist()]
+                return runner(input_ids, position_offset, cur, kv_caches), list(kv_caches)
         if isinstance(position_offset, int):
             positions = torch.arange(position_offset, position_offset + T, device=device).unsqueeze(0).expand(B, T)
         else:

@@ -158,3 +158,46 @@ def test_byte_accounting():
     assert state.reserved_bytes() == 2 * pool.bytes_per_block()
     assert state.fragmentation_bytes() == state.reserved_bytes() - state.live_bytes()
     assert pool.reserved_bytes() == pool.capacity_blocks * pool.bytes_per_block()
+
+
+# --- storage-backed pools keep the reference's logical behaviour ----------------------------------
+def test_storage_backed_pool_matches_plain_pool():
+    from src.cache.paged_kv import KVStorage
+
+    g = torch.Generator().manual_seed(31)
+    storage = KVStorage(reserve_blocks=5)
+    plain = LayerBlockPool(block_size=4, initial_blocks=2, growth_factor=2.0)
+    backed = LayerBlockPool(block_size=4, initial_blocks=2, growth_factor=2.0, storage=storage)
+    sp = [PagedKVCacheState(pool=plain) for _ in range(3)]
+    sb = [PagedKVCacheState(pool=backed) for _ in range(3)]
+    for step in range(6):
+        T = [9, 3, 7, 1, 12, 4][step]
+        k = torch.randn(3, 2, T, 8, generator=g)
+        v = torch.randn(3, 2, T, 8, generator=g)
+        cur = torch.tensor([T, max(T - 2, 0), T])
+        BatchedPagedKVCache(sp, plain).append_batch(k, v, cur)
+        BatchedPagedKVCache(sb, backed).append_batch(k, v, cur)
+        if step == 3:
+            sp[1].release()
+            sb[1].release()
+        assert [s.block_ids for s in sp] == [s.block_ids for s in sb]
+        assert plain.capacity_blocks == backed.capacity_blocks and plain.free_block_ids == backed.free_block_ids
+        assert torch.equal(plain.k_blocks, backed.k_blocks) and torch.equal(plain.v_blocks, backed.v_blocks)
+        assert backed.reserved_bytes() == plain.reserved_bytes()
+        assert backed.k_blocks.data_ptr() == storage.k.data_ptr()
+    assert storage.blocks >= backed.capacity_blocks > 5  # outgrew the reservation once
+
+
+def test_storage_reuse_starts_from_zeroed_blocks():
+    from src.cache.paged_kv import KVStorage
+
+    storage = KVStorage(reserve_blocks=16)
+    first = LayerBlockPool(block_size=4, initial_blocks=4, growth_factor=2.0, storage=storage)
+    st = PagedKVCacheState(pool=first)
+    st.append(torch.ones(1, 2, 14, 8), torch.ones(1, 2, 14, 8), length=14)  # held, never released
+    ptr = storage.k.data_ptr()
+    second = LayerBlockPool(block_size=4, initial_blocks=4, growth_factor=2.0, storage=storage)
+    second.ensure_initialized(2, 8, torch.float32, "cpu")
+    assert second.k_blocks.data_ptr() == ptr
+    assert float(second.k_blocks.abs().sum()) == 0.0 and float(second.v_blocks.abs().sum()) == 0.0
+    assert second.free_block_ids == [0, 1, 2, 3] and second.capacity_blocks == 4
