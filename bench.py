@@ -21,7 +21,8 @@ Also reported on the same line:
                  at 32 req/s, max batch 8, prefill chunk 256, 1536-token iteration budget, greedy;
                  tokens/s and p50 TTFT on the scheduler's virtual clock, plus wall time.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-e2e]
-                       [--no-secondary] [--calibrate-copy]
+                       [--no-secondary] [--no-decode] [--calibrate-copy]
+(--no-decode skips the headline decode measurement; it is for profiling the other workloads alone.)
 """
 from __future__ import annotations
 
@@ -303,11 +304,13 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True)
     }
 
 
-def continuous_batching_pair(device) -> dict:
+def continuous_batching_pair(device, with_cpu: bool = True) -> dict:
     """GPU run (hip_paged) and the same-run CPU baseline (torch paged_reference on the host cores)."""
     import torch
 
     gpu = continuous_batching(device, "hip_paged")
+    if not with_cpu:
+        return gpu
     torch.set_num_threads(cpu_threads())
     log(f"continuous batching on the CPU ({torch.get_num_threads()} threads)")
     cpu = continuous_batching(torch.device("cpu"), "paged_reference", warmup=False)
@@ -326,6 +329,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the headline decode (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true", help="also run a copy kernel of known size")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -341,51 +345,54 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
-    log("building the large ragged decode batch (B=256, 32x128, bf16 KV)")
-    batch = workloads.large_decode(seed=0, device=dev)
-    nbytes = batch.decode_bytes()
-    log(f"pool blocks={batch.k_pool.shape[0]} tokens={sum(batch.seq_lens)} algorithmic bytes/call={nbytes}")
-    ms, wall_ms, _ = time_decode(batch, args.steps, args.warmup)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"decode: {ms:.3f} ms/call (events), {wall_ms:.3f} ms/call (wall), {gbs:.1f} GB/s")
-
-    traffic = pmc_traffic_bytes()
     result = {
         "metric": METRIC,
-        "value": round(gbs, 2),
+        "value": None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16-kv/f32-acc",
         "data": "synthetic",
-        "config": {
-            "workload": "large ragged paged decode: 256 requests, 32 heads x 128, block 16, lengths log-uniform "
-                        "[512, 32768], bf16 KV, fp32 q/out, pool 1.1x, shuffled block tables",
-            "batch": batch.batch,
-            "tokens": sum(batch.seq_lens),
-            "bytes_per_step": nbytes,
-        },
-        "pct_peak_hbm": round(100.0 * gbs / HBM_PEAK_GBS, 2),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(gbs, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-        },
     }
-    if not args.no_cpu_baseline:
-        log("CPU baseline (oracle over the batch)")
-        result["cpu_baseline"] = cpu_baseline(batch)
-        result["cpu_reference_loop"] = reference_loop_rate(batch)
-    del batch
-    torch.cuda.empty_cache()
+    if not args.no_decode:
+        log("building the large ragged decode batch (B=256, 32x128, bf16 KV)")
+        batch = workloads.large_decode(seed=0, device=dev)
+        nbytes = batch.decode_bytes()
+        log(f"pool blocks={batch.k_pool.shape[0]} tokens={sum(batch.seq_lens)} algorithmic bytes/call={nbytes}")
+        ms, wall_ms, _ = time_decode(batch, args.steps, args.warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"decode: {ms:.3f} ms/call (events), {wall_ms:.3f} ms/call (wall), {gbs:.1f} GB/s")
+        result.update({
+            "value": round(gbs, 2),
+            "ms_per_step": round(ms, 4),
+            "config": {
+                "workload": "large ragged paged decode: 256 requests, 32 heads x 128, block 16, lengths log-uniform "
+                            "[512, 32768], bf16 KV, fp32 q/out, pool 1.1x, shuffled block tables",
+                "batch": batch.batch,
+                "tokens": sum(batch.seq_lens),
+                "bytes_per_step": nbytes,
+            },
+            "pct_peak_hbm": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+            "roofline": {
+                "bound": "hbm",
+                "achieved": round(gbs, 2),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": pmc_traffic_bytes(),
+            },
+        })
+        if not args.no_cpu_baseline:
+            log("CPU baseline (oracle over the batch)")
+            result["cpu_baseline"] = cpu_baseline(batch)
+            result["cpu_reference_loop"] = reference_loop_rate(batch)
+        del batch
+        torch.cuda.empty_cache()
     if args.calibrate_copy:
         calibration_copy(dev)
     if not args.no_secondary:
@@ -393,7 +400,7 @@ def main() -> int:
         result["secondary"] = secondary_workloads(dev, args.steps)
     if not args.no_e2e:
         log("end-to-end continuous batching (200 requests, 32 req/s)")
-        result["continuous_batching"] = continuous_batching_pair(dev)
+        result["continuous_batching"] = continuous_batching_pair(dev, with_cpu=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
 
