@@ -22,10 +22,37 @@ struct AttnArgs {
   const int32_t* order;  // decode only: request processing order, may be null
   int32_t B, H, T, head_dim, block_size;
   float scale_log2;      // softmax scale * log2(e)
-  int32_t num_splits;    // decode: workgroups per (request, head), >= 1
-  int32_t split_blocks;  // decode: KV blocks per split when num_splits > 1
-  float* ws;             // decode: [B*H*num_splits][head_dim + 2] partial (m, l, acc) records
+  int32_t num_splits;    // workgroups per work unit along the KV axis, >= 1
+  int32_t split_blocks;  // KV blocks per split when num_splits > 1
+  float* ws;             // partial (m, l, acc[head_dim]) records of the splits
 };
+
+// Wave-wide partner exchange on gfx950 without an LDS round trip: v_permlane16_swap /
+// v_permlane32_swap with both operands equal leave, in every lane, its own value in one result
+// and the value of lane ^ 16 (resp. lane ^ 32) in the other, so a symmetric op over the two
+// results reduces over the lane pair.
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Wide-tile bf16-KV prefill (128 query rows per workgroup, KV staged through LDS). Defined in
+// pa_prefill_wide.hip.
+bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size);
+int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len);
+int launch_prefill_wide(const AttnArgs& a, int io_dtype, hipStream_t stream);
 
 // Generic one-wavefront-per-(request, head, query row) kernel for shapes without a tuned kernel
 // (any block_size, head_dim <= 512). Defined in pa_decode.hip.

@@ -188,11 +188,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
   const int n = valid_keys(L, C, 0);
   int nb = (n + BS - 1) / BS;
   nb = nb < a.max_pages ? nb : a.max_pages;
-  int jb = 0, je = nb;
+  int jb = 0, je = nb, nact = 1;
   if (nsplit > 1) {
+    nact = nb > 0 ? (nb + a.split_blocks - 1) / a.split_blocks : 1;
+    if (split >= nact) return;  // uniform over the workgroup, before any barrier
     jb = split * a.split_blocks;
     je = jb + a.split_blocks < nb ? jb + a.split_blocks : nb;
-    if (jb > je) jb = je;
   }
 
   const int r = lane % LPR;
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
       lsum = fmaf(sm_l[ww], f, lsum);
       A = fmaf(sm_acc[ww][d], f, A);
     }
-    if (nsplit == 1) {
+    if (nact == 1) {
       IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
       Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
     } else {
@@ -276,20 +277,24 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
   }
 }
 
-// Merge the num_splits partial records of each (request, head): one wavefront per pair.
+// Merge the partial records of each (request, head) written by its active splits (the number a
+// split computes from the request's length): one wavefront per pair.
 template <typename IO>
 __global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh % a.H;
   const int HD = a.head_dim;
-  const int S = a.num_splits;
-  const float* base = a.ws + (int64_t)bh * S * (HD + 2);
+  int nb = (valid_keys(a.seq_lens[b], a.cur_lens[b], 0) + 15) / 16;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+  const int nact = nb > 0 ? (nb + a.split_blocks - 1) / a.split_blocks : 1;
+  if (nact == 1) return;  // the split wrote the output itself
+  const float* base = a.ws + (int64_t)bh * a.num_splits * (HD + 2);
   float M = kNegBig;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, base[(int64_t)s * (HD + 2)]);
+  for (int s = 0; s < nact; ++s) M = fmaxf(M, base[(int64_t)s * (HD + 2)]);
   IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
   for (int d = threadIdx.x; d < HD; d += kWave) {
     float lsum = 0.f, A = 0.f;
-    for (int s = 0; s < S; ++s) {
+    for (int s = 0; s < nact; ++s) {
       const float* rec = base + (int64_t)s * (HD + 2);
       const float f = fast_exp2(rec[0] - M);
       lsum = fmaf(rec[1], f, lsum);

@@ -1,12 +1,12 @@
 // Chunked causal prefill attention over paged KV for gfx950, on matrix cores.
 //
-// One workgroup of 4 wavefronts per (request, head, tile of 16 query rows); the wavefronts take
-// the tile's KV blocks round-robin and merge their online-softmax states in LDS at the end.
-// For each 16-token KV block a wavefront computes the transposed score tile S^T = K Q^T (16 keys x
-// 16 queries) and accumulates the transposed output O^T += V^T P^T. With the 16x16 MFMA output
-// layout (lane = 16*G + c holds rows 4G..4G+3 of column c), lane (G, c) then owns query c's
-// scores for keys 4G..4G+3, its output column, and its softmax state, so:
-//   - the row max / row sum over keys is 4 registers plus two cross-group shuffles;
+// Work unit = (request, head, tile of 16 query rows). One workgroup of 4 wavefronts per unit and
+// KV split; the wavefronts take the split's KV blocks round-robin and merge their online-softmax
+// states in LDS at the end. For each 16-token KV block a wavefront computes the transposed score
+// tile S^T = K Q^T (16 keys x 16 queries) and accumulates the transposed output O^T += V^T P^T.
+// With the 16x16 MFMA output layout (lane = 16*G + c holds rows 4G..4G+3 of column c), lane
+// (G, c) then owns query c's scores for keys 4G..4G+3, its output column, and its softmax state:
+//   - the row max / row sum over keys is a few registers plus two cross-group permlane swaps;
 //   - the score registers ARE the B operand (P^T) of the next product, with no data movement;
 //   - rescaling the output by the new running max is a per-lane scalar.
 // The contraction index of each product is permuted so that every lane reads contiguous 16-byte
@@ -16,6 +16,17 @@
 // fp32 KV uses v_mfma_f32_16x16x4_f32 (fp32 products, like the reference). bf16 KV uses
 // v_mfma_f32_16x16x32_bf16 for QK^T (q rounded to bf16) and v_mfma_f32_16x16x16_bf16 for PV
 // (softmax weights rounded to bf16), accumulating in fp32.
+//
+// Split-K: when num_splits > 1 each unit's KV blocks are cut into ranges of split_blocks blocks,
+// one workgroup per range. Work items are ordered split-major, so the grid holds many
+// equal-sized items instead of a few long ones. A unit with one active split writes its output
+// directly; otherwise each split writes its (m, l, acc) rows to the workspace and
+// prefill_merge_kernel combines them. (A same-launch merge by the last split to finish needs
+// agent-scope fences, which write back the die-local L2 in every workgroup: on MI355X that made
+// split launches 5-20x slower than the second launch.)
+#include <stdlib.h>
+#include <string.h>
+
 #include <type_traits>
 
 #include "pa_attention.h"
@@ -43,26 +54,39 @@ __device__ __forceinline__ void load_words(const void* p, uint32_t (&w)[NWORDS])
   }
 }
 
+template <typename KV, int HD>
+struct PrefillShape {
+  static constexpr bool kBf16 = std::is_same<KV, uint16_t>::value;
+  static constexpr int QD = HD / 4;              // head_dim values per lane in the QK^T operands
+  static constexpr int DT = HD / 16;             // output tiles of 16 head_dim columns
+  static constexpr int KW = kBf16 ? QD / 2 : QD;  // 32-bit words of K per lane per block
+  static constexpr int VW = kBf16 ? DT / 2 : DT;  // 32-bit words per V row per lane per block
+};
+
 template <typename KV, typename IO, int HD>
 __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
   constexpr int BS = 16;
   constexpr int NW = 4;
-  constexpr int QD = HD / 4;   // head_dim values per lane in the QK^T operands
-  constexpr int DT = HD / 16;  // output tiles of 16 head_dim columns
-  constexpr bool kBf16 = std::is_same<KV, uint16_t>::value;
+  using Sh = PrefillShape<KV, HD>;
+  constexpr int QD = Sh::QD, DT = Sh::DT, KW = Sh::KW, VW = Sh::VW;
+  constexpr bool kBf16 = Sh::kBf16;
 
   __shared__ float sm_o[NW][16][HD + 1];
   __shared__ float sm_m[NW][16];
   __shared__ float sm_l[NW][16];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int G = lane >> 4;
   const int c = lane & 15;
 
+  // Work item: split-major, then (request, head), then query tiles from the last (heaviest) one.
   const int ntiles = (a.T + 15) / 16;
-  const int qt = blockIdx.x % ntiles;
-  const int bh = blockIdx.x / ntiles;
+  const int units = a.B * a.H * ntiles;
+  const int split = blockIdx.x / units;
+  const int unit = blockIdx.x - split * units;
+  const int qt = ntiles - 1 - unit % ntiles;
+  const int bh = unit / ntiles;
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int i0 = qt * 16;
@@ -75,6 +99,13 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
   const int n_max = valid_keys(L, C, i_last);  // nondecreasing in the row index
   int nb = (n_max + BS - 1) / BS;
   nb = nb < a.max_pages ? nb : a.max_pages;
+  int jb = 0, je = nb, nact = 1;
+  if (a.num_splits > 1) {
+    nact = nb > 0 ? (nb + a.split_blocks - 1) / a.split_blocks : 1;
+    if (split >= nact) return;  // uniform over the workgroup, before any barrier
+    jb = split * a.split_blocks;
+    je = jb + a.split_blocks < nb ? jb + a.split_blocks : nb;
+  }
 
   // Q operand: row i, head_dim [G*QD, G*QD + QD), pre-scaled into the log2 domain.
   float qv[QD];
@@ -110,8 +141,6 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
 
   // Registers of one KV tile as this lane needs them: K row c, head_dim [G*QD, G*QD + QD), and
   // V rows 4G..4G+3, head_dim [c*DT, c*DT + DT).
-  constexpr int KW = kBf16 ? QD / 2 : QD;
-  constexpr int VW = kBf16 ? DT / 2 : DT;
   struct Tile {
     uint32_t k[KW];
     uint32_t v[4][VW];
@@ -124,6 +153,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) load_words<VW>(vpool + base + (4 * G + r) * HD + c * DT, t.v[r]);
   };
+
+  // Fold one tile (KV block j) into the running state.
   auto fold = [&](const Tile& tl, int j) {
     // ---- S^T = K Q^T ------------------------------------------------------------------------
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
@@ -147,8 +178,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
       p[r] = (tl.ok && t < n_c) ? sacc[r] : -INFINITY;
       mloc = fmaxf(mloc, p[r]);
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    mloc = max_xor32(max_xor16(mloc));
     const float mnew = fmaxf(m, mloc);
     const float alpha = fast_exp2(m - mnew);
     float ps = 0.f;
@@ -157,8 +187,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
       p[r] = fast_exp2(p[r] - mnew);
       ps += p[r];
     }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = sum_xor32(sum_xor16(ps));
     l = l * alpha + ps;
     m = mnew;
 #pragma unroll
@@ -183,32 +212,36 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
     }
   };
 
-  // This wave's blocks j = w + k*NW, k < mine, in chunks of one page-table entry per lane; the
-  // next block's tile is loaded into the second register set while the current one is folded.
-  const int mine = nb > w ? (nb - w + NW - 1) / NW : 0;
+  // This wave's blocks j = jb + w + k*NW, k < mine, in chunks of one page-table entry per lane.
+  // The next block's tile loads into the second register set while the current one is folded;
+  // the steady-state loop issues its loads unconditionally so the compiler's wait counts stay
+  // exact, and the tail is peeled.
+  const int span = je - jb;
+  const int mine = span > w ? (span - w + NW - 1) / NW : 0;
   for (int c0 = 0; c0 < mine; c0 += kWave) {
     const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
     int ids = -1;
-    if (lane < cnt) ids = pt[w + (c0 + lane) * NW];
+    if (lane < cnt) ids = pt[jb + w + (c0 + lane) * NW];
+    auto jidx = [&](int k) { return jb + w + (c0 + k) * NW; };
     Tile t0, t1;
     issue(t0, __builtin_amdgcn_readlane(ids, 0));
-    int i = 0;
-    for (; i + 2 < cnt; i += 2) {
-      issue(t1, __builtin_amdgcn_readlane(ids, i + 1));
-      fold(t0, w + (c0 + i) * NW);
-      issue(t0, __builtin_amdgcn_readlane(ids, i + 2));
-      fold(t1, w + (c0 + i + 1) * NW);
+    int k = 0;
+    for (; k + 2 < cnt; k += 2) {
+      issue(t1, __builtin_amdgcn_readlane(ids, k + 1));
+      fold(t0, jidx(k));
+      issue(t0, __builtin_amdgcn_readlane(ids, k + 2));
+      fold(t1, jidx(k + 1));
     }
-    if (i + 1 < cnt) {
-      issue(t1, __builtin_amdgcn_readlane(ids, i + 1));
-      fold(t0, w + (c0 + i) * NW);
-      fold(t1, w + (c0 + i + 1) * NW);
+    if (k + 1 < cnt) {
+      issue(t1, __builtin_amdgcn_readlane(ids, k + 1));
+      fold(t0, jidx(k));
+      fold(t1, jidx(k + 1));
     } else {
-      fold(t0, w + (c0 + i) * NW);
+      fold(t0, jidx(k));
     }
   }
 
-  // ---- merge the wavefronts' states and write the tile -----------------------------------
+  // ---- merge the wavefronts' states ---------------------------------------------------------
 #pragma unroll
   for (int t = 0; t < DT; ++t)
 #pragma unroll
@@ -219,11 +252,12 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
   }
   __syncthreads();
 
-  for (int idx = threadIdx.x; idx < 16 * HD; idx += NW * kWave) {
+  const int rows = a.T - i0 < 16 ? a.T - i0 : 16;
+  float* rec0 = nullptr;
+  if (nact > 1) rec0 = a.ws + ((int64_t)unit * a.num_splits) * 16 * (HD + 2);
+  for (int idx = threadIdx.x; idx < rows * HD; idx += NW * kWave) {
     const int cc = idx / HD;
     const int d = idx - cc * HD;
-    const int row = i0 + cc;
-    if (row >= a.T) continue;
     float M = kNegBig;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_m[ww][cc]);
@@ -234,7 +268,51 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const AttnArgs a) {
       lsum = fmaf(sm_l[ww][cc], f, lsum);
       A = fmaf(sm_o[ww][cc][d], f, A);
     }
-    IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
+    if (nact == 1) {
+      IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(i0 + cc) * a.o_st;
+      Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
+    } else {
+      float* rec = rec0 + ((int64_t)split * 16 + cc) * (HD + 2);
+      if (d == 0) {
+        rec[0] = M;
+        rec[1] = lsum;
+      }
+      rec[2 + d] = A;
+    }
+  }
+}
+
+// Merge the partial rows of each unit's active splits (the number a split computes from the
+// request's lengths): one workgroup per (request, head, 16-row tile).
+template <typename IO, int HD>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
+  const int ntiles = (a.T + 15) / 16;
+  const int unit = blockIdx.x;
+  const int qt = ntiles - 1 - unit % ntiles;
+  const int bh = unit / ntiles;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int i0 = qt * 16;
+  const int i_last = (i0 + 15) < (a.T - 1) ? (i0 + 15) : (a.T - 1);
+  int nb = (valid_keys(a.seq_lens[b], a.cur_lens[b], i_last) + 15) / 16;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+  const int nact = nb > 0 ? (nb + a.split_blocks - 1) / a.split_blocks : 1;
+  if (nact == 1) return;  // the split wrote the output itself
+  const int rows = a.T - i0 < 16 ? a.T - i0 : 16;
+  const float* rec0 = a.ws + ((int64_t)unit * a.num_splits) * 16 * (HD + 2);
+  for (int idx = threadIdx.x; idx < rows * HD; idx += 256) {
+    const int cc = idx / HD;
+    const int d = idx - cc * HD;
+    float M = kNegBig;
+    for (int s = 0; s < nact; ++s) M = fmaxf(M, rec0[((int64_t)s * 16 + cc) * (HD + 2)]);
+    float lsum = 0.f, A = 0.f;
+    for (int s = 0; s < nact; ++s) {
+      const float* rec = rec0 + ((int64_t)s * 16 + cc) * (HD + 2);
+      const float f = fast_exp2(rec[0] - M);
+      lsum = fmaf(rec[1], f, lsum);
+      A = fmaf(rec[2 + d], f, A);
+    }
+    IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(i0 + cc) * a.o_st;
     Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
   }
 }
@@ -246,9 +324,43 @@ static bool dispatch_prefill_io(const AttnArgs& a, dim3 grid, hipStream_t stream
   return false;
 }
 
+template <typename IO>
+static void launch_prefill_merge(const AttnArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.head_dim == 64) prefill_merge_kernel<IO, 64><<<grid, 256, 0, stream>>>(a);
+  else prefill_merge_kernel<IO, 128><<<grid, 256, 0, stream>>>(a);
+}
+
+static bool prefill_fast_shape(int32_t head_dim, int32_t block_size) {
+  return block_size == 16 && (head_dim == 64 || head_dim == 128);
+}
+
+// Kernel choice for bf16 KV: the wide-tile kernel when its (request, head, 128-row tile) units
+// fill the GPU at least twice over, else the 16-row kernel. PAGED_HIP_PREFILL_KERNEL=wide / tile
+// forces one of them (tests use it to cover both at small sizes).
+static bool use_wide_prefill(int32_t batch, int32_t num_heads, int32_t query_len) {
+  const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
+  if (env != nullptr && strcmp(env, "wide") == 0) return true;
+  if (env != nullptr && strcmp(env, "tile") == 0) return false;
+  return prefill_wide_units(batch, num_heads, query_len) >= 2 * (int64_t)pa_host::device_cu_count();
+}
+
+static int prefill_num_splits(int32_t max_pages, int32_t split_blocks) {
+  if (split_blocks <= 0 || max_pages <= split_blocks) return 1;
+  return (int)((max_pages + split_blocks - 1) / split_blocks);
+}
+
 }  // namespace pa
 
 using namespace pa;
+
+extern "C" size_t pa_prefill_workspace_size(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
+                                            int32_t max_pages, int32_t split_blocks) {
+  if (batch <= 0 || num_heads <= 0 || query_len <= 0 || !prefill_fast_shape(head_dim, 16)) return 0;
+  const int s = prefill_num_splits(max_pages, split_blocks);
+  if (s <= 1) return 0;
+  const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);
+  return (size_t)units * s * 16 * (head_dim + 2) * sizeof(float);
+}
 
 extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                           void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
@@ -257,7 +369,8 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
                           const int32_t* seq_lens, const int32_t* cur_lens,
                           int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
-                          int32_t block_size, float scale, void* stream_) {
+                          int32_t block_size, float scale, int32_t split_blocks,
+                          void* workspace, size_t workspace_bytes, void* stream_) {
   pa_host::clear_error();
   PA_CHECK_ARG(batch >= 0 && num_heads > 0 && query_len >= 0 && head_dim > 0 && block_size > 0,
                "bad sizes: batch=%d heads=%d query_len=%d head_dim=%d block_size=%d", batch, num_heads,
@@ -283,12 +396,23 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   a.scale_log2 = scale * kLog2e;
   a.num_splits = 1; a.split_blocks = 0; a.ws = nullptr;
 
-  const bool fast = block_size == 16 && (head_dim == 64 || head_dim == 128);
-  if (!fast) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
+  if (!prefill_fast_shape(head_dim, block_size)) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
+  if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
+      use_wide_prefill(batch, num_heads, query_len))
+    return launch_prefill_wide(a, io_dtype, stream);
 
   const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);
-  if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
-  const dim3 grid((unsigned)units);
+  const int nsplit = prefill_num_splits(max_pages, split_blocks);
+  if (nsplit > 1) {
+    const size_t need = pa_prefill_workspace_size(batch, num_heads, query_len, head_dim, max_pages, split_blocks);
+    if (workspace == nullptr || workspace_bytes < need)
+      PA_FAIL(PA_ERR_WORKSPACE, "prefill workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
+    a.num_splits = nsplit;
+    a.split_blocks = split_blocks;
+    a.ws = static_cast<float*>(workspace);
+  }
+  if (units * nsplit > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
+  const dim3 grid((unsigned)(units * nsplit));
   bool ok;
   if (kv_dtype == PA_DTYPE_F32)
     ok = io_dtype == PA_DTYPE_F32 ? dispatch_prefill_io<float, float>(a, grid, stream)
@@ -298,5 +422,10 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                   : dispatch_prefill_io<uint16_t, uint16_t>(a, grid, stream);
   if (!ok) PA_FAIL(PA_ERR_UNSUPPORTED, "no prefill kernel for head_dim %d", head_dim);
   PA_CHECK_LAUNCH("prefill kernel");
+  if (nsplit > 1) {
+    if (io_dtype == PA_DTYPE_F32) launch_prefill_merge<float>(a, dim3((unsigned)units), stream);
+    else launch_prefill_merge<uint16_t>(a, dim3((unsigned)units), stream);
+    PA_CHECK_LAUNCH("prefill merge kernel");
+  }
   return PA_OK;
 }

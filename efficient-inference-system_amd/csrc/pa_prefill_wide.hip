@@ -1,0 +1,320 @@
+// Wide-tile chunked prefill attention for bf16 KV pools on gfx950 (long chunks over long
+// contexts, where the 16-row kernel would re-read every KV block once per 16 query rows).
+//
+// One workgroup of 4 wavefronts per (request, head, tile of 128 query rows); wavefront w owns
+// rows 32w..32w+31 of the tile. The workgroup walks the KV blocks in steps of 32 keys (two
+// 16-token blocks): each step's K and V tiles are loaded from HBM once, cooperatively, into
+// double-buffered LDS (the next step's global loads are in flight while the current step is
+// computed), and all four wavefronts read them from there.
+//
+// Per step and wavefront, with v_mfma_f32_32x32x16_bf16 (fp32 accumulation):
+//   S^T = K Q^T      32 keys x 32 queries; A = K rows from LDS, B = the wavefront's q (bf16,
+//                    pre-scaled into the log2 domain) held in registers for the whole walk;
+//   online softmax   lane (G2, c) = (lane / 32, lane % 32) holds query c's scores for keys
+//                    8j + 4*G2 + r (j, r < 4), so the row max / sum are 16 registers plus one
+//                    v_permlane32_swap;
+//   O^T += V^T P^T   the softmax weights of chunk mc (keys 16mc..16mc+15) are, as held, the B
+//                    operand of one MFMA per 32-row output tile (k slot (G2, e) = key
+//                    8*(2mc + e/4) + 4*G2 + e%4). Output tile u row R holds head_dim index
+//                    R*HD/32 + u, so each lane reads HD/32 contiguous values of each of its 16
+//                    key rows from LDS and the A operands are assembled in registers.
+// The QK^T contraction slot (G2, e) of MFMA s is head_dim index G2*HD/2 + 8s + e. A and B of each
+// product use the same slot map, so results do not depend on the hardware's k ordering.
+// Rounding matches the 16-row bf16 kernel: q*scale and the softmax weights are rounded to bf16
+// (nearest even) for the products, scores and accumulators stay fp32. The running max is updated
+// lazily (see kRescaleSlack) and interior steps skip the causal/length mask.
+#include "pa_attention.h"
+
+#ifndef PA_WIDE_KFIRST
+#define PA_WIDE_KFIRST 0
+#endif
+#ifndef PA_WIDE_PRIO
+#define PA_WIDE_PRIO 0
+#endif
+
+namespace pa {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values to packed bf16 (round to nearest even) with gfx950's v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Lazy rescaling threshold (log2 units): the running max only moves when a step's max exceeds it
+// by more than this, so softmax weights stay <= 2^8 and the accumulators are rescaled only in
+// the few steps where the max jumps.
+constexpr float kRescaleSlack = 8.f;
+
+constexpr int kWideWaves = 4;
+constexpr int kWideRows = kWideWaves * 32;  // query rows per workgroup
+
+template <typename IO, int HD>
+__global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const AttnArgs a) {
+  constexpr int NW = kWideWaves;
+  constexpr int KS = 32;                 // keys per step
+  constexpr int QH = HD / 2;             // head_dim values per lane in the QK^T operands
+  constexpr int NQ = HD / 16;            // QK^T MFMAs per step (k = 16 each)
+  constexpr int DU = HD / 32;            // output tiles of 32 head_dim rows
+  constexpr int RS = HD + 8;             // LDS row stride in bf16 elements (16-byte pad)
+  constexpr int RPC = HD / 8;            // 16-byte chunks per key row
+  constexpr int CPT = KS * RPC / (NW * kWave);  // chunks per thread per K (or V) step tile
+  static_assert(CPT >= 1 && KS * RPC == CPT * NW * kWave, "tile split");
+  constexpr int VW = DU / 2 > 0 ? DU / 2 : 1;     // 32-bit words per key row per lane (V reads)
+
+  __shared__ __attribute__((aligned(16))) uint16_t sk[2][KS * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t sv[2][KS * RS];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int G2 = lane >> 5;
+  const int c = lane & 31;
+
+  const int ntiles = (a.T + kWideRows - 1) / kWideRows;
+  const int unit = blockIdx.x;
+  const int qt = ntiles - 1 - unit % ntiles;  // heaviest (last) tiles of each (request, head) first
+  const int bh = unit / ntiles;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int i0 = qt * kWideRows;
+  const int iw = i0 + 32 * w;
+  const int i = iw + c;
+
+  const int L = a.seq_lens[b];
+  const int C = a.cur_lens[b];
+  const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
+  const int last_wg = (i0 + kWideRows - 1) < (a.T - 1) ? (i0 + kWideRows - 1) : (a.T - 1);
+  const int n_wg = valid_keys(L, C, last_wg);  // nondecreasing in the row index
+  int nb = (n_wg + 15) / 16;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+  const int nsteps = (nb + 1) / 2;
+  int wsteps = 0;  // steps this wavefront computes (its rows need no keys beyond them)
+  if (iw < a.T) {
+    const int last_w = (iw + 31) < (a.T - 1) ? (iw + 31) : (a.T - 1);
+    wsteps = (valid_keys(L, C, last_w) + KS - 1) / KS;
+    wsteps = wsteps < nsteps ? wsteps : nsteps;
+  }
+
+  // B operand of S^T = K Q^T: q[i][G2*QH + 8s + e] for MFMA s, pre-scaled, rounded to bf16.
+  bf16x8 qb[NQ];
+  {
+    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
+                   (int64_t)(i < a.T ? i : 0) * a.q_st + G2 * QH;
+    const float qs = i < a.T ? a.scale_log2 : 0.f;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        wd[e] = pack_bf16x2(Elem<IO>::load(qp + 8 * s + 2 * e) * qs, Elem<IO>::load(qp + 8 * s + 2 * e + 1) * qs);
+      qb[s] = __builtin_bit_cast(bf16x8, (u32x4{wd[0], wd[1], wd[2], wd[3]}));
+    }
+  }
+
+  f32x16 oacc[DU];
+#pragma unroll
+  for (int u = 0; u < DU; ++u)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[u][e] = 0.f;
+  float m = kNegBig, l = 0.f;
+
+  const uint16_t* kpool = static_cast<const uint16_t*>(a.k_pool);
+  const uint16_t* vpool = static_cast<const uint16_t*>(a.v_pool);
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+
+  // Page-table entries of step st: block 2st always exists (st < nsteps); 2st+1 may not.
+  auto step_blocks = [&](int st, int& e0, int& e1) {
+    e0 = pt[2 * st];
+    e1 = 2 * st + 1 < nb ? pt[2 * st + 1] : -1;
+  };
+  auto ok_blk = [&](int e) { return e >= 0 && e < a.num_blocks; };
+
+  // Cooperative global loads of one step's K and V tiles (thread t: chunks t + 256n).
+  u32x4 kr[CPT], vr[CPT];
+  auto gload = [&](int st) {
+    int e0, e1;
+    step_blocks(st, e0, e1);
+#pragma unroll
+    for (int n = 0; n < CPT; ++n) {
+      const int q = threadIdx.x + n * NW * kWave;
+      const int kk = q / RPC;
+      const int col = (q - kk * RPC) * 8;
+      const int e = kk < 16 ? e0 : e1;
+      const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
+      const int64_t off = (((int64_t)blk * a.H + h) * 16 + (kk & 15)) * HD + col;
+      kr[n] = *reinterpret_cast<const u32x4*>(kpool + off);
+      vr[n] = *reinterpret_cast<const u32x4*>(vpool + off);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int n = 0; n < CPT; ++n) {
+      const int q = threadIdx.x + n * NW * kWave;
+      const int kk = q / RPC;
+      const int col = (q - kk * RPC) * 8;
+      *reinterpret_cast<u32x4*>(&sk[buf][kk * RS + col]) = kr[n];
+      *reinterpret_cast<u32x4*>(&sv[buf][kk * RS + col]) = vr[n];
+    }
+  };
+
+  auto compute = [&](int buf, int st) {
+    // ---- S^T = K Q^T ------------------------------------------------------------------------
+    f32x16 sacc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+    const uint16_t* krow = &sk[buf][c * RS + G2 * QH];
+#if PA_WIDE_KFIRST
+    bf16x8 kf[NQ];
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 8 * s);
+#if PA_WIDE_PRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qb[s], sacc, 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, NQ, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, NQ, 0);
+#if PA_WIDE_PRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+#else
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 8 * s);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s], sacc, 0, 0, 0);
+    }
+#endif
+    // ---- online softmax (keys 8j + 4*G2 + r of this step) --------------------------------------
+    int e0, e1;
+    step_blocks(st, e0, e1);
+    const bool ok0 = ok_blk(e0), ok1 = ok_blk(e1);
+    const int t0 = st * KS + 4 * G2;
+    // Interior steps (both blocks valid, every key below every row's limit) need no mask.
+    const bool full = ok0 && ok1 && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
+    float p[16];
+    float mloc = -INFINITY;
+    if (full) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        p[e] = sacc[e];
+        mloc = fmaxf(mloc, p[e]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = t0 + 8 * j + r;
+          const bool ok = (j < 2 ? ok0 : ok1) && t < n_c;
+          p[4 * j + r] = ok ? sacc[4 * j + r] : -INFINITY;
+          mloc = fmaxf(mloc, p[4 * j + r]);
+        }
+    }
+    mloc = max_xor32(mloc);
+    const bool grow = mloc > m + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float mnew = grow ? mloc : m;
+      const float alpha = fast_exp2(m - mnew);
+      l *= alpha;
+#pragma unroll
+      for (int u = 0; u < DU; ++u) oacc[u] *= alpha;
+      m = mnew;
+    }
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      p[e] = fast_exp2(p[e] - m);
+      ps += p[e];
+    }
+    l += sum_xor32(ps);
+    // ---- O^T += V^T P^T -----------------------------------------------------------------------
+    // V values of this lane's 16 key rows, head_dim [c*DU, c*DU + DU).
+    uint32_t vf[16][VW];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint16_t* vp = &sv[buf][(8 * j + 4 * G2 + r) * RS + c * DU];
+        if constexpr (DU == 4) {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
+          vf[4 * j + r][0] = x[0];
+          vf[4 * j + r][1] = x[1];
+        } else {
+          vf[4 * j + r][0] = *reinterpret_cast<const uint32_t*>(vp);
+        }
+      }
+#pragma unroll
+    for (int mc = 0; mc < 2; ++mc) {
+      uint32_t pw[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(p[8 * mc + 2 * q], p[8 * mc + 2 * q + 1]);
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
+#pragma unroll
+      for (int u = 0; u < DU; ++u) {
+        uint32_t aw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t x0 = vf[8 * mc + 2 * q][u >> 1], x1 = vf[8 * mc + 2 * q + 1][u >> 1];
+          aw[q] = (u & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+        }
+        oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, (u32x4{aw[0], aw[1], aw[2], aw[3]})), pb, oacc[u], 0, 0, 0);
+      }
+    }
+  };
+
+  if (nsteps > 0) {
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int st = 0; st < nsteps; ++st) {
+      const bool more = st + 1 < nsteps;
+      if (more) gload(st + 1);
+      if (st < wsteps) compute(st & 1, st);
+      if (more) lstore((st + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- write: lane holds O^T rows 8j + 4*G2 + r (head_dim R*DU + u) of query column c ---------
+  if (i >= a.T) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_st;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int R = 8 * j + 4 * G2 + r;
+#pragma unroll
+      for (int u = 0; u < DU; ++u) Elem<IO>::store(op + R * DU + u, oacc[u][4 * j + r] * inv);
+    }
+}
+
+bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size) {
+  return kv_dtype == PA_DTYPE_BF16 && block_size == 16 && (head_dim == 64 || head_dim == 128);
+}
+
+int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len) {
+  return (int64_t)batch * num_heads * ((query_len + kWideRows - 1) / kWideRows);
+}
+
+int launch_prefill_wide(const AttnArgs& a, int io_dtype, hipStream_t stream) {
+  const int64_t units = prefill_wide_units(a.B, a.H, a.T);
+  if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
+  const dim3 grid((unsigned)units), block(kWideWaves * kWave);
+  if (io_dtype == PA_DTYPE_F32) {
+    if (a.head_dim == 64) prefill_wide_kernel<float, 64><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<float, 128><<<grid, block, 0, stream>>>(a);
+  } else {
+    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
+  }
+  PA_CHECK_LAUNCH("wide prefill kernel");
+  return PA_OK;
+}
+
+}  // namespace pa

@@ -55,8 +55,10 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _i64, _i32,
          _c_void_p, _c_void_p,
          _i32, _i32, _i32, _i32, _i32,
-         _f32, _c_void_p],
+         _f32, _i32,  # scale, split_blocks
+         _c_void_p, _size_t, _c_void_p],  # workspace, bytes, stream
     ),
+    "pa_prefill_workspace_size": (_size_t, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "pa_kv_append": (
         _int,
         [_c_void_p, _c_void_p, _i64, _i64, _i64, _int,

@@ -46,6 +46,7 @@ def cu_count(device: torch.device) -> int:
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The device's split-K partial-result workspace, at least `nbytes` long."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     ws = _workspaces.get(idx)
     if ws is None or ws.numel() < nbytes:
@@ -64,6 +65,15 @@ def default_split_blocks(batch: int, num_heads: int, max_pages: int, device: tor
     splits = math.ceil(target / units)
     blocks = max(16, math.ceil(max_pages / splits))
     return 0 if blocks >= max_pages else blocks
+
+
+def default_prefill_split_blocks(batch: int, num_heads: int, query_len: int, max_pages: int,
+                                 device: torch.device) -> int:
+    """KV blocks per prefill split-K workgroup. Always 0: measured on MI355X, the second (merge)
+    launch costs more than the load balance it buys, from the chunked-prefill workload (4 x 8
+    heads, 16-row tiles over up to 58 blocks: 24.5 us unsplit, 32-95 us split) up to 8 x 32
+    heads with 512-token chunks. Callers may still pass split_blocks explicitly."""
+    return 0
 
 
 def _check_pool(name: str, k_pool: torch.Tensor, v_pool: torch.Tensor) -> None:
@@ -134,9 +144,11 @@ def paged_attention_prefill_hip(
     seq_lens: torch.Tensor,
     current_lengths: torch.Tensor,
     *,
+    split_blocks: int | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Chunked causal prefill attention for q [B, H, T, Hd]; returns a tensor shaped like q."""
+    """Chunked causal prefill attention for q [B, H, T, Hd]; returns a tensor shaped like q.
+    split_blocks: KV blocks per split-K workgroup (0: none; None: default_prefill_split_blocks)."""
     _require_gpu("paged_attention_prefill_hip", q, k_pool, v_pool, page_table, seq_lens, current_lengths)
     _check_pool("paged_attention_prefill_hip", k_pool, v_pool)
     B, H, T, Hd = q.shape
@@ -152,7 +164,11 @@ def paged_attention_prefill_hip(
         out = torch.empty_like(q)
     max_pages = page_table.shape[1] if page_table.dim() == 2 else 0
     pt_stride = page_table.stride(0) if page_table.dim() == 2 and B > 0 else max_pages
+    if split_blocks is None:
+        split_blocks = default_prefill_split_blocks(B, H, T, max_pages, q.device)
     lib = _lib.load()
+    ws_bytes = lib.pa_prefill_workspace_size(B, H, T, Hd, max_pages, split_blocks) if bs == 16 else 0
+    ws_ptr = _workspace(q.device, ws_bytes).data_ptr() if ws_bytes else None
     status = lib.pa_prefill(
         q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _lib.dtype_code(q.dtype),
@@ -160,7 +176,8 @@ def paged_attention_prefill_hip(
         page_table.data_ptr() if max_pages else None, pt_stride, max_pages,
         seq_lens.data_ptr(), current_lengths.data_ptr(),
         B, H, T, Hd, bs,
-        1.0 / math.sqrt(Hd), _stream_ptr(q.device),
+        1.0 / math.sqrt(Hd), split_blocks,
+        ws_ptr, ws_bytes, _stream_ptr(q.device),
     )
     _lib.check(status, "pa_prefill")
     return out

@@ -35,8 +35,8 @@ import torch
 from src.cache.paged_kv import BatchedPagedKVCache
 from src.kernels import _lib
 from src.kernels.hip_paged_attention import (
-    _workspace, default_split_blocks, kv_append_hip, pack_metadata_hip, paged_attention_decode_hip,
-    paged_attention_prefill_hip)
+    _workspace, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
+    pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
 from src.kernels.staging import upload
 
 T_BUCKETS = (16, 32, 64, 128, 256)
@@ -96,8 +96,13 @@ class _Captured:
         self.pos = torch.zeros((B,), dtype=torch.long, device=device)
         self.cur = torch.ones((B,), dtype=torch.int32, device=device)
         self.csr = torch.zeros((3 * B + 1 + B * pages,), dtype=torch.int32, device=device)
-        self.split_blocks = default_split_blocks(B, H, pages, device) if Tb == 1 else 0
-        ws_bytes = _lib.load().pa_decode_workspace_size(B, H, Hd, pages, self.split_blocks) if Tb == 1 else 0
+        lib = _lib.load()
+        if Tb == 1:
+            self.split_blocks = default_split_blocks(B, H, pages, device)
+            ws_bytes = lib.pa_decode_workspace_size(B, H, Hd, pages, self.split_blocks)
+        else:
+            self.split_blocks = default_prefill_split_blocks(B, H, Tb, pages, device)
+            ws_bytes = lib.pa_prefill_workspace_size(B, H, Tb, Hd, pages, self.split_blocks)
         # Allocated outside the capture and referenced here, so the address the graph records
         # stays valid for the graph's lifetime.
         self.ws = _workspace(device, ws_bytes) if ws_bytes else None
@@ -150,7 +155,8 @@ class GraphedStep:
             if Tb == 1:
                 o = paged_attention_decode_hip(q, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
             else:
-                o = paged_attention_prefill_hip(q, k_pool, v_pool, pt, seq32, cap.cur)
+                o = paged_attention_prefill_hip(q, k_pool, v_pool, pt, seq32, cap.cur,
+                                                split_blocks=cap.split_blocks)
             x = x + a.out_proj(a._merge_heads(o))
             x = x + blk.mlp(blk.ln2(x))
         return m.lm_head(m.ln_f(x))

@@ -9,6 +9,9 @@
   large_decode    256 requests, 32 heads x 128, lengths log-uniform in [512, 32768] (request b
                   drawn from seed + b), pool = ceil(1.1 * blocks needed), shuffled block lists;
                   bf16 KV (N(0,1) drawn in fp32, rounded to nearest even), fp32 q.
+  large_prefill   8 requests, 32 heads x 128, cached context uniform in [1024, 4096] aligned to 16
+                  plus a new 512-token chunk already in the cache; pool = ceil(1.1 * blocks
+                  needed), shuffled block lists; bf16 KV, fp32 q (the MFMA-utilisation workload).
 Q, K and V are i.i.d. N(0, 1). Block lists are drawn on the host with torch.Generator; pool
 contents are drawn on the target device. Each workload also carries its algorithmic HBM bytes:
 K and V rows read, q read and output written (fp32), page-table entries and two int32 lengths.
@@ -179,3 +182,29 @@ def chunked_prefill(seed: int = 0, device="cpu", batch: int = 4, heads: int = 8,
 def prefill_flops(prev_lens: list[int], chunk_lens: list[int], heads: int, head_dim: int) -> int:
     """Useful FLOPs of causal chunked prefill (QK^T and PV over attended keys of real rows)."""
     return sum(4 * heads * head_dim * (c * c0 + c * (c + 1) // 2) for c0, c in zip(prev_lens, chunk_lens))
+
+
+def large_prefill(seed: int = 0, device="cpu", batch: int = 8, heads: int = 32, head_dim: int = 128,
+                  chunk: int = 512, ctx_lo: int = 1024, ctx_hi: int = 4096,
+                  kv_dtype: torch.dtype = torch.bfloat16) -> PagedBatch:
+    """Chunked prefill after the chunk's append: seq_lens = context + chunk, cur_lens = chunk."""
+    g = torch.Generator().manual_seed(seed + 300007)
+    ctx = [BLOCK * int(x) for x in torch.randint(ctx_lo // BLOCK, ctx_hi // BLOCK + 1, (batch,), generator=g).tolist()]
+    lens = [c0 + chunk for c0 in ctx]
+    need = sum(math.ceil(L / BLOCK) for L in lens)
+    pool_blocks = math.ceil(1.1 * need)
+    perm = torch.randperm(pool_blocks, generator=g).tolist()
+    lists, pos = [], 0
+    for L in lens:
+        n = math.ceil(L / BLOCK)
+        lists.append(perm[pos:pos + n])
+        pos += n
+    dg = _device_gen(device, seed + 400009)
+    q = torch.empty(batch, heads, chunk, head_dim, device=device)
+    k = torch.empty(pool_blocks, heads, BLOCK, head_dim, device=device, dtype=kv_dtype)
+    v = torch.empty_like(k)
+    for t in (q, k, v):
+        _fill_normal(t, dg)
+    b = _batch(q, k, v, lists, lens, [chunk] * batch, device)
+    b.extra["prev_lens"] = ctx
+    return b

@@ -67,8 +67,8 @@ const char* pa_last_error_message(void);
  * blocks between them and merge their online-softmax states in LDS. When split_blocks > 0 and a
  * request has more than split_blocks KV blocks, its blocks are also divided among several
  * workgroups whose partial results are merged by a second kernel; that path needs a workspace of
- * pa_decode_workspace_size() bytes (no zeroing needed). split_blocks <= 0 means one workgroup per
- * (request, head) and no workspace.
+ * pa_decode_workspace_size() bytes (no initialisation needed). split_blocks <= 0 means one
+ * workgroup per (request, head) and no workspace.
  *
  * order: optional int32 [B] permutation giving the processing order of requests (e.g. longest
  * first, for load balance); NULL means 0..B-1. Results do not depend on it.
@@ -83,7 +83,8 @@ int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
               void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of workspace pa_decode needs for these sizes (0 when split_blocks <= 0 or no request can
- * need more than one split). No reference counterpart: the Triton decode path has no split-K. */
+ * need more than one split). No reference counterpart: the Triton decode path has no split-K.
+ * Calls that share a workspace must not run concurrently (e.g. on different streams). */
 size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                 int32_t max_pages, int32_t split_blocks);
 
@@ -93,6 +94,10 @@ size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_d
  * (src/kernels/triton_paged_attention.py:220-258) behind paged_attention()
  * (src/kernels/paged_attention.py:44-51). fp32 KV uses fp32 MFMA (16x16x4); bf16 KV uses bf16
  * MFMA with fp32 accumulation (q and the softmax weights are rounded to bf16 for the products).
+ * Work is one workgroup per (request, head, 16-row query tile); with split_blocks > 0 each tile's
+ * KV blocks are also cut into ranges of split_blocks blocks, one workgroup each, whose partial
+ * results a second kernel merges through a workspace of pa_prefill_workspace_size() bytes (no
+ * initialisation needed). split_blocks <= 0 means no split and no workspace.
  */
 int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
@@ -101,7 +106,13 @@ int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_
                const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
                const int32_t* seq_lens, const int32_t* cur_lens,
                int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
-               int32_t block_size, float scale, void* stream);
+               int32_t block_size, float scale, int32_t split_blocks,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace pa_prefill needs for these sizes (0 when no split applies). No reference
+ * counterpart: the Triton prefill path has no split-K. */
+size_t pa_prefill_workspace_size(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
+                                 int32_t max_pages, int32_t split_blocks);
 
 /*
  * KV append / scatter: writes k_new[b, :, j, :] and v_new[b, :, j, :] into pool slot

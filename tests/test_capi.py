@@ -32,7 +32,7 @@ def lib():
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
         "pa_decode", "pa_decode_workspace_size", "pa_kv_append", "pa_last_error_message",
-        "pa_pack_metadata", "pa_prefill", "pa_version", "pa_zero_blocks",
+        "pa_pack_metadata", "pa_prefill", "pa_prefill_workspace_size", "pa_version", "pa_zero_blocks",
     ])
 
 
@@ -51,6 +51,11 @@ def test_host_only_entry_points(lib):
     assert lib.pa_decode_workspace_size(8, 8, 64, 64, 0) == 0
     assert lib.pa_decode_workspace_size(8, 8, 64, 64, 16) == 8 * 8 * 4 * (64 + 2) * 4
     assert lib.pa_decode_workspace_size(8, 8, 64, 16, 16) == 0
+    # prefill: 4 requests x 8 heads x 16 tiles of 16 rows, 58 pages in splits of 16 -> 4 splits
+    assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 58, 0) == 0
+    assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 58, 16) == 4 * 8 * 16 * 4 * 16 * (64 + 2) * 4
+    assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 16, 16) == 0
+    assert lib.pa_prefill_workspace_size(4, 8, 256, 96, 58, 16) == 0  # no tuned kernel: no split
 
 
 def test_argument_errors_are_reported_without_a_device(lib):
@@ -63,4 +68,4 @@ def test_argument_errors_are_reported_without_a_device(lib):
     assert st == _lib.PA_ERR_INVALID_ARGUMENT
     # zero-sized work is a no-op success
     assert lib.pa_prefill(None, 0, 0, 0, None, 0, 0, 0, 0, None, None, 0, 0, None, 0, 0, None, None,
-                          0, 8, 4, 64, 16, 1.0, None) == _lib.PA_OK
+                          0, 8, 4, 64, 16, 1.0, 0, None, 0, None) == _lib.PA_OK

@@ -92,6 +92,8 @@ def test_split_path_matches_oracle_and_unsplit(device, split_blocks):
     got = run(b, split_blocks=split_blocks)
     assert max_err(got, oracle_out(b)) <= 1e-4
     assert max_err(got, run(b, split_blocks=0).cpu().numpy()) <= 1e-5
+    # the merge order is fixed, so a second call reproduces the first bit for bit
+    assert torch.equal(got, run(b, split_blocks=split_blocks))
 
 
 @pytest.mark.parametrize("Hd,bs", [(16, 8), (32, 16), (96, 16), (64, 32), (80, 4)])

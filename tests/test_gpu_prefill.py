@@ -40,8 +40,8 @@ def make_prefill(device, seed, ctx, curs, T, H, Hd, bs=16, kv_dtype=torch.float3
     return workloads._batch(q, k, v, lists, lens, list(curs), device)
 
 
-def run(b):
-    return paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+def run(b, **kw):
+    return paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t, **kw)
 
 
 def oracle_out(b):
@@ -128,3 +128,108 @@ def test_prefill_strided_views_and_tiles(device):
     want = oracle.paged_attention(q.cpu().contiguous(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists, b.seq_lens,
                                   b.cur_lens)
     assert max_err(out, want) <= 1e-4
+
+
+@pytest.mark.parametrize("kv_dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("split_blocks", [1, 3, 16])
+def test_prefill_split_k(device, kv_dtype, tol, head_dim, split_blocks):
+    """Split-K prefill (splits, then the merge kernel) against the oracle and the unsplit kernel,
+    with tiles whose block count is below, at and above the split size, an empty request and
+    padded rows; a second call must reproduce the first bit for bit (fixed merge order)."""
+    ctx = [0, 16, 300, 7, 600, 0]
+    curs = [40, 33, 1, 17, 0, 0]
+    T = 40
+    b = make_prefill(device, 26, ctx, curs, T=T, H=3, Hd=head_dim, kv_dtype=kv_dtype)
+    print(f"split prefill kv={kv_dtype} hd={head_dim} split_blocks={split_blocks}", flush=True)
+    got = run(b, split_blocks=split_blocks)
+    err = max_err(got, oracle_out(b))
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= tol
+    # bf16 KV rounds the softmax weights relative to the running max, which depends on the split
+    assert float((got - run(b, split_blocks=0)).abs().max()) <= (1e-5 if kv_dtype == torch.float32 else 5e-3)
+    assert torch.equal(got, run(b, split_blocks=split_blocks))
+
+
+def test_prefill_split_then_other_shapes_share_the_workspace(device):
+    """Split calls of different shapes and kinds in sequence share one workspace."""
+    b1 = make_prefill(device, 27, [500, 200, 37], [64, 64, 5], T=64, H=8, Hd=64)
+    b2 = make_prefill(device, 28, [900], [16], T=16, H=2, Hd=128)
+    want1, want2 = oracle_out(b1), oracle_out(b2)
+    for _ in range(2):
+        assert max_err(run(b1, split_blocks=4), want1) <= 1e-4
+        dec = paged_attention_decode_hip(b1.q[:, :, -1:].contiguous(), b1.k_pool, b1.v_pool, b1.page_table,
+                                         b1.seq_lens_t, torch.ones_like(b1.cur_lens_t), split_blocks=2)
+        # every request's last row attends all of its keys, as the decode row does
+        assert float((dec - run(b1, split_blocks=0)[:, :, -1:]).abs().max()) <= 1e-5
+        assert max_err(run(b2, split_blocks=5), want2) <= 1e-4
+
+
+# ---- wide-tile bf16 kernel (128 query rows per workgroup, KV staged through LDS) -------------
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
+def test_wide_prefill_forced_small(device, monkeypatch, head_dim, io_dtype):
+    """The wide kernel on ragged requests: contexts 0 / unaligned / long, chunk rows padded
+    (C < T), T not a multiple of 128 nor of 32, an empty request; against the oracle on the same
+    bf16 KV and against the 16-row kernel."""
+    ctx = [0, 37, 700, 16, 0, 1200]
+    curs = [150, 150, 3, 90, 0, 150]
+    T = 150
+    b = make_prefill(device, 31, ctx, curs, T=T, H=3, Hd=head_dim, kv_dtype=torch.bfloat16)
+    q = b.q.to(io_dtype)
+    print(f"wide prefill hd={head_dim} io={io_dtype}", flush=True)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "wide")
+    got = paged_attention_prefill_hip(q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "tile")
+    tile = paged_attention_prefill_hip(q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    want = oracle.paged_attention(q.float().cpu(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists, b.seq_lens,
+                                  b.cur_lens, nthreads=NTHREADS)
+    err = max_err(got, want)
+    print(f"  max err vs oracle {err:.2e}, vs 16-row kernel {float((got - tile).abs().max()):.2e}", flush=True)
+    tol = 2e-2 if io_dtype == torch.float32 else 3e-2  # bf16 output adds one rounding
+    assert err <= tol
+    assert float((got.float() - tile.float()).abs().max()) <= (5e-3 if io_dtype == torch.float32 else 2e-2)
+
+
+def test_wide_prefill_negative_pages_and_strided_views(device, monkeypatch):
+    """A -1 page entry skips its 16 keys in the wide kernel as in the 16-row kernel; q/out are
+    the model's transposed views; the untouched request matches the oracle."""
+    B, H, T, Hd = 2, 4, 96, 128
+    b = make_prefill(device, 32, [300, 40], [96, 96], T=T, H=H, Hd=Hd, kv_dtype=torch.bfloat16)
+    pt = b.page_table.clone()
+    pt[0, 3] = -1
+    x = torch.randn(B, T, H * Hd, device=device)
+    q = x.view(B, T, H, Hd).transpose(1, 2)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "wide")
+    got = paged_attention_prefill_hip(q, b.k_pool, b.v_pool, pt, b.seq_lens_t, b.cur_lens_t)
+    assert got.stride() == q.stride()
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "tile")
+    tile = paged_attention_prefill_hip(q, b.k_pool, b.v_pool, pt, b.seq_lens_t, b.cur_lens_t)
+    full = paged_attention_prefill_hip(q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    assert float((got - tile).abs().max()) <= 5e-3
+    assert float((got[0] - full[0]).abs().max()) > 1e-2  # the skipped keys did matter
+    want = oracle.paged_attention(q[1:].cpu().contiguous(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists[1:],
+                                  b.seq_lens[1:], b.cur_lens[1:], nthreads=NTHREADS)
+    assert max_err(got[1:], want) <= 2e-2
+
+
+def test_large_prefill_sampled_parity(device):
+    """The MFMA-utilisation workload at full size (8 requests x 32 heads x 128, chunk 512 over
+    1-4k contexts, bf16 KV) through the default dispatch (the wide kernel at this size); two
+    requests x four heads are checked against the oracle on the same bf16 values."""
+    from src.kernels.hip_paged_attention import cu_count
+    b = workloads.large_prefill(seed=0, device=device)
+    print(f"large prefill ctx={b.extra['prev_lens']}", flush=True)
+    out = paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    assert 8 * 32 * 4 >= 2 * cu_count(device)  # the wide kernel's grid rule holds at this size
+    for r in (0, 5):
+        ids = torch.tensor(b.block_lists[r], device=device, dtype=torch.long)
+        k = b.k_pool.index_select(0, ids)[:, :4].contiguous().cpu()
+        v = b.v_pool.index_select(0, ids)[:, :4].contiguous().cpu()
+        lists = [list(range(len(b.block_lists[r])))]
+        want = oracle.paged_attention(b.q[r:r + 1, :4].cpu(), k, v, lists, [b.seq_lens[r]], [b.cur_lens[r]],
+                                      nthreads=NTHREADS)
+        err = max_err(out[r:r + 1, :4], want)
+        print(f"  request {r}: max err {err:.2e}", flush=True)
+        assert err <= 2e-2
