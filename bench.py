@@ -14,8 +14,10 @@ Also reported on the same line:
   cpu_baseline   the oracle (C restatement of the reference's paged attention, fp64
                  accumulation) over the same batch on this host's cores, plus the rate of the
                  reference's own per-token torch loop on a small slice of it;
-  secondary      the ragged fp32 decode (8 requests x 6 layers) and the chunked prefill (4 requests,
-                 fp32 and bf16 KV; MFMA utilisation against the fp32 / bf16 matrix peaks);
+  secondary      the ragged fp32 decode (8 requests x 6 layers), the chunked prefill (4 requests,
+                 fp32 and bf16 KV) and the large prefill (8 requests x 32 heads x 128, 512-token
+                 chunks over 1-4k contexts, bf16 and fp32 KV); MFMA utilisation against the fp32 /
+                 bf16 matrix peaks;
   continuous_batching  the end-to-end run: decoder LM (vocab 5000, d_model 512, 8 heads,
                  6 layers, d_ff 2048, KV block 16, fp32, weights N(0, 0.02)), 200 Poisson requests
                  at 32 req/s, max batch 8, prefill chunk 256, 1536-token iteration budget, greedy;
@@ -217,6 +219,23 @@ def secondary_workloads(device, steps: int) -> dict:
             "useful_gflop": round(flops / 1e9, 4), "TFLOPs": round(tfs, 2),
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
         }
+    for kv_dtype, tag in ((torch.bfloat16, "bf16kv"), (torch.float32, "fp32")):
+        b = workloads.large_prefill(seed=0, device=device, kv_dtype=kv_dtype)
+        H, Hd = b.q.shape[1], b.q.shape[3]
+        flops = workloads.prefill_flops(b.extra["prev_lens"], b.cur_lens, H, Hd)
+        ms = time_call(lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t,
+                                                           b.cur_lens_t), max(3, steps // 2))
+        peak = 157.3 if tag == "fp32" else 2500.0
+        tfs = flops / (ms * 1e-3) / 1e12
+        res[f"large_prefill_{tag}"] = {
+            "workload": f"{b.batch} requests, {H} heads x {Hd}, context {b.extra['prev_lens']} + chunk 512 each, "
+                        f"{'bf16' if tag == 'bf16kv' else 'fp32'} KV, fp32 q/out"
+                        + (" (wide-tile kernel: 128 query rows per workgroup)" if tag == "bf16kv" else ""),
+            "attention_us": round(1e3 * ms, 1), "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1),
+            "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
+        }
+        del b
+        torch.cuda.empty_cache()
     return res
 
 
@@ -396,7 +415,7 @@ def main() -> int:
     if args.calibrate_copy:
         calibration_copy(dev)
     if not args.no_secondary:
-        log("secondary workloads (ragged fp32 decode, chunked prefill)")
+        log("secondary workloads (ragged fp32 decode, chunked prefill, large prefill)")
         result["secondary"] = secondary_workloads(dev, args.steps)
     if not args.no_e2e:
         log("end-to-end continuous batching (200 requests, 32 req/s)")

@@ -1,0 +1,251 @@
+// Small-M fp32 linear layers for the decode step of the paged-attention model (gfx950).
+//
+// A decode step multiplies at most 16 token rows by each weight matrix, so the work is a stream
+// of the weights (N x K fp32) against a few rows of activations. Library GEMMs tile such shapes
+// into a few tens of workgroups; here one workgroup of 8 wavefronts owns a 16-column tile of the
+// output, its wavefronts split K eight ways, and each wavefront accumulates the 16 (rows) x 16
+// (columns) tile with v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation) over its K
+// range; the eight partial tiles are summed in LDS and the epilogue is applied once.
+//   A (16 x 4): lane (G, c) holds x[row c][k(G, s)]     (rows >= M are zero)
+//   B (4 x 16): lane (G, c) holds W[col n0 + c][k(G, s)] (torch Linear weight, row-major [N, K])
+// with the contraction slot of MFMA s mapped to k(G, s) = k_wave + G*KL + s, so every lane reads
+// KL contiguous floats of one activation row and of one weight row (16-byte loads).
+// Fusions:
+//   prologue  LayerNorm of the activation rows (biased variance, like torch.nn.LayerNorm);
+//   epilogue  bias, exact (erf) GELU, residual add; or, for the K/V projections, a scatter of
+//             each row's head_dim vectors into its KV-pool slot (the append of the decode step).
+#include <math.h>
+
+#include "pa_common.h"
+
+namespace pa {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLinWaves = 8;
+constexpr int kLinRows = 16;  // maximum activation rows (MFMA tile height)
+
+struct LinArgs {
+  const float* x;
+  int64_t x_stride;
+  int32_t M, K;
+  const float* ln_w;  // null: no LayerNorm
+  const float* ln_b;
+  float ln_eps;
+  const float* w[3];  // segment weights, each [seg_n, K]
+  const float* b[3];  // segment biases (null: none)
+  int32_t seg_n, nseg;
+  int32_t act;        // 0 none, 1 GELU (erf)
+  const float* res;   // residual rows (null: none), same columns as out
+  int64_t res_stride;
+  float* out;         // segment 0's rows (and all segments' when there is no pool)
+  int64_t out_stride;
+  void* k_pool;       // when set: segments 1 and 2 are scattered into the K / V pools
+  void* v_pool;
+  int32_t pool_bf16;
+  int64_t num_blocks;
+  const int32_t* slots;  // per row: block * block_size + offset, < 0 = skip
+  int32_t H, Hd, bs;
+};
+
+template <int K>
+__global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const LinArgs a) {
+  constexpr int KW = K / kLinWaves;  // K range of one wavefront
+  constexpr int KL = KW / 4;         // contiguous k values per lane
+  static_assert(KL % 4 == 0, "16-byte loads");
+
+  __shared__ float sm_part[kLinWaves][16][17];
+  __shared__ float sm_mean[kLinRows];
+  __shared__ float sm_rstd[kLinRows];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int G = lane >> 4;
+  const int c = lane & 15;
+
+  const int tiles_per_seg = (a.seg_n + 15) / 16;
+  const int seg = blockIdx.x / tiles_per_seg;
+  const int n0 = (blockIdx.x - seg * tiles_per_seg) * 16;
+  const float* W = a.w[seg];
+
+  // ---- LayerNorm statistics of the activation rows (two rows per wavefront) -----------------
+  if (a.ln_w != nullptr) {
+    constexpr int PL = K / kWave;  // values per lane of one row (lane + 64e)
+    for (int r = w; r < kLinRows; r += kLinWaves) {
+      if (r >= a.M) break;
+      const float* xr = a.x + (int64_t)r * a.x_stride + lane;
+      float v[PL];
+#pragma unroll
+      for (int e = 0; e < PL; ++e) v[e] = xr[e * kWave];
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < PL; ++e) s += v[e];
+      const float mean = wave_sum(s) / K;
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < PL; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
+      const float var = wave_sum(q) / K;
+      if (lane == 0) {
+        sm_mean[r] = mean;
+        sm_rstd[r] = 1.f / sqrtf(var + a.ln_eps);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- operands: this lane's activation row c and weight row n0 + c over k(G, 0..KL) --------
+  const int kb = w * KW + G * KL;
+  float xa[KL], wb[KL];
+  if (c < a.M) {
+    const float* xr = a.x + (int64_t)c * a.x_stride + kb;
+#pragma unroll
+    for (int e = 0; e < KL; e += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(xr + e);
+      xa[e] = t[0]; xa[e + 1] = t[1]; xa[e + 2] = t[2]; xa[e + 3] = t[3];
+    }
+    if (a.ln_w != nullptr) {
+      const float mean = sm_mean[c], rstd = sm_rstd[c];
+#pragma unroll
+      for (int e = 0; e < KL; e += 4) {
+        const f32x4 g = *reinterpret_cast<const f32x4*>(a.ln_w + kb + e);
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(a.ln_b + kb + e);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xa[e + q] = fmaf((xa[e + q] - mean) * rstd, g[q], bb[q]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < KL; ++e) xa[e] = 0.f;
+  }
+  {
+    const int n = n0 + c < a.seg_n ? n0 + c : a.seg_n - 1;  // clamp: the column is discarded
+    const float* wr = W + (int64_t)n * a.K + kb;
+#pragma unroll
+    for (int e = 0; e < KL; e += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(wr + e);
+      wb[e] = t[0]; wb[e + 1] = t[1]; wb[e + 2] = t[2]; wb[e + 3] = t[3];
+    }
+  }
+
+  // ---- D[m][n] += x[m][k] W[n][k] over this wavefront's K range (4 independent chains) ---------
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KL; ++s) acc[s & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s], wb[s], acc[s & 3], 0, 0, 0);
+  const f32x4 d = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  // lane (G, c) holds D[4G + i][c]: rows 4G..4G+3 of output column n0 + c
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sm_part[w][4 * G + i][c] = d[i];
+  __syncthreads();
+
+  // ---- epilogue: one thread per (row, column) of the tile --------------------------------------
+  if (threadIdx.x >= 256) return;
+  const int m = threadIdx.x >> 4;
+  const int cc = threadIdx.x & 15;
+  const int n = n0 + cc;
+  if (m >= a.M || n >= a.seg_n) return;
+  float v = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < kLinWaves; ++ww) v += sm_part[ww][m][cc];
+  if (a.b[seg] != nullptr) v += a.b[seg][n];
+  if (a.act == 1) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+  if (a.k_pool != nullptr && seg > 0) {
+    const int slot = a.slots[m];
+    const int64_t blk = slot >= 0 ? slot / a.bs : -1;
+    if (blk < 0 || blk >= a.num_blocks) return;
+    const int h = n / a.Hd, dd = n - h * a.Hd;
+    const int64_t off = ((blk * a.H + h) * a.bs + (slot - blk * a.bs)) * a.Hd + dd;
+    void* pool = seg == 1 ? a.k_pool : a.v_pool;
+    if (a.pool_bf16)
+      static_cast<uint16_t*>(pool)[off] = f32_to_bf16(v);
+    else
+      static_cast<float*>(pool)[off] = v;
+    return;
+  }
+  if (a.res != nullptr) v += a.res[(int64_t)m * a.res_stride + seg * a.seg_n + n];
+  a.out[(int64_t)m * a.out_stride + seg * a.seg_n + n] = v;
+}
+
+static bool small_linear_k_supported(int32_t K) {
+  return K == 128 || K == 256 || K == 512 || K == 1024 || K == 2048;
+}
+
+static int launch_small_linear(const LinArgs& a, hipStream_t stream) {
+  const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + 15) / 16);
+  if (tiles > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
+  const dim3 grid((unsigned)tiles), block(kLinWaves * kWave);
+  switch (a.K) {
+    case 128: small_linear_kernel<128><<<grid, block, 0, stream>>>(a); break;
+    case 256: small_linear_kernel<256><<<grid, block, 0, stream>>>(a); break;
+    case 512: small_linear_kernel<512><<<grid, block, 0, stream>>>(a); break;
+    case 1024: small_linear_kernel<1024><<<grid, block, 0, stream>>>(a); break;
+    case 2048: small_linear_kernel<2048><<<grid, block, 0, stream>>>(a); break;
+    default: PA_FAIL(PA_ERR_UNSUPPORTED, "small linear: in_features must be 128, 256, 512, 1024 or 2048, got %d", a.K);
+  }
+  PA_CHECK_LAUNCH("small linear kernel");
+  return PA_OK;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" int pa_linear_rows(const float* x, int64_t x_stride, int32_t rows, int32_t in_features,
+                              const float* weight, const float* bias, int32_t out_features,
+                              const float* ln_weight, const float* ln_bias, float ln_eps,
+                              int32_t activation, const float* residual, int64_t residual_stride,
+                              float* out, int64_t out_stride, void* stream) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(rows >= 0 && rows <= kLinRows, "rows must be in [0, %d], got %d", kLinRows, rows);
+  PA_CHECK_ARG(out_features > 0 && in_features > 0, "bad sizes: in=%d out=%d", in_features, out_features);
+  PA_CHECK_ARG(activation == 0 || activation == 1, "bad activation %d", activation);
+  if (rows == 0) return PA_OK;
+  PA_CHECK_ARG(x && weight && out, "null x/weight/out");
+  PA_CHECK_ARG((ln_weight == nullptr) == (ln_bias == nullptr), "LayerNorm needs both weight and bias");
+  PA_CHECK_ARG(aligned16(x) && aligned16(weight) && x_stride % 4 == 0 && (!ln_weight || (aligned16(ln_weight) &&
+               aligned16(ln_bias))), "x, weight and LayerNorm parameters must be 16-byte aligned with x_stride % 4 == 0");
+  PA_CHECK_ARG(x_stride >= in_features && out_stride >= out_features &&
+               (residual == nullptr || residual_stride >= out_features), "row strides smaller than the rows");
+  LinArgs a{};
+  a.x = x; a.x_stride = x_stride; a.M = rows; a.K = in_features;
+  a.ln_w = ln_weight; a.ln_b = ln_bias; a.ln_eps = ln_eps;
+  a.w[0] = weight; a.b[0] = bias; a.seg_n = out_features; a.nseg = 1;
+  a.act = activation; a.res = residual; a.res_stride = residual_stride;
+  a.out = out; a.out_stride = out_stride;
+  return launch_small_linear(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int32_t d_model,
+                             const float* ln_weight, const float* ln_bias, float ln_eps,
+                             const float* wq, const float* bq, const float* wk, const float* bk,
+                             const float* wv, const float* bv,
+                             float* q_out, int64_t q_stride,
+                             void* k_pool, void* v_pool, int pool_dtype, int64_t num_blocks,
+                             const int32_t* slot_mapping, int32_t num_heads, int32_t head_dim,
+                             int32_t block_size, void* stream) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(rows >= 0 && rows <= kLinRows, "rows must be in [0, %d], got %d", kLinRows, rows);
+  PA_CHECK_ARG(num_heads > 0 && head_dim > 0 && block_size > 0 && d_model == num_heads * head_dim,
+               "d_model must equal num_heads * head_dim");
+  PA_CHECK_ARG(pool_dtype == PA_DTYPE_F32 || pool_dtype == PA_DTYPE_BF16, "bad pool dtype %d", pool_dtype);
+  if (rows == 0) return PA_OK;
+  PA_CHECK_ARG(x && wq && wk && wv && q_out && k_pool && v_pool && slot_mapping, "null pointer argument");
+  PA_CHECK_ARG((ln_weight == nullptr) == (ln_bias == nullptr), "LayerNorm needs both weight and bias");
+  PA_CHECK_ARG(aligned16(x) && aligned16(wq) && aligned16(wk) && aligned16(wv) && x_stride % 4 == 0 &&
+               (!ln_weight || (aligned16(ln_weight) && aligned16(ln_bias))),
+               "x, weights and LayerNorm parameters must be 16-byte aligned with x_stride % 4 == 0");
+  PA_CHECK_ARG(x_stride >= d_model && q_stride >= d_model, "row strides smaller than the rows");
+  LinArgs a{};
+  a.x = x; a.x_stride = x_stride; a.M = rows; a.K = d_model;
+  a.ln_w = ln_weight; a.ln_b = ln_bias; a.ln_eps = ln_eps;
+  a.w[0] = wq; a.w[1] = wk; a.w[2] = wv; a.b[0] = bq; a.b[1] = bk; a.b[2] = bv;
+  a.seg_n = d_model; a.nseg = 3;
+  a.act = 0; a.res = nullptr; a.res_stride = 0;
+  a.out = q_out; a.out_stride = q_stride;
+  a.k_pool = k_pool; a.v_pool = v_pool; a.pool_bf16 = pool_dtype == PA_DTYPE_BF16; a.num_blocks = num_blocks;
+  a.slots = slot_mapping; a.H = num_heads; a.Hd = head_dim; a.bs = block_size;
+  return launch_small_linear(a, static_cast<hipStream_t>(stream));
+}

@@ -72,6 +72,23 @@ SIGNATURES: dict[str, tuple] = {
          _i32, _i32, _i32, _i32,
          _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     ),
+    "pa_linear_rows": (
+        _int,
+        [_c_void_p, _i64, _i32, _i32,  # x, stride, rows, in_features
+         _c_void_p, _c_void_p, _i32,  # weight, bias, out_features
+         _c_void_p, _c_void_p, _f32,  # LayerNorm weight, bias, eps
+         _i32, _c_void_p, _i64,  # activation, residual, stride
+         _c_void_p, _i64, _c_void_p],  # out, stride, stream
+    ),
+    "pa_qkv_append": (
+        _int,
+        [_c_void_p, _i64, _i32, _i32,  # x, stride, rows, d_model
+         _c_void_p, _c_void_p, _f32,  # LayerNorm weight, bias, eps
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # wq, bq, wk, bk, wv, bv
+         _c_void_p, _i64,  # q_out, stride
+         _c_void_p, _c_void_p, _int, _i64,  # k pool, v pool, pool dtype, num_blocks
+         _c_void_p, _i32, _i32, _i32, _c_void_p],  # slots, heads, head_dim, block_size, stream
+    ),
     "pa_zero_blocks": (
         _int,
         [_c_void_p, _c_void_p, _int, _i64, _i32, _i32, _i32, _c_void_p, _i32, _c_void_p],

@@ -1,0 +1,106 @@
+"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32, <= 16 rows).
+
+  linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
+  qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
+                   one launch; returns q                                     (pa_qkv_append)
+
+They stand in for the nn.LayerNorm / nn.Linear / nn.GELU calls and the append of the
+reference's cached forward (src/model/transformer.py:30-35, src/model/attention.py:46-64) on
+one-token steps. All work is enqueued on torch's current stream; tensors must be on a HIP device.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from src.kernels import _lib
+
+MAX_ROWS = 16
+SUPPORTED_FEATURES = (128, 256, 512, 1024, 2048)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return t.data_ptr() if t is not None else None
+
+
+def _rows(x: torch.Tensor, name: str) -> None:
+    if not x.is_cuda or x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError(f"{name} must be a float32 [rows, features] tensor with unit column stride on a HIP device")
+
+
+def supported(linear: nn.Linear) -> bool:
+    return (linear.weight.dtype == torch.float32 and linear.weight.is_contiguous()
+            and linear.in_features in SUPPORTED_FEATURES)
+
+
+def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | None = None, gelu: bool = False,
+                    residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 16)."""
+    _rows(x, "x")
+    M, K = x.shape
+    if K != linear.in_features:
+        raise ValueError(f"x has {K} features, the layer takes {linear.in_features}")
+    N = linear.out_features
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    _rows(out, "out")
+    if residual is not None:
+        _rows(residual, "residual")
+    status = _lib.load().pa_linear_rows(
+        x.data_ptr(), x.stride(0), M, K,
+        linear.weight.data_ptr(), _ptr(linear.bias), N,
+        _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
+        float(ln.eps) if ln is not None else 0.0,
+        1 if gelu else 0, _ptr(residual), residual.stride(0) if residual is not None else 0,
+        out.data_ptr(), out.stride(0), _stream(x.device),
+    )
+    _lib.check(status, "pa_linear_rows")
+    return out
+
+
+def qkv_append_hip(x: torch.Tensor, ln: nn.LayerNorm, attn, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                   slot_mapping: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """q = LN(x) Wq^T + bq for the rows of x; the K and V rows go straight into their pool slots."""
+    _rows(x, "x")
+    M, D = x.shape
+    if out is None:
+        out = torch.empty((M, D), dtype=torch.float32, device=x.device)
+    nblk, H, bs, Hd = k_pool.shape
+    if slot_mapping.dtype != torch.int32 or slot_mapping.numel() < M:
+        raise ValueError("slot_mapping must be int32 with one entry per row")
+    status = _lib.load().pa_qkv_append(
+        x.data_ptr(), x.stride(0), M, D,
+        _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
+        float(ln.eps) if ln is not None else 0.0,
+        attn.q_proj.weight.data_ptr(), _ptr(attn.q_proj.bias), attn.k_proj.weight.data_ptr(), _ptr(attn.k_proj.bias),
+        attn.v_proj.weight.data_ptr(), _ptr(attn.v_proj.bias),
+        out.data_ptr(), out.stride(0),
+        k_pool.data_ptr(), v_pool.data_ptr(), _lib.dtype_code(k_pool.dtype), nblk,
+        slot_mapping.data_ptr(), H, Hd, bs, _stream(x.device),
+    )
+    _lib.check(status, "pa_qkv_append")
+    return out
+
+
+def model_supported(model) -> bool:
+    """True when every linear layer of the model's cached step fits the fused decode kernels."""
+    for blk in model.blocks:
+        a = blk.attn
+        fc1, act, fc2 = blk.mlp[0], blk.mlp[1], blk.mlp[2]
+        layers = (a.q_proj, a.k_proj, a.v_proj, a.out_proj, fc1, fc2)
+        if not all(supported(l) for l in layers):
+            return False
+        if not isinstance(act, nn.GELU) or act.approximate != "none":
+            return False
+        if not all(_ln_supported(n) for n in (blk.ln1, blk.ln2)):
+            return False
+    return supported(model.lm_head) and _ln_supported(model.ln_f)
+
+
+def _ln_supported(n) -> bool:
+    return (isinstance(n, nn.LayerNorm) and n.elementwise_affine and n.bias is not None
+            and n.weight.dtype == torch.float32 and tuple(n.normalized_shape) == (n.weight.numel(),))

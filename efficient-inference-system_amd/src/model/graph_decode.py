@@ -14,6 +14,12 @@ whole step once per (batch size, query-length bucket) and replays it:
                              kernel otherwise), output projection, MLP and residuals; final
                              LayerNorm and lm_head.
 
+One-token steps of up to 16 requests run the layers through the fused decode kernels
+(src/kernels/hip_linear.py) when the model's shapes allow: per layer one launch for LayerNorm +
+q/k/v projections + KV append, the decode attention, one for the output projection + residual,
+one for LayerNorm + fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. Set
+PAGED_HIP_FUSED_DECODE=0 to use the torch layers instead.
+
 Query lengths T > 1 are padded up to a bucket (16, 32, 64, 128, 256) with token id 0 and the
 logits of the real rows are returned. Padded rows are never appended to the cache (their slots
 are -1) and no real row reads them, so real rows are computed exactly as in eager mode; padded
@@ -33,7 +39,7 @@ import os
 import torch
 
 from src.cache.paged_kv import BatchedPagedKVCache
-from src.kernels import _lib
+from src.kernels import _lib, hip_linear
 from src.kernels.hip_paged_attention import (
     _workspace, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
     pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
@@ -44,6 +50,10 @@ T_BUCKETS = (16, 32, 64, 128, 256)
 
 def graphs_enabled() -> bool:
     return os.environ.get("PAGED_HIP_GRAPHS", "1") != "0"
+
+
+def fused_decode_enabled() -> bool:
+    return os.environ.get("PAGED_HIP_FUSED_DECODE", "1") != "0"
 
 
 def bucket_for(T: int) -> int | None:
@@ -106,6 +116,7 @@ class _Captured:
         # Allocated outside the capture and referenced here, so the address the graph records
         # stays valid for the graph's lifetime.
         self.ws = _workspace(device, ws_bytes) if ws_bytes else None
+        self.fused = Tb == 1 and B <= hip_linear.MAX_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
         self.signature = _signature(pools)
         self.graph = None
         self.logits = None
@@ -144,6 +155,8 @@ class GraphedStep:
         steps = torch.arange(Tb, device=cap.ids.device).view(1, Tb)
         positions = torch.clamp(cap.pos.view(B, 1) + steps, max=m.max_seq_len - 1)
         x = m.token_emb(cap.ids) + m.pos_emb(positions)
+        if cap.fused:
+            return self._fused_decode_layers(cap, pools, x.view(B, -1), pt, seq32, slots)
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
@@ -160,6 +173,22 @@ class GraphedStep:
             x = x + a.out_proj(a._merge_heads(o))
             x = x + blk.mlp(blk.ln2(x))
         return m.lm_head(m.ln_f(x))
+
+    def _fused_decode_layers(self, cap: _Captured, pools, x, pt, seq32, slots) -> torch.Tensor:
+        """The layers of a one-token step through the fused decode kernels; x is [B, d_model]."""
+        m = self.model
+        B = cap.B
+        for blk, pool in zip(m.blocks, pools):
+            k_pool, v_pool = _pool_tensors(pool)
+            a = blk.attn
+            q = hip_linear.qkv_append_hip(x, blk.ln1, a, k_pool, v_pool, slots)
+            q4 = q.view(B, 1, a.num_heads, a.head_dim).transpose(1, 2)
+            o = paged_attention_decode_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
+            x1 = hip_linear.linear_rows_hip(o.transpose(1, 2).reshape(B, a.d_model), a.out_proj, residual=x)
+            h = hip_linear.linear_rows_hip(x1, blk.mlp[0], ln=blk.ln2, gelu=True)
+            x = hip_linear.linear_rows_hip(h, blk.mlp[2], residual=x1)
+        logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
+        return logits.view(B, 1, -1)
 
     def _capture(self, cap: _Captured, pools) -> None:
         # Warm-up on a side stream (initialises library handles); it performs the same step the

@@ -155,6 +155,44 @@ int pa_zero_blocks(void* k_pool, void* v_pool, int pool_dtype, int64_t num_block
                    int32_t num_heads, int32_t block_size, int32_t head_dim,
                    const int32_t* block_ids, int32_t n_ids, void* stream);
 
+/*
+ * Decode-step linear layers of the model around the paged attention (fp32, at most 16 token rows).
+ * No reference counterpart as entry points: they replace the torch nn.Linear / nn.LayerNorm /
+ * nn.GELU calls of the reference's cached forward (src/model/transformer.py:30-35,
+ * src/model/attention.py:46-48,64) on one-token steps, where a step is a few rows against every
+ * weight matrix.
+ *
+ * pa_linear_rows: out[m, :] = act(LN(x[m, :]) W^T + bias) + residual[m, :] for m < rows (<= 16).
+ *   weight is torch's [out_features, in_features] row-major; in_features must be 128, 256, 512,
+ *   1024 or 2048;
+ *   ln_weight/ln_bias NULL skips the LayerNorm (biased variance, eps ln_eps, like
+ *   torch.nn.LayerNorm); bias and residual may be NULL; activation 0 = none, 1 = exact (erf)
+ *   GELU (torch.nn.GELU()). x, weight and LayerNorm parameters 16-byte aligned.
+ */
+int pa_linear_rows(const float* x, int64_t x_stride, int32_t rows, int32_t in_features,
+                   const float* weight, const float* bias, int32_t out_features,
+                   const float* ln_weight, const float* ln_bias, float ln_eps,
+                   int32_t activation, const float* residual, int64_t residual_stride,
+                   float* out, int64_t out_stride, void* stream);
+
+/*
+ * pa_qkv_append: the three projections of a cached attention layer in one launch, with the
+ * LayerNorm before them and the KV append after them: q_out[m, :] = LN(x[m, :]) wq^T + bq, and
+ * the rows LN(x[m, :]) wk^T + bk and LN(x[m, :]) wv^T + bv are written, split into num_heads
+ * vectors of head_dim, into pool slot slot_mapping[m] of the K and V pools (converted to the pool
+ * dtype; slot < 0 or a block outside [0, num_blocks) skips the row). Replaces
+ * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 16 and
+ * d_model in {128, 256, 512, 1024, 2048}.
+ */
+int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int32_t d_model,
+                  const float* ln_weight, const float* ln_bias, float ln_eps,
+                  const float* wq, const float* bq, const float* wk, const float* bk,
+                  const float* wv, const float* bv,
+                  float* q_out, int64_t q_stride,
+                  void* k_pool, void* v_pool, int pool_dtype, int64_t num_blocks,
+                  const int32_t* slot_mapping, int32_t num_heads, int32_t head_dim,
+                  int32_t block_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

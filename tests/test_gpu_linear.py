@@ -1,0 +1,113 @@
+"""Decode-step linear kernels (pa_linear_rows, pa_qkv_append) against float64 torch on the CPU:
+LayerNorm prologue, bias / GELU / residual epilogues, every supported in_features, ragged
+out_features, 1..16 rows, and the K/V scatter into fp32 and bf16 pools (bit-exact placement,
+skipped slots untouched)."""
+import pytest
+import torch
+import torch.nn as nn
+
+from src.kernels import hip_linear
+
+pytestmark = pytest.mark.gpu
+
+
+def ref_linear(x, lin, ln=None, gelu=False, residual=None):
+    x = x.double().cpu()
+    if ln is not None:
+        x = nn.functional.layer_norm(x, (x.shape[1],), ln.weight.double().cpu(), ln.bias.double().cpu(), ln.eps)
+    y = x @ lin.weight.double().cpu().t()
+    if lin.bias is not None:
+        y = y + lin.bias.double().cpu()
+    if gelu:
+        y = nn.functional.gelu(y)
+    if residual is not None:
+        y = y + residual.double().cpu()
+    return y
+
+
+@pytest.mark.parametrize("K", [128, 256, 512, 1024, 2048])
+@pytest.mark.parametrize("M", [1, 3, 8, 16])
+def test_linear_rows_shapes(device, K, M):
+    torch.manual_seed(K + M)
+    N = 300 if K != 512 else 5000  # out_features not a multiple of 16 (partial last tile)
+    lin = nn.Linear(K, N).to(device)
+    x = torch.randn(M, K, device=device)
+    got = hip_linear.linear_rows_hip(x, lin)
+    err = (got.double().cpu() - ref_linear(x, lin)).abs().max().item()
+    print(f"linear K={K} M={M} N={N}: max err {err:.2e}", flush=True)
+    assert err <= 2e-5
+
+
+@pytest.mark.parametrize("use_ln,gelu,res,bias", [(True, False, False, True), (True, True, False, True),
+                                                  (False, False, True, True), (True, True, True, False)])
+def test_linear_rows_fusions(device, use_ln, gelu, res, bias):
+    torch.manual_seed(7)
+    M, K, N = 5, 512, 2048
+    lin = nn.Linear(K, N, bias=bias).to(device)
+    ln = nn.LayerNorm(K).to(device)
+    with torch.no_grad():
+        ln.weight.normal_(1.0, 0.1)
+        ln.bias.normal_(0.0, 0.1)
+    x = torch.randn(M, K, device=device) * 3 + 0.5
+    r = torch.randn(M, N, device=device) if res else None
+    got = hip_linear.linear_rows_hip(x, lin, ln=ln if use_ln else None, gelu=gelu, residual=r)
+    want = ref_linear(x, lin, ln if use_ln else None, gelu, r)
+    assert (got.double().cpu() - want).abs().max().item() <= 2e-5
+
+
+def test_linear_rows_strided_rows_and_out(device):
+    torch.manual_seed(8)
+    lin = nn.Linear(256, 64).to(device)
+    big = torch.randn(6, 400, device=device)
+    x = big[:, 8:264]  # row stride 400, 16-byte aligned start
+    out = torch.full((6, 80), 7.0, device=device)
+    hip_linear.linear_rows_hip(x, lin, out=out[:, :64])
+    assert (out[:, 64:] == 7.0).all()
+    assert (out[:, :64].double().cpu() - ref_linear(x, lin)).abs().max().item() <= 2e-5
+
+
+def test_linear_rows_rejects_bad_shapes(device):
+    lin = nn.Linear(96, 32).to(device)
+    with pytest.raises(Exception):
+        hip_linear.linear_rows_hip(torch.randn(2, 96, device=device), lin)  # in_features 96 unsupported
+    lin = nn.Linear(128, 32).to(device)
+    with pytest.raises(ValueError):
+        hip_linear.linear_rows_hip(torch.randn(17, 128, device=device), lin)  # more than 16 rows
+
+
+class _Attn(nn.Module):
+    def __init__(self, d, h):
+        super().__init__()
+        self.num_heads, self.head_dim, self.d_model = h, d // h, d
+        self.q_proj, self.k_proj, self.v_proj = nn.Linear(d, d), nn.Linear(d, d), nn.Linear(d, d)
+
+
+@pytest.mark.parametrize("pool_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d,h", [(512, 8), (128, 2)])
+def test_qkv_append(device, pool_dtype, d, h):
+    torch.manual_seed(9)
+    M, bs, nblk = 6, 16, 12
+    attn = _Attn(d, h).to(device)
+    ln = nn.LayerNorm(d).to(device)
+    x = torch.randn(M, d, device=device)
+    k_pool = torch.zeros(nblk, h, bs, d // h, device=device, dtype=pool_dtype)
+    v_pool = torch.zeros_like(k_pool)
+    slots = torch.tensor([5 * bs + 3, -1, 0, 11 * bs + 15, 12 * bs, 2 * bs + 7], dtype=torch.int32, device=device)
+    q = hip_linear.qkv_append_hip(x, ln, attn, k_pool, v_pool, slots)
+    xn = nn.functional.layer_norm(x.double().cpu(), (d,), ln.weight.double().cpu(), ln.bias.double().cpu(), ln.eps)
+    assert (q.double().cpu() - ref_linear(xn, attn.q_proj)).abs().max().item() <= 2e-5
+    kref = ref_linear(xn, attn.k_proj).float()
+    vref = ref_linear(xn, attn.v_proj).float()
+    want_k = torch.zeros(nblk, h, bs, d // h, dtype=pool_dtype)
+    want_v = torch.zeros_like(want_k)
+    for m, s in enumerate(slots.tolist()):
+        if s < 0 or s // bs >= nblk:
+            continue  # skipped rows (negative slot, block out of range)
+        want_k[s // bs, :, s % bs] = kref[m].view(h, d // h).to(pool_dtype)
+        want_v[s // bs, :, s % bs] = vref[m].view(h, d // h).to(pool_dtype)
+    got_k, got_v = k_pool.cpu(), v_pool.cpu()
+    written = want_k.abs().sum(dim=(1, 3)) > 0
+    assert torch.equal(got_k.abs().sum(dim=(1, 3)) > 0, written)  # exactly the target slots
+    tol = 2e-5 if pool_dtype == torch.float32 else 1e-2
+    assert (got_k.float() - want_k.float()).abs().max().item() <= tol
+    assert (got_v.float() - want_v.float()).abs().max().item() <= tol
