@@ -5,18 +5,21 @@
 // into a few tens of workgroups; here one workgroup of 8 wavefronts owns a 16-column tile of the
 // output, its wavefronts split K eight ways, and each wavefront accumulates the 16 (rows) x 16
 // (columns) tile with v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation) over its K
-// range; the eight partial tiles are summed in LDS and the epilogue is applied once.
+// range; the eight partial tiles are summed in LDS and the epilogue is applied once. Every global
+// load of a workgroup (weights, activations, LayerNorm parameters, bias, residual) is issued at
+// its start, so a launch costs one memory round trip.
 //   A (16 x 4): lane (G, c) holds x[row c][k(G, s)]     (rows >= M are zero)
 //   B (4 x 16): lane (G, c) holds W[col n0 + c][k(G, s)] (torch Linear weight, row-major [N, K])
 // with the contraction slot of MFMA s mapped to k(G, s) = k_wave + G*KL + s, so every lane reads
 // KL contiguous floats of one activation row and of one weight row (16-byte loads).
 // Fusions:
-//   prologue  LayerNorm of the activation rows (biased variance, like torch.nn.LayerNorm);
+//   prologue  LayerNorm of the activation rows (biased variance, like torch.nn.LayerNorm),
+//             computed from the slices the lanes already hold (no second pass over memory);
 //   epilogue  bias, exact (erf) GELU, residual add; or, for the K/V projections, a scatter of
 //             each row's head_dim vectors into its KV-pool slot (the append of the decode step).
 #include <math.h>
 
-#include "pa_common.h"
+#include "pa_attention.h"
 
 namespace pa {
 
@@ -48,15 +51,14 @@ struct LinArgs {
   int32_t H, Hd, bs;
 };
 
-template <int K>
+template <int K, bool LN>
 __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const LinArgs a) {
   constexpr int KW = K / kLinWaves;  // K range of one wavefront
   constexpr int KL = KW / 4;         // contiguous k values per lane
   static_assert(KL % 4 == 0, "16-byte loads");
 
   __shared__ float sm_part[kLinWaves][16][17];
-  __shared__ float sm_mean[kLinRows];
-  __shared__ float sm_rstd[kLinRows];
+  __shared__ float sm_red[2][kLinWaves][kLinRows];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
@@ -67,63 +69,83 @@ __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const L
   const int seg = blockIdx.x / tiles_per_seg;
   const int n0 = (blockIdx.x - seg * tiles_per_seg) * 16;
   const float* W = a.w[seg];
-
-  // ---- LayerNorm statistics of the activation rows (two rows per wavefront) -----------------
-  if (a.ln_w != nullptr) {
-    constexpr int PL = K / kWave;  // values per lane of one row (lane + 64e)
-    for (int r = w; r < kLinRows; r += kLinWaves) {
-      if (r >= a.M) break;
-      const float* xr = a.x + (int64_t)r * a.x_stride + lane;
-      float v[PL];
-#pragma unroll
-      for (int e = 0; e < PL; ++e) v[e] = xr[e * kWave];
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < PL; ++e) s += v[e];
-      const float mean = wave_sum(s) / K;
-      float q = 0.f;
-#pragma unroll
-      for (int e = 0; e < PL; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
-      const float var = wave_sum(q) / K;
-      if (lane == 0) {
-        sm_mean[r] = mean;
-        sm_rstd[r] = 1.f / sqrtf(var + a.ln_eps);
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- operands: this lane's activation row c and weight row n0 + c over k(G, 0..KL) --------
   const int kb = w * KW + G * KL;
-  float xa[KL], wb[KL];
-  if (c < a.M) {
-    const float* xr = a.x + (int64_t)c * a.x_stride + kb;
+  const bool row_ok = c < a.M;
+
+  // ---- every global load first: weight row n0 + c and activation row c over k(G, 0..KL), the
+  // LayerNorm parameters of those k, and the epilogue operands of thread (m, n0 + cc) ----------
+  // LayerNorm parameters are preloaded with the rest up to K = 1024; at K = 2048 they would not
+  // fit the register budget and are read after the statistics.
+  constexpr bool PRE = LN && KL <= 32;
+  float wb[KL], xa[KL], lg[PRE ? KL : 1], lb[PRE ? KL : 1];
+  {
+    const int n = n0 + c < a.seg_n ? n0 + c : a.seg_n - 1;  // clamp: the column is discarded
+    const float* wr = W + (int64_t)n * a.K + kb;
+    const float* xr = a.x + (int64_t)(row_ok ? c : 0) * a.x_stride + kb;
 #pragma unroll
     for (int e = 0; e < KL; e += 4) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(xr + e);
+      const f32x4 t = *reinterpret_cast<const f32x4*>(wr + e);
+      wb[e] = t[0]; wb[e + 1] = t[1]; wb[e + 2] = t[2]; wb[e + 3] = t[3];
+    }
+#pragma unroll
+    for (int e = 0; e < KL; e += 4) {
+      const f32x4 t = row_ok ? *reinterpret_cast<const f32x4*>(xr + e) : f32x4{0.f, 0.f, 0.f, 0.f};
       xa[e] = t[0]; xa[e + 1] = t[1]; xa[e + 2] = t[2]; xa[e + 3] = t[3];
     }
-    if (a.ln_w != nullptr) {
-      const float mean = sm_mean[c], rstd = sm_rstd[c];
+    if constexpr (PRE) {
+#pragma unroll
+      for (int e = 0; e < KL; e += 4) {
+        const f32x4 g = *reinterpret_cast<const f32x4*>(a.ln_w + kb + e);
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(a.ln_b + kb + e);
+        lg[e] = g[0]; lg[e + 1] = g[1]; lg[e + 2] = g[2]; lg[e + 3] = g[3];
+        lb[e] = bb[0]; lb[e + 1] = bb[1]; lb[e + 2] = bb[2]; lb[e + 3] = bb[3];
+      }
+    }
+  }
+  const int m = (threadIdx.x >> 4) & 15;
+  const int cc = threadIdx.x & 15;
+  const int n = n0 + cc;
+  const bool live = threadIdx.x < 256 && m < a.M && n < a.seg_n;
+  float bias_v = 0.f, res_v = 0.f;
+  if (live) {
+    if (a.b[seg] != nullptr) bias_v = a.b[seg][n];
+    if (a.res != nullptr) res_v = a.res[(int64_t)m * a.res_stride + seg * a.seg_n + n];
+  }
+
+  // ---- LayerNorm of row c from the loaded slices: the row is spread over the 4 lane groups of
+  // each of the 8 wavefronts, so the sums reduce with two permlane swaps and one LDS exchange ---
+  if constexpr (LN) {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < KL; ++e) s += xa[e];
+    s = sum_xor32(sum_xor16(s));
+    if (G == 0) sm_red[0][w][c] = s;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kLinWaves; ++ww) tot += sm_red[0][ww][c];
+    const float mean = tot / K;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < KL; ++e) q = fmaf(xa[e] - mean, xa[e] - mean, q);
+    q = sum_xor32(sum_xor16(q));
+    if (G == 0) sm_red[1][w][c] = q;
+    __syncthreads();
+    float var = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kLinWaves; ++ww) var += sm_red[1][ww][c];
+    const float rstd = 1.f / sqrtf(var / K + a.ln_eps);
+    if constexpr (PRE) {
+#pragma unroll
+      for (int e = 0; e < KL; ++e) xa[e] = row_ok ? fmaf((xa[e] - mean) * rstd, lg[e], lb[e]) : 0.f;
+    } else {
 #pragma unroll
       for (int e = 0; e < KL; e += 4) {
         const f32x4 g = *reinterpret_cast<const f32x4*>(a.ln_w + kb + e);
         const f32x4 bb = *reinterpret_cast<const f32x4*>(a.ln_b + kb + e);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xa[e + q] = fmaf((xa[e + q] - mean) * rstd, g[q], bb[q]);
+        for (int q2 = 0; q2 < 4; ++q2) xa[e + q2] = row_ok ? fmaf((xa[e + q2] - mean) * rstd, g[q2], bb[q2]) : 0.f;
       }
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < KL; ++e) xa[e] = 0.f;
-  }
-  {
-    const int n = n0 + c < a.seg_n ? n0 + c : a.seg_n - 1;  // clamp: the column is discarded
-    const float* wr = W + (int64_t)n * a.K + kb;
-#pragma unroll
-    for (int e = 0; e < KL; e += 4) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(wr + e);
-      wb[e] = t[0]; wb[e + 1] = t[1]; wb[e + 2] = t[2]; wb[e + 3] = t[3];
     }
   }
 
@@ -140,15 +162,11 @@ __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const L
   __syncthreads();
 
   // ---- epilogue: one thread per (row, column) of the tile --------------------------------------
-  if (threadIdx.x >= 256) return;
-  const int m = threadIdx.x >> 4;
-  const int cc = threadIdx.x & 15;
-  const int n = n0 + cc;
-  if (m >= a.M || n >= a.seg_n) return;
+  if (!live) return;
   float v = 0.f;
 #pragma unroll
   for (int ww = 0; ww < kLinWaves; ++ww) v += sm_part[ww][m][cc];
-  if (a.b[seg] != nullptr) v += a.b[seg][n];
+  v += bias_v;
   if (a.act == 1) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
   if (a.k_pool != nullptr && seg > 0) {
     const int slot = a.slots[m];
@@ -163,8 +181,7 @@ __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const L
       static_cast<float*>(pool)[off] = v;
     return;
   }
-  if (a.res != nullptr) v += a.res[(int64_t)m * a.res_stride + seg * a.seg_n + n];
-  a.out[(int64_t)m * a.out_stride + seg * a.seg_n + n] = v;
+  a.out[(int64_t)m * a.out_stride + seg * a.seg_n + n] = v + res_v;
 }
 
 static bool small_linear_k_supported(int32_t K) {
@@ -175,19 +192,47 @@ static int launch_small_linear(const LinArgs& a, hipStream_t stream) {
   const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + 15) / 16);
   if (tiles > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
   const dim3 grid((unsigned)tiles), block(kLinWaves * kWave);
+  const bool ln = a.ln_w != nullptr;
+#define PA_LIN_CASE(KK)                                                                   \
+  case KK:                                                                                \
+    if (ln) small_linear_kernel<KK, true><<<grid, block, 0, stream>>>(a);                 \
+    else small_linear_kernel<KK, false><<<grid, block, 0, stream>>>(a);                   \
+    break;
   switch (a.K) {
-    case 128: small_linear_kernel<128><<<grid, block, 0, stream>>>(a); break;
-    case 256: small_linear_kernel<256><<<grid, block, 0, stream>>>(a); break;
-    case 512: small_linear_kernel<512><<<grid, block, 0, stream>>>(a); break;
-    case 1024: small_linear_kernel<1024><<<grid, block, 0, stream>>>(a); break;
-    case 2048: small_linear_kernel<2048><<<grid, block, 0, stream>>>(a); break;
+    PA_LIN_CASE(128)
+    PA_LIN_CASE(256)
+    PA_LIN_CASE(512)
+    PA_LIN_CASE(1024)
+    PA_LIN_CASE(2048)
     default: PA_FAIL(PA_ERR_UNSUPPORTED, "small linear: in_features must be 128, 256, 512, 1024 or 2048, got %d", a.K);
   }
+#undef PA_LIN_CASE
   PA_CHECK_LAUNCH("small linear kernel");
   return PA_OK;
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Token + position embedding of a [B, T] step: row b*T + t = tok[ids[b, t]] + pos[min(p0[b] + t,
+// max_pos - 1)]; an id outside the vocabulary gives a zero token row. One workgroup per row.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* ids, const int64_t* pos0, int32_t T,
+                                                        const float* tok, int64_t vocab, const float* pos_tab,
+                                                        int32_t max_pos, int32_t d, float* out, int64_t out_stride) {
+  const int row = blockIdx.x;
+  const int b = row / T, t = row - b * T;
+  const int64_t id = ids[row];
+  int64_t p = pos0[b] + t;
+  p = p < max_pos - 1 ? p : max_pos - 1;
+  p = p > 0 ? p : 0;
+  const bool ok = id >= 0 && id < vocab;
+  const f32x4* tr = reinterpret_cast<const f32x4*>(tok + (ok ? id : 0) * d);
+  const f32x4* pr = reinterpret_cast<const f32x4*>(pos_tab + p * d);
+  f32x4* o = reinterpret_cast<f32x4*>(out + (int64_t)row * out_stride);
+  for (int k = threadIdx.x; k < d / 4; k += 256) {
+    const f32x4 tv = ok ? tr[k] : f32x4{0.f, 0.f, 0.f, 0.f};
+    o[k] = tv + pr[k];
+  }
+}
 
 }  // namespace pa
 
@@ -248,4 +293,24 @@ extern "C" int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int
   a.k_pool = k_pool; a.v_pool = v_pool; a.pool_bf16 = pool_dtype == PA_DTYPE_BF16; a.num_blocks = num_blocks;
   a.slots = slot_mapping; a.H = num_heads; a.Hd = head_dim; a.bs = block_size;
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pa_embed_rows(const int64_t* ids, const int64_t* pos_start, int32_t batch, int32_t query_len,
+                             const float* token_table, int64_t vocab, const float* pos_table, int32_t max_pos,
+                             int32_t d_model, float* out, int64_t out_stride, void* stream) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(batch >= 0 && query_len >= 0 && vocab > 0 && max_pos > 0 && d_model > 0 && d_model % 4 == 0,
+               "bad sizes: batch=%d query_len=%d vocab=%lld max_pos=%d d_model=%d", batch, query_len,
+               (long long)vocab, max_pos, d_model);
+  const int64_t rows = (int64_t)batch * query_len;
+  if (rows == 0) return PA_OK;
+  PA_CHECK_ARG(ids && pos_start && token_table && pos_table && out, "null pointer argument");
+  PA_CHECK_ARG(aligned16(token_table) && aligned16(pos_table) && aligned16(out) && out_stride % 4 == 0 &&
+               out_stride >= d_model, "tables and out must be 16-byte aligned with out_stride % 4 == 0");
+  if (rows > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  embed_rows_kernel<<<dim3((unsigned)rows), dim3(256), 0, st>>>(ids, pos_start, query_len, token_table, vocab,
+                                                                 pos_table, max_pos, d_model, out, out_stride);
+  PA_CHECK_LAUNCH("embedding kernel");
+  return PA_OK;
 }

@@ -89,6 +89,12 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _c_void_p, _int, _i64,  # k pool, v pool, pool dtype, num_blocks
          _c_void_p, _i32, _i32, _i32, _c_void_p],  # slots, heads, head_dim, block_size, stream
     ),
+    "pa_embed_rows": (
+        _int,
+        [_c_void_p, _c_void_p, _i32, _i32,  # ids, pos_start, batch, query_len
+         _c_void_p, _i64, _c_void_p, _i32,  # token table, vocab, position table, max_pos
+         _i32, _c_void_p, _i64, _c_void_p],  # d_model, out, out stride, stream
+    ),
     "pa_zero_blocks": (
         _int,
         [_c_void_p, _c_void_p, _int, _i64, _i32, _i32, _i32, _c_void_p, _i32, _c_void_p],

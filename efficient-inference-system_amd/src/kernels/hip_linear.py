@@ -3,6 +3,7 @@
   linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
   qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
                    one launch; returns q                                     (pa_qkv_append)
+  embed_rows_hip   token + clamped position embedding of a [B, T] step       (pa_embed_rows)
 
 They stand in for the nn.LayerNorm / nn.Linear / nn.GELU calls and the append of the
 reference's cached forward (src/model/transformer.py:30-35, src/model/attention.py:46-64) on
@@ -83,6 +84,23 @@ def qkv_append_hip(x: torch.Tensor, ln: nn.LayerNorm, attn, k_pool: torch.Tensor
         slot_mapping.data_ptr(), H, Hd, bs, _stream(x.device),
     )
     _lib.check(status, "pa_qkv_append")
+    return out
+
+
+def embed_rows_hip(ids: torch.Tensor, pos_start: torch.Tensor, token_emb: nn.Embedding, pos_emb: nn.Embedding,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """[B*T, d] rows token_emb(ids[b, t]) + pos_emb(min(pos_start[b] + t, max_pos - 1))."""
+    if ids.dtype != torch.int64 or pos_start.dtype != torch.int64 or not ids.is_contiguous():
+        raise ValueError("ids and pos_start must be int64 (ids contiguous [B, T])")
+    B, T = ids.shape
+    d = token_emb.embedding_dim
+    if out is None:
+        out = torch.empty((B * T, d), dtype=torch.float32, device=ids.device)
+    status = _lib.load().pa_embed_rows(
+        ids.data_ptr(), pos_start.data_ptr(), B, T, token_emb.weight.data_ptr(), token_emb.num_embeddings,
+        pos_emb.weight.data_ptr(), pos_emb.num_embeddings, d, out.data_ptr(), out.stride(0), _stream(ids.device),
+    )
+    _lib.check(status, "pa_embed_rows")
     return out
 
 

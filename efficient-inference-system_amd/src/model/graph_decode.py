@@ -117,6 +117,8 @@ class _Captured:
         # stays valid for the graph's lifetime.
         self.ws = _workspace(device, ws_bytes) if ws_bytes else None
         self.fused = Tb == 1 and B <= hip_linear.MAX_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
+        self.embed_fused = (fused_decode_enabled() and model.token_emb.weight.dtype == torch.float32
+                            and model.pos_emb.weight.dtype == torch.float32 and model.token_emb.embedding_dim % 4 == 0)
         self.signature = _signature(pools)
         self.graph = None
         self.logits = None
@@ -152,9 +154,12 @@ class GraphedStep:
             csr[3 * B + 1:], csr[0:B + 1], csr[B + 1:2 * B + 1], csr[2 * B + 1:3 * B + 1],
             query_len=Tb, block_size=m.kv_block_size, max_pages=cap.pages, with_slots=True,
         )
-        steps = torch.arange(Tb, device=cap.ids.device).view(1, Tb)
-        positions = torch.clamp(cap.pos.view(B, 1) + steps, max=m.max_seq_len - 1)
-        x = m.token_emb(cap.ids) + m.pos_emb(positions)
+        if cap.embed_fused:
+            x = hip_linear.embed_rows_hip(cap.ids, cap.pos, m.token_emb, m.pos_emb).view(B, Tb, -1)
+        else:
+            steps = torch.arange(Tb, device=cap.ids.device).view(1, Tb)
+            positions = torch.clamp(cap.pos.view(B, 1) + steps, max=m.max_seq_len - 1)
+            x = m.token_emb(cap.ids) + m.pos_emb(positions)
         if cap.fused:
             return self._fused_decode_layers(cap, pools, x.view(B, -1), pt, seq32, slots)
         for blk, pool in zip(m.blocks, pools):

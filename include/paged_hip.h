@@ -193,6 +193,17 @@ int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int32_t d_mode
                   const int32_t* slot_mapping, int32_t num_heads, int32_t head_dim,
                   int32_t block_size, void* stream);
 
+/*
+ * pa_embed_rows: x[b*T + t, :] = token_table[ids[b, t], :] + pos_table[min(pos_start[b] + t,
+ * max_pos - 1), :] for a [batch, query_len] step (ids and pos_start int64, tables fp32 row-major
+ * [vocab, d_model] / [max_pos, d_model]); an id outside [0, vocab) gives a zero token row. Replaces
+ * the position arithmetic and the two nn.Embedding lookups of the reference's forward
+ * (src/model/transformer.py:144-150) in one launch.
+ */
+int pa_embed_rows(const int64_t* ids, const int64_t* pos_start, int32_t batch, int32_t query_len,
+                  const float* token_table, int64_t vocab, const float* pos_table, int32_t max_pos,
+                  int32_t d_model, float* out, int64_t out_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -111,3 +111,37 @@ def test_qkv_append(device, pool_dtype, d, h):
     tol = 2e-5 if pool_dtype == torch.float32 else 1e-2
     assert (got_k.float() - want_k.float()).abs().max().item() <= tol
     assert (got_v.float() - want_v.float()).abs().max().item() <= tol
+
+
+def test_embed_rows(device):
+    """Token + position embedding of a [B, T] step, positions clamped to the table like the
+    graph step's padded rows; an out-of-vocabulary id gives a zero token row."""
+    torch.manual_seed(10)
+    tok, pos = nn.Embedding(300, 128).to(device), nn.Embedding(64, 128).to(device)
+    ids = torch.randint(0, 300, (3, 20), device=device)
+    ids[1, 4] = 300
+    p0 = torch.tensor([0, 30, 55], device=device)
+    got = hip_linear.embed_rows_hip(ids, p0, tok, pos).cpu()
+    want = torch.empty(3 * 20, 128)
+    for b in range(3):
+        for t in range(20):
+            i = int(ids[b, t])
+            row = tok.weight[i].cpu() if i < 300 else torch.zeros(128)
+            want[b * 20 + t] = row + pos.weight[min(int(p0[b]) + t, 63)].cpu()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("K", [128, 1024, 2048])
+def test_linear_rows_layernorm_every_width(device, K):
+    """The LayerNorm prologue at every kernel width (preloaded parameters up to 1024, read after
+    the statistics at 2048), with rows of different means and scales."""
+    torch.manual_seed(K)
+    M, N = 7, 96
+    lin = nn.Linear(K, N).to(device)
+    ln = nn.LayerNorm(K, eps=1e-5).to(device)
+    with torch.no_grad():
+        ln.weight.normal_(1.0, 0.2)
+        ln.bias.normal_(0.0, 0.2)
+    x = torch.randn(M, K, device=device) * torch.linspace(0.1, 10, M, device=device).view(M, 1) + 3.0
+    got = hip_linear.linear_rows_hip(x, lin, ln=ln, gelu=True)
+    assert (got.double().cpu() - ref_linear(x, lin, ln, True)).abs().max().item() <= 5e-5
