@@ -1,14 +1,15 @@
 // Small-M fp32 linear layers for the decode step of the paged-attention model (gfx950).
 //
-// A decode step multiplies at most 16 token rows by each weight matrix, so the work is a stream
-// of the weights (N x K fp32) against a few rows of activations. Library GEMMs tile such shapes
-// into a few tens of workgroups; here one workgroup of 8 wavefronts owns a 16-column tile of the
-// output, its wavefronts split K eight ways, and each wavefront accumulates the 16 (rows) x 16
+// A decode step (or a short prefill chunk) multiplies at most 64 token rows by each weight matrix,
+// so the work is a stream of the weights (N x K fp32) against a few rows of activations. Library
+// GEMMs tile such shapes into a few tens of workgroups; here one workgroup of 8 wavefronts owns a
+// 16-row x 16-column tile of the output (grid x: column tiles, y: row tiles), its wavefronts split
+// K eight ways, and each wavefront accumulates the 16 (rows) x 16
 // (columns) tile with v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation) over its K
 // range; the eight partial tiles are summed in LDS and the epilogue is applied once. Every global
 // load of a workgroup (weights, activations, LayerNorm parameters, bias, residual) is issued at
 // its start, so a launch costs one memory round trip.
-//   A (16 x 4): lane (G, c) holds x[row c][k(G, s)]     (rows >= M are zero)
+//   A (16 x 4): lane (G, c) holds x[row r0 + c][k(G, s)]  (rows >= M are zero)
 //   B (4 x 16): lane (G, c) holds W[col n0 + c][k(G, s)] (torch Linear weight, row-major [N, K])
 // with the contraction slot of MFMA s mapped to k(G, s) = k_wave + G*KL + s, so every lane reads
 // KL contiguous floats of one activation row and of one weight row (16-byte loads).
@@ -26,7 +27,8 @@ namespace pa {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLinWaves = 8;
-constexpr int kLinRows = 16;  // maximum activation rows (MFMA tile height)
+constexpr int kLinRows = 16;     // activation rows per workgroup (MFMA tile height)
+constexpr int kLinMaxRows = 64;  // rows per call: up to four row tiles (grid y)
 
 struct LinArgs {
   const float* x;
@@ -70,7 +72,8 @@ __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const L
   const int n0 = (blockIdx.x - seg * tiles_per_seg) * 16;
   const float* W = a.w[seg];
   const int kb = w * KW + G * KL;
-  const bool row_ok = c < a.M;
+  const int r0 = blockIdx.y * kLinRows;  // first activation row of this workgroup
+  const bool row_ok = r0 + c < a.M;
 
   // ---- every global load first: weight row n0 + c and activation row c over k(G, 0..KL), the
   // LayerNorm parameters of those k, and the epilogue operands of thread (m, n0 + cc) ----------
@@ -81,7 +84,7 @@ __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const L
   {
     const int n = n0 + c < a.seg_n ? n0 + c : a.seg_n - 1;  // clamp: the column is discarded
     const float* wr = W + (int64_t)n * a.K + kb;
-    const float* xr = a.x + (int64_t)(row_ok ? c : 0) * a.x_stride + kb;
+    const float* xr = a.x + (int64_t)(row_ok ? r0 + c : 0) * a.x_stride + kb;
 #pragma unroll
     for (int e = 0; e < KL; e += 4) {
       const f32x4 t = *reinterpret_cast<const f32x4*>(wr + e);
@@ -102,7 +105,8 @@ __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const L
       }
     }
   }
-  const int m = (threadIdx.x >> 4) & 15;
+  const int ml = (threadIdx.x >> 4) & 15;  // row within the tile
+  const int m = r0 + ml;
   const int cc = threadIdx.x & 15;
   const int n = n0 + cc;
   const bool live = threadIdx.x < 256 && m < a.M && n < a.seg_n;
@@ -165,7 +169,7 @@ __global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const L
   if (!live) return;
   float v = 0.f;
 #pragma unroll
-  for (int ww = 0; ww < kLinWaves; ++ww) v += sm_part[ww][m][cc];
+  for (int ww = 0; ww < kLinWaves; ++ww) v += sm_part[ww][ml][cc];
   v += bias_v;
   if (a.act == 1) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
   if (a.k_pool != nullptr && seg > 0) {
@@ -191,7 +195,7 @@ static bool small_linear_k_supported(int32_t K) {
 static int launch_small_linear(const LinArgs& a, hipStream_t stream) {
   const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + 15) / 16);
   if (tiles > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
-  const dim3 grid((unsigned)tiles), block(kLinWaves * kWave);
+  const dim3 grid((unsigned)tiles, (unsigned)((a.M + kLinRows - 1) / kLinRows)), block(kLinWaves * kWave);
   const bool ln = a.ln_w != nullptr;
 #define PA_LIN_CASE(KK)                                                                   \
   case KK:                                                                                \
@@ -244,7 +248,7 @@ extern "C" int pa_linear_rows(const float* x, int64_t x_stride, int32_t rows, in
                               int32_t activation, const float* residual, int64_t residual_stride,
                               float* out, int64_t out_stride, void* stream) {
   pa_host::clear_error();
-  PA_CHECK_ARG(rows >= 0 && rows <= kLinRows, "rows must be in [0, %d], got %d", kLinRows, rows);
+  PA_CHECK_ARG(rows >= 0 && rows <= kLinMaxRows, "rows must be in [0, %d], got %d", kLinMaxRows, rows);
   PA_CHECK_ARG(out_features > 0 && in_features > 0, "bad sizes: in=%d out=%d", in_features, out_features);
   PA_CHECK_ARG(activation == 0 || activation == 1, "bad activation %d", activation);
   if (rows == 0) return PA_OK;
@@ -272,7 +276,7 @@ extern "C" int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int
                              const int32_t* slot_mapping, int32_t num_heads, int32_t head_dim,
                              int32_t block_size, void* stream) {
   pa_host::clear_error();
-  PA_CHECK_ARG(rows >= 0 && rows <= kLinRows, "rows must be in [0, %d], got %d", kLinRows, rows);
+  PA_CHECK_ARG(rows >= 0 && rows <= kLinMaxRows, "rows must be in [0, %d], got %d", kLinMaxRows, rows);
   PA_CHECK_ARG(num_heads > 0 && head_dim > 0 && block_size > 0 && d_model == num_heads * head_dim,
                "d_model must equal num_heads * head_dim");
   PA_CHECK_ARG(pool_dtype == PA_DTYPE_F32 || pool_dtype == PA_DTYPE_BF16, "bad pool dtype %d", pool_dtype);

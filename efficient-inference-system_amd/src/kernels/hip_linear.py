@@ -1,4 +1,4 @@
-"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32, <= 16 rows).
+"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32, <= 64 rows).
 
   linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
   qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
@@ -7,7 +7,7 @@
 
 They stand in for the nn.LayerNorm / nn.Linear / nn.GELU calls and the append of the
 reference's cached forward (src/model/transformer.py:30-35, src/model/attention.py:46-64) on
-one-token steps. All work is enqueued on torch's current stream; tensors must be on a HIP device.
+one-token steps and short prefill chunks. All work is enqueued on torch's current stream; tensors must be on a HIP device.
 """
 from __future__ import annotations
 
@@ -16,7 +16,7 @@ import torch.nn as nn
 
 from src.kernels import _lib
 
-MAX_ROWS = 16
+MAX_ROWS = 64
 SUPPORTED_FEATURES = (128, 256, 512, 1024, 2048)
 
 
@@ -40,7 +40,7 @@ def supported(linear: nn.Linear) -> bool:
 
 def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | None = None, gelu: bool = False,
                     residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 16)."""
+    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 64)."""
     _rows(x, "x")
     M, K = x.shape
     if K != linear.in_features:

@@ -23,6 +23,26 @@ class _PinnedRing:
         self.events: list[torch.cuda.Event | None] = [None] * _SLOTS
         self.next = 0
 
+    def upload_into(self, arr: np.ndarray, dst: torch.Tensor) -> None:
+        """Asynchronous copy of arr into the first arr.nbytes bytes of the device tensor dst
+        (contiguous), through the next pinned slot."""
+        nbytes = arr.nbytes
+        if nbytes > _SLOT_BYTES:
+            dst.view(-1).view(torch.uint8)[:nbytes].copy_(torch.from_numpy(arr.view(np.uint8).reshape(-1)).pin_memory(),
+                                                          non_blocking=True)
+            return
+        i = self.next
+        self.next = (i + 1) % _SLOTS
+        ev = self.events[i]
+        if ev is not None:
+            ev.synchronize()
+        self.host_np[i * _SLOT_BYTES:i * _SLOT_BYTES + nbytes] = arr.view(np.uint8).reshape(-1)
+        dst.view(-1).view(torch.uint8)[:nbytes].copy_(self.host[i * _SLOT_BYTES:i * _SLOT_BYTES + nbytes],
+                                                      non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self.events[i] = ev
+
     def upload(self, arr: np.ndarray) -> torch.Tensor:
         nbytes = arr.nbytes
         if nbytes > _SLOT_BYTES:
@@ -55,3 +75,17 @@ def upload(arr: np.ndarray, device: torch.device) -> torch.Tensor:
     if ring is None:
         ring = _rings[idx] = _PinnedRing(torch.device("cuda", idx))
     return ring.upload(arr)
+
+
+def upload_into(arr: np.ndarray, dst: torch.Tensor) -> None:
+    """Asynchronously copy a contiguous numpy array into the leading bytes of the contiguous
+    device tensor dst (on the current stream), without an intermediate device buffer."""
+    arr = np.ascontiguousarray(arr)
+    if not dst.is_contiguous() or dst.numel() * dst.element_size() < arr.nbytes:
+        raise ValueError("upload_into: destination must be contiguous and large enough")
+    device = dst.device
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ring = _rings.get(idx)
+    if ring is None:
+        ring = _rings[idx] = _PinnedRing(torch.device("cuda", idx))
+    ring.upload_into(arr, dst)

@@ -14,11 +14,12 @@ whole step once per (batch size, query-length bucket) and replays it:
                              kernel otherwise), output projection, MLP and residuals; final
                              LayerNorm and lm_head.
 
-One-token steps of up to 16 requests run the layers through the fused decode kernels
-(src/kernels/hip_linear.py) when the model's shapes allow: per layer one launch for LayerNorm +
-q/k/v projections + KV append, the decode attention, one for the output projection + residual,
-one for LayerNorm + fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. Set
-PAGED_HIP_FUSED_DECODE=0 to use the torch layers instead.
+Steps of at most 64 rows (B * bucketed T: every decode step of up to 64 requests, short prefill
+chunks) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
+shapes allow: per layer one launch for LayerNorm + q/k/v projections + KV append, the attention
+(decode or chunked prefill kernel), one for the output projection + residual, one for LayerNorm +
+fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. Set PAGED_HIP_FUSED_DECODE=0 to use
+the torch layers instead.
 
 Query lengths T > 1 are padded up to a bucket (16, 32, 64, 128, 256) with token id 0 and the
 logits of the real rows are returned. Padded rows are never appended to the cache (their slots
@@ -36,6 +37,7 @@ from __future__ import annotations
 import math
 import os
 
+import numpy as np
 import torch
 
 from src.cache.paged_kv import BatchedPagedKVCache
@@ -43,7 +45,7 @@ from src.kernels import _lib, hip_linear
 from src.kernels.hip_paged_attention import (
     _workspace, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
     pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
-from src.kernels.staging import upload
+from src.kernels.staging import upload_into
 
 T_BUCKETS = (16, 32, 64, 128, 256)
 
@@ -116,7 +118,7 @@ class _Captured:
         # Allocated outside the capture and referenced here, so the address the graph records
         # stays valid for the graph's lifetime.
         self.ws = _workspace(device, ws_bytes) if ws_bytes else None
-        self.fused = Tb == 1 and B <= hip_linear.MAX_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
+        self.fused = B * Tb <= hip_linear.MAX_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
         self.embed_fused = (fused_decode_enabled() and model.token_emb.weight.dtype == torch.float32
                             and model.pos_emb.weight.dtype == torch.float32 and model.token_emb.embedding_dim % 4 == 0)
         self.signature = _signature(pools)
@@ -161,7 +163,7 @@ class GraphedStep:
             positions = torch.clamp(cap.pos.view(B, 1) + steps, max=m.max_seq_len - 1)
             x = m.token_emb(cap.ids) + m.pos_emb(positions)
         if cap.fused:
-            return self._fused_decode_layers(cap, pools, x.view(B, -1), pt, seq32, slots)
+            return self._fused_layers(cap, pools, x.view(B * Tb, -1), pt, seq32, slots)
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
@@ -179,21 +181,24 @@ class GraphedStep:
             x = x + blk.mlp(blk.ln2(x))
         return m.lm_head(m.ln_f(x))
 
-    def _fused_decode_layers(self, cap: _Captured, pools, x, pt, seq32, slots) -> torch.Tensor:
-        """The layers of a one-token step through the fused decode kernels; x is [B, d_model]."""
+    def _fused_layers(self, cap: _Captured, pools, x, pt, seq32, slots) -> torch.Tensor:
+        """The layers of a step through the fused kernels; x is [B * Tb, d_model] (<= 64 rows)."""
         m = self.model
-        B = cap.B
+        B, Tb = cap.B, cap.Tb
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
             q = hip_linear.qkv_append_hip(x, blk.ln1, a, k_pool, v_pool, slots)
-            q4 = q.view(B, 1, a.num_heads, a.head_dim).transpose(1, 2)
-            o = paged_attention_decode_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
-            x1 = hip_linear.linear_rows_hip(o.transpose(1, 2).reshape(B, a.d_model), a.out_proj, residual=x)
+            q4 = q.view(B, Tb, a.num_heads, a.head_dim).transpose(1, 2)
+            if Tb == 1:
+                o = paged_attention_decode_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
+            else:
+                o = paged_attention_prefill_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
+            x1 = hip_linear.linear_rows_hip(o.transpose(1, 2).reshape(B * Tb, a.d_model), a.out_proj, residual=x)
             h = hip_linear.linear_rows_hip(x1, blk.mlp[0], ln=blk.ln2, gelu=True)
             x = hip_linear.linear_rows_hip(h, blk.mlp[2], residual=x1)
         logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
-        return logits.view(B, 1, -1)
+        return logits.view(B, Tb, -1)
 
     def _capture(self, cap: _Captured, pools) -> None:
         # Warm-up on a side stream (initialises library handles); it performs the same step the
@@ -236,19 +241,23 @@ class GraphedStep:
                 self.captured.clear()  # every graph holds the old storage addresses
             cap = _Captured(m, B, Tb, pages, device, pools)
             self.captured[key] = cap
-        cap.csr[: buf.size].copy_(upload(buf, device))
-        if Tb == T:
-            cap.ids.copy_(input_ids)
+        upload_into(buf, cap.csr)
+        if (Tb == T and not isinstance(positions, int) and positions.dtype == cap.pos.dtype
+                and input_ids.dtype == cap.ids.dtype and positions.device == device):
+            torch._foreach_copy_([cap.ids, cap.pos], [input_ids, positions.view(B)])  # one launch
         else:
-            cap.ids.zero_()
-            cap.ids[:, :T].copy_(input_ids)
-        if isinstance(positions, int):
-            cap.pos.fill_(positions)
-        else:
-            cap.pos.copy_(positions.view(B))
+            if Tb == T:
+                cap.ids.copy_(input_ids)
+            else:
+                cap.ids.zero_()
+                cap.ids[:, :T].copy_(input_ids)
+            if isinstance(positions, int):
+                cap.pos.fill_(positions)
+            else:
+                cap.pos.copy_(positions.view(B))
         ones = all(c == 1 for c in current_lengths)
         if not (ones and getattr(cap, "cur_ones", True)):
-            cap.cur.copy_(upload(torch.tensor(current_lengths, dtype=torch.int32).numpy(), device))
+            upload_into(np.asarray(current_lengths, dtype=np.int32), cap.cur)
             cap.cur_ones = ones
         if cap.graph is None:
             self._capture(cap, pools)

@@ -156,13 +156,13 @@ int pa_zero_blocks(void* k_pool, void* v_pool, int pool_dtype, int64_t num_block
                    const int32_t* block_ids, int32_t n_ids, void* stream);
 
 /*
- * Decode-step linear layers of the model around the paged attention (fp32, at most 16 token rows).
+ * Decode-step linear layers of the model around the paged attention (fp32, at most 64 token rows).
  * No reference counterpart as entry points: they replace the torch nn.Linear / nn.LayerNorm /
  * nn.GELU calls of the reference's cached forward (src/model/transformer.py:30-35,
- * src/model/attention.py:46-48,64) on one-token steps, where a step is a few rows against every
- * weight matrix.
+ * src/model/attention.py:46-48,64) on one-token steps and short prefill chunks, where a step is
+ * a few rows against every weight matrix.
  *
- * pa_linear_rows: out[m, :] = act(LN(x[m, :]) W^T + bias) + residual[m, :] for m < rows (<= 16).
+ * pa_linear_rows: out[m, :] = act(LN(x[m, :]) W^T + bias) + residual[m, :] for m < rows (<= 64).
  *   weight is torch's [out_features, in_features] row-major; in_features must be 128, 256, 512,
  *   1024 or 2048;
  *   ln_weight/ln_bias NULL skips the LayerNorm (biased variance, eps ln_eps, like
@@ -181,7 +181,7 @@ int pa_linear_rows(const float* x, int64_t x_stride, int32_t rows, int32_t in_fe
  * the rows LN(x[m, :]) wk^T + bk and LN(x[m, :]) wv^T + bv are written, split into num_heads
  * vectors of head_dim, into pool slot slot_mapping[m] of the K and V pools (converted to the pool
  * dtype; slot < 0 or a block outside [0, num_blocks) skips the row). Replaces
- * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 16 and
+ * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 64 and
  * d_model in {128, 256, 512, 1024, 2048}.
  */
 int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int32_t d_model,
