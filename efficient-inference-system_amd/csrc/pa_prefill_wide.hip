@@ -2,10 +2,10 @@
 // contexts, where the 16-row kernel would re-read every KV block once per 16 query rows).
 //
 // One workgroup of 4 wavefronts per (request, head, tile of 128 query rows); wavefront w owns
-// rows 32w..32w+31 of the tile. The workgroup walks the KV blocks in steps of 32 keys (two
-// 16-token blocks): each step's K and V tiles are loaded from HBM once, cooperatively, into
-// double-buffered LDS (the next step's global loads are in flight while the current step is
-// computed), and all four wavefronts read them from there.
+// rows 32w..32w+31 of the tile. The workgroup walks the KV blocks in steps of 32 keys (head_dim
+// 128) or 64 keys (head_dim 64): each step's K and V tiles are loaded from HBM once,
+// cooperatively, into double-buffered LDS (the next step's global loads and page-table entries
+// are in flight while the current step is computed), and all four wavefronts read them there.
 //
 // Per step and wavefront, with v_mfma_f32_32x32x16_bf16 (fp32 accumulation):
 //   S^T = K Q^T      32 keys x 32 queries; A = K rows from LDS, B = the wavefront's q (bf16,
@@ -25,18 +25,10 @@
 // lazily (see kRescaleSlack) and interior steps skip the causal/length mask.
 #include "pa_attention.h"
 
-#ifndef PA_WIDE_KFIRST
-#define PA_WIDE_KFIRST 0
-#endif
-#ifndef PA_WIDE_PRIO
-#define PA_WIDE_PRIO 0
-#endif
-
 namespace pa {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Two fp32 values to packed bf16 (round to nearest even) with gfx950's v_cvt_pk_bf16_f32.
@@ -53,12 +45,21 @@ constexpr float kRescaleSlack = 8.f;
 constexpr int kWideWaves = 4;
 constexpr int kWideRows = kWideWaves * 32;  // query rows per workgroup
 
-template <typename IO, int HD>
+// NSUB = 32-key sub-tiles per step: the per-step costs (barrier, mask test, max/sum exchange,
+// lazy-rescale test) are paid once per NSUB * 32 keys. Measured on the large-prefill workload
+// (8 x 32 heads, chunk 512 over 1.8-3.7k contexts), same box: head_dim 128 460 us with NSUB 1,
+// 536 us with 2 (308 registers: one wavefront per SIMD), 516 us with 4; head_dim 64 266 us with 1,
+// 243 us with 2, 340 us with 4.
+template <int HD>
+constexpr int wide_nsub() { return HD == 64 ? 2 : 1; }
+
+template <typename IO, int HD, int NSUB>
 __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const AttnArgs a) {
   constexpr int NW = kWideWaves;
-  constexpr int KS = 32;                 // keys per step
+  constexpr int KS = 32 * NSUB;          // keys per step
+  constexpr int NBS = KS / 16;           // KV blocks per step
   constexpr int QH = HD / 2;             // head_dim values per lane in the QK^T operands
-  constexpr int NQ = HD / 16;            // QK^T MFMAs per step (k = 16 each)
+  constexpr int NQ = HD / 16;            // QK^T MFMAs per sub-tile (k = 16 each)
   constexpr int DU = HD / 32;            // output tiles of 32 head_dim rows
   constexpr int RS = HD + 8;             // LDS row stride in bf16 elements (16-byte pad)
   constexpr int RPC = HD / 8;            // 16-byte chunks per key row
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   const int n_wg = valid_keys(L, C, last_wg);  // nondecreasing in the row index
   int nb = (n_wg + 15) / 16;
   nb = nb < a.max_pages ? nb : a.max_pages;
-  const int nsteps = (nb + 1) / 2;
+  const int nsteps = (nb + NBS - 1) / NBS;
   int wsteps = 0;  // steps this wavefront computes (its rows need no keys beyond them)
   if (iw < a.T) {
     const int last_w = (iw + 31) < (a.T - 1) ? (iw + 31) : (a.T - 1);
@@ -125,25 +126,20 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   const uint16_t* kpool = static_cast<const uint16_t*>(a.k_pool);
   const uint16_t* vpool = static_cast<const uint16_t*>(a.v_pool);
   const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
-
-  // Page-table entries of step st: block 2st always exists (st < nsteps); 2st+1 may not.
-  auto step_blocks = [&](int st, int& e0, int& e1) {
-    e0 = pt[2 * st];
-    e1 = 2 * st + 1 < nb ? pt[2 * st + 1] : -1;
-  };
   auto ok_blk = [&](int e) { return e >= 0 && e < a.num_blocks; };
 
-  // Cooperative global loads of one step's K and V tiles (thread t: chunks t + 256n).
+  // Cooperative global loads of one step's K and V tiles (thread t: chunks t + 256n); the step's
+  // page-table entries are kept for its compute (-1 past the request's blocks).
   u32x4 kr[CPT], vr[CPT];
-  auto gload = [&](int st) {
-    int e0, e1;
-    step_blocks(st, e0, e1);
+  auto gload = [&](int st, int (&ent)[NBS]) {
+#pragma unroll
+    for (int j = 0; j < NBS; ++j) ent[j] = NBS * st + j < nb ? pt[NBS * st + j] : -1;
 #pragma unroll
     for (int n = 0; n < CPT; ++n) {
       const int q = threadIdx.x + n * NW * kWave;
       const int kk = q / RPC;
       const int col = (q - kk * RPC) * 8;
-      const int e = kk < 16 ? e0 : e1;
+      const int e = ent[kk >> 4];
       const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
       const int64_t off = (((int64_t)blk * a.H + h) * 16 + (kk & 15)) * HD + col;
       kr[n] = *reinterpret_cast<const u32x4*>(kpool + off);
@@ -161,57 +157,50 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
     }
   };
 
-  auto compute = [&](int buf, int st) {
-    // ---- S^T = K Q^T ------------------------------------------------------------------------
-    f32x16 sacc;
+  auto compute = [&](int buf, int st, const int (&ent)[NBS]) {
+    // ---- S^T = K Q^T for each 32-key sub-tile (independent MFMA chains, interleaved) ----------
+    f32x16 sacc[NSUB];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+    for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[u][e] = 0.f;
     const uint16_t* krow = &sk[buf][c * RS + G2 * QH];
-#if PA_WIDE_KFIRST
-    bf16x8 kf[NQ];
 #pragma unroll
-    for (int s = 0; s < NQ; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 8 * s);
-#if PA_WIDE_PRIO
-    __builtin_amdgcn_s_setprio(1);
-#endif
+    for (int s = 0; s < NQ; ++s)
 #pragma unroll
-    for (int s = 0; s < NQ; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qb[s], sacc, 0, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, NQ, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, NQ, 0);
-#if PA_WIDE_PRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
-#else
+      for (int u = 0; u < NSUB; ++u) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + u * 32 * RS + 8 * s);
+        sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s], sacc[u], 0, 0, 0);
+      }
+    // ---- online softmax (sub-tile u, keys 32u + 8j + 4*G2 + r of this step) -------------------
+    bool all_ok = true;
 #pragma unroll
-    for (int s = 0; s < NQ; ++s) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 8 * s);
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s], sacc, 0, 0, 0);
-    }
-#endif
-    // ---- online softmax (keys 8j + 4*G2 + r of this step) --------------------------------------
-    int e0, e1;
-    step_blocks(st, e0, e1);
-    const bool ok0 = ok_blk(e0), ok1 = ok_blk(e1);
-    const int t0 = st * KS + 4 * G2;
-    // Interior steps (both blocks valid, every key below every row's limit) need no mask.
-    const bool full = ok0 && ok1 && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
-    float p[16];
+    for (int j = 0; j < NBS; ++j) all_ok = all_ok && ok_blk(ent[j]);
+    // Interior steps (every block valid, every key below every row's limit) need no mask.
+    const bool full = all_ok && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
+    float p[NSUB][16];
     float mloc = -INFINITY;
     if (full) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        p[e] = sacc[e];
-        mloc = fmaxf(mloc, p[e]);
-      }
+      for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          p[u][e] = sacc[u][e];
+          mloc = fmaxf(mloc, p[u][e]);
+        }
     } else {
+      const int t0 = st * KS + 4 * G2;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = t0 + 8 * j + r;
-          const bool ok = (j < 2 ? ok0 : ok1) && t < n_c;
-          p[4 * j + r] = ok ? sacc[4 * j + r] : -INFINITY;
-          mloc = fmaxf(mloc, p[4 * j + r]);
+        for (int j = 0; j < 4; ++j) {
+          const bool okb = ok_blk(ent[2 * u + (j >> 1)]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 32 * u + 8 * j + r;
+            p[u][4 * j + r] = (okb && t < n_c) ? sacc[u][4 * j + r] : -INFINITY;
+            mloc = fmaxf(mloc, p[u][4 * j + r]);
+          }
         }
     }
     mloc = max_xor32(mloc);
@@ -226,57 +215,65 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
     }
     float ps = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      p[e] = fast_exp2(p[e] - m);
-      ps += p[e];
-    }
-    l += sum_xor32(ps);
-    // ---- O^T += V^T P^T -----------------------------------------------------------------------
-    // V values of this lane's 16 key rows, head_dim [c*DU, c*DU + DU).
-    uint32_t vf[16][VW];
+    for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint16_t* vp = &sv[buf][(8 * j + 4 * G2 + r) * RS + c * DU];
-        if constexpr (DU == 4) {
-          const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
-          vf[4 * j + r][0] = x[0];
-          vf[4 * j + r][1] = x[1];
-        } else {
-          vf[4 * j + r][0] = *reinterpret_cast<const uint32_t*>(vp);
-        }
+      for (int e = 0; e < 16; ++e) {
+        p[u][e] = fast_exp2(p[u][e] - m);
+        ps += p[u][e];
       }
+    l += sum_xor32(ps);
+    // ---- O^T += V^T P^T, per sub-tile ---------------------------------------------------------
 #pragma unroll
-    for (int mc = 0; mc < 2; ++mc) {
-      uint32_t pw[4];
+    for (int u2 = 0; u2 < NSUB; ++u2) {
+      // V values of this lane's 16 key rows of the sub-tile, head_dim [c*DU, c*DU + DU).
+      uint32_t vf[16][VW];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(p[8 * mc + 2 * q], p[8 * mc + 2 * q + 1]);
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int u = 0; u < DU; ++u) {
-        uint32_t aw[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t x0 = vf[8 * mc + 2 * q][u >> 1], x1 = vf[8 * mc + 2 * q + 1][u >> 1];
-          aw[q] = (u & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+        for (int r = 0; r < 4; ++r) {
+          const uint16_t* vp = &sv[buf][(32 * u2 + 8 * j + 4 * G2 + r) * RS + c * DU];
+          if constexpr (DU == 4) {
+            const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
+            vf[4 * j + r][0] = x[0];
+            vf[4 * j + r][1] = x[1];
+          } else {
+            vf[4 * j + r][0] = *reinterpret_cast<const uint32_t*>(vp);
+          }
         }
-        oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, (u32x4{aw[0], aw[1], aw[2], aw[3]})), pb, oacc[u], 0, 0, 0);
+#pragma unroll
+      for (int mc = 0; mc < 2; ++mc) {
+        uint32_t pw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(p[u2][8 * mc + 2 * q], p[u2][8 * mc + 2 * q + 1]);
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
+#pragma unroll
+        for (int d = 0; d < DU; ++d) {
+          uint32_t aw[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t x0 = vf[8 * mc + 2 * q][d >> 1], x1 = vf[8 * mc + 2 * q + 1][d >> 1];
+            aw[q] = (d & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+          }
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, (u32x4{aw[0], aw[1], aw[2], aw[3]})), pb, oacc[d], 0, 0, 0);
+        }
       }
     }
   };
 
   if (nsteps > 0) {
-    gload(0);
+    int cur[NBS], nxt[NBS];
+    gload(0, cur);
     lstore(0);
     __syncthreads();
     for (int st = 0; st < nsteps; ++st) {
       const bool more = st + 1 < nsteps;
-      if (more) gload(st + 1);
-      if (st < wsteps) compute(st & 1, st);
+      if (more) gload(st + 1, nxt);
+      if (st < wsteps) compute(st & 1, st, cur);
       if (more) lstore((st + 1) & 1);
       __syncthreads();
+#pragma unroll
+      for (int j = 0; j < NBS; ++j) cur[j] = nxt[j];
     }
   }
 
@@ -307,11 +304,11 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, hipStream_t stream) {
   if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
   const dim3 grid((unsigned)units), block(kWideWaves * kWave);
   if (io_dtype == PA_DTYPE_F32) {
-    if (a.head_dim == 64) prefill_wide_kernel<float, 64><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<float, 128><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<float, 64, wide_nsub<64>()><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<float, 128, wide_nsub<128>()><<<grid, block, 0, stream>>>(a);
   } else {
-    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64, wide_nsub<64>()><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<uint16_t, 128, wide_nsub<128>()><<<grid, block, 0, stream>>>(a);
   }
   PA_CHECK_LAUNCH("wide prefill kernel");
   return PA_OK;
