@@ -2,13 +2,13 @@
 //
 // A decode step (or a short prefill chunk) multiplies at most 64 token rows by each weight matrix,
 // so the work is a stream of the weights (N x K fp32) against a few rows of activations. Library
-// GEMMs tile such shapes into a few tens of workgroups; here one workgroup of 8 wavefronts owns a
-// 16-row x 16-column tile of the output (grid x: column tiles, y: row tiles), its wavefronts split
-// K eight ways, and each wavefront accumulates the 16 (rows) x 16
-// (columns) tile with v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation) over its K
-// range; the eight partial tiles are summed in LDS and the epilogue is applied once. Every global
-// load of a workgroup (weights, activations, LayerNorm parameters, bias, residual) is issued at
-// its start, so a launch costs one memory round trip.
+// GEMMs tile such shapes into a few tens of workgroups; here one workgroup of 8 (16 at K = 2048)
+// wavefronts owns a 16-row x 16-column tile of the output (grid x: column tiles, y: row tiles),
+// its wavefronts split K, and each wavefront accumulates the 16 (rows) x 16 (columns) tile with
+// v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation) over its K range; the partial tiles
+// are summed in LDS and the epilogue is applied once. Every global load of a workgroup (weights,
+// activations, LayerNorm parameters, bias, residual) is issued at its start, so a launch costs
+// one memory round trip.
 //   A (16 x 4): lane (G, c) holds x[row r0 + c][k(G, s)]  (rows >= M are zero)
 //   B (4 x 16): lane (G, c) holds W[col n0 + c][k(G, s)] (torch Linear weight, row-major [N, K])
 // with the contraction slot of MFMA s mapped to k(G, s) = k_wave + G*KL + s, so every lane reads
@@ -26,7 +26,6 @@ namespace pa {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLinWaves = 8;
 constexpr int kLinRows = 16;     // activation rows per workgroup (MFMA tile height)
 constexpr int kLinMaxRows = 64;  // rows per call: up to four row tiles (grid y)
 
@@ -53,8 +52,14 @@ struct LinArgs {
   int32_t H, Hd, bs;
 };
 
+// Wavefronts per workgroup (they split K): 16 at K = 2048 keeps more of the 128 KB weight tile in
+// flight per compute unit (fc2 of the benchmark model, 8 rows: 9.3 -> 8.2 us inside a graph).
+template <int K>
+constexpr int lin_waves() { return K >= 2048 ? 16 : 8; }
+
 template <int K, bool LN>
-__global__ __launch_bounds__(kLinWaves * kWave) void small_linear_kernel(const LinArgs a) {
+__global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(const LinArgs a) {
+  constexpr int kLinWaves = lin_waves<K>();
   constexpr int KW = K / kLinWaves;  // K range of one wavefront
   constexpr int KL = KW / 4;         // contiguous k values per lane
   static_assert(KL % 4 == 0, "16-byte loads");
@@ -195,12 +200,12 @@ static bool small_linear_k_supported(int32_t K) {
 static int launch_small_linear(const LinArgs& a, hipStream_t stream) {
   const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + 15) / 16);
   if (tiles > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
-  const dim3 grid((unsigned)tiles, (unsigned)((a.M + kLinRows - 1) / kLinRows)), block(kLinWaves * kWave);
+  const dim3 grid((unsigned)tiles, (unsigned)((a.M + kLinRows - 1) / kLinRows));
   const bool ln = a.ln_w != nullptr;
 #define PA_LIN_CASE(KK)                                                                   \
   case KK:                                                                                \
-    if (ln) small_linear_kernel<KK, true><<<grid, block, 0, stream>>>(a);                 \
-    else small_linear_kernel<KK, false><<<grid, block, 0, stream>>>(a);                   \
+    if (ln) small_linear_kernel<KK, true><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a); \
+    else small_linear_kernel<KK, false><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a);   \
     break;
   switch (a.K) {
     PA_LIN_CASE(128)
