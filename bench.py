@@ -229,8 +229,8 @@ def secondary_workloads(device, steps: int) -> dict:
         tfs = flops / (ms * 1e-3) / 1e12
         res[f"large_prefill_{tag}"] = {
             "workload": f"{b.batch} requests, {H} heads x {Hd}, context {b.extra['prev_lens']} + chunk 512 each, "
-                        f"{'bf16' if tag == 'bf16kv' else 'fp32'} KV, fp32 q/out"
-                        + (" (wide-tile kernel: 128 query rows per workgroup)" if tag == "bf16kv" else ""),
+                        f"{'bf16' if tag == 'bf16kv' else 'fp32'} KV, fp32 q/out "
+                        "(wide-tile kernel: 128 query rows per workgroup, KV staged through LDS)",
             "attention_us": round(1e3 * ms, 1), "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1),
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
         }

@@ -48,11 +48,11 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Wide-tile bf16-KV prefill (128 query rows per workgroup, KV staged through LDS). Defined in
-// pa_prefill_wide.hip.
+// Wide-tile prefill (128 query rows per workgroup, KV staged through LDS; bf16 or fp32 KV).
+// Defined in pa_prefill_wide.hip.
 bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size);
 int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len);
-int launch_prefill_wide(const AttnArgs& a, int io_dtype, hipStream_t stream);
+int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream);
 
 // Generic one-wavefront-per-(request, head, query row) kernel for shapes without a tuned kernel
 // (any block_size, head_dim <= 512). Defined in pa_decode.hip.

@@ -24,7 +24,6 @@
 
 namespace pa {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLinRows = 16;     // activation rows per workgroup (MFMA tile height)
 constexpr int kLinMaxRows = 64;  // rows per call: up to four row tiles (grid y)

@@ -42,7 +42,6 @@ __device__ __forceinline__ int tile_of(int unit, int ntiles, int pairs) {
   return unit / ntiles >= pairs / 2 ? slot : ntiles - 1 - slot;
 }
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
@@ -354,8 +353,8 @@ static bool prefill_fast_shape(int32_t head_dim, int32_t block_size) {
   return block_size == 16 && (head_dim == 64 || head_dim == 128);
 }
 
-// Kernel choice for bf16 KV: the wide-tile kernel when its (request, head, 128-row tile) units
-// fill the GPU at least twice over, else the 16-row kernel. PAGED_HIP_PREFILL_KERNEL=wide / tile
+// Kernel choice: the wide-tile kernel when its (request, head, 128-row tile) units fill the GPU
+// at least twice over, else the 16-row kernel. PAGED_HIP_PREFILL_KERNEL=wide / tile
 // forces one of them (tests use it to cover both at small sizes).
 static bool use_wide_prefill(int32_t batch, int32_t num_heads, int32_t query_len) {
   const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
@@ -419,7 +418,7 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   if (!prefill_fast_shape(head_dim, block_size)) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
   if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
       use_wide_prefill(batch, num_heads, query_len))
-    return launch_prefill_wide(a, io_dtype, stream);
+    return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
 
   const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);
   const int nsplit = prefill_num_splits(max_pages, split_blocks);

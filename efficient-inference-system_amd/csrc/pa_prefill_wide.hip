@@ -291,19 +291,235 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
     }
 }
 
+// fp32 KV: the same workgroup layout, LDS staging and online softmax, on v_mfma_f32_32x32x2_f32
+// (fp32 products, like the reference's fp32 path):
+//   S^T = K Q^T      MFMA s (s < HD/2) contracts head_dim slot G2 = index G2*HD/2 + s: lane
+//                    (G2, c) gives K[key c][index] (A, from LDS) and q[query c][index] (B, held
+//                    in registers for the whole walk);
+//   O^T += V^T P^T   MFMA (j, r) contracts key slot G2 = key 8j + 4*G2 + r, the key whose score
+//                    lane (G2, c) holds in its register 4j + r: A = V[that key][c*DU + d] (output
+//                    tile d, row c) and B = its softmax weight, exactly as held.
+// Per 32-key step a wavefront issues HD MFMAs of 32x32x2 (HD/2 for QK^T, HD/2 for PV), so the
+// per-step costs are small next to the matrix work.
+template <typename IO, int HD>
+__global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(const AttnArgs a) {
+  constexpr int NW = kWideWaves;
+  constexpr int KS = 32;                 // keys per step (two 16-token blocks)
+  constexpr int NBS = 2;
+  constexpr int QH = HD / 2;             // head_dim values per lane in the QK^T operands
+  constexpr int DU = HD / 32;            // output tiles of 32 head_dim rows
+  constexpr int RS = HD + 4;             // LDS row stride in floats (16-byte pad)
+  constexpr int RPC = HD / 4;            // 16-byte chunks per key row
+  constexpr int CPT = KS * RPC / (NW * kWave);
+  static_assert(CPT >= 1 && KS * RPC == CPT * NW * kWave, "tile split");
+
+  __shared__ __attribute__((aligned(16))) float sk[2][KS * RS];
+  __shared__ __attribute__((aligned(16))) float sv[2][KS * RS];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int G2 = lane >> 5;
+  const int c = lane & 31;
+
+  const int ntiles = (a.T + kWideRows - 1) / kWideRows;
+  const int unit = blockIdx.x;
+  const int qt = ntiles - 1 - unit % ntiles;
+  const int bh = unit / ntiles;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int i0 = qt * kWideRows;
+  const int iw = i0 + 32 * w;
+  const int i = iw + c;
+
+  const int L = a.seq_lens[b];
+  const int C = a.cur_lens[b];
+  const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
+  const int last_wg = (i0 + kWideRows - 1) < (a.T - 1) ? (i0 + kWideRows - 1) : (a.T - 1);
+  const int n_wg = valid_keys(L, C, last_wg);
+  int nb = (n_wg + 15) / 16;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+  const int nsteps = (nb + NBS - 1) / NBS;
+  int wsteps = 0;
+  if (iw < a.T) {
+    const int last_w = (iw + 31) < (a.T - 1) ? (iw + 31) : (a.T - 1);
+    wsteps = (valid_keys(L, C, last_w) + KS - 1) / KS;
+    wsteps = wsteps < nsteps ? wsteps : nsteps;
+  }
+
+  // B operand of S^T = K Q^T: q[i][G2*QH + s], pre-scaled into the log2 domain.
+  float qf[QH];
+  {
+    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
+                   (int64_t)(i < a.T ? i : 0) * a.q_st + G2 * QH;
+    const float qs = i < a.T ? a.scale_log2 : 0.f;
+#pragma unroll
+    for (int s = 0; s < QH; ++s) qf[s] = Elem<IO>::load(qp + s) * qs;
+  }
+
+  f32x16 oacc[DU];
+#pragma unroll
+  for (int d = 0; d < DU; ++d)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[d][e] = 0.f;
+  float m = kNegBig, l = 0.f;
+
+  const float* kpool = static_cast<const float*>(a.k_pool);
+  const float* vpool = static_cast<const float*>(a.v_pool);
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+  auto ok_blk = [&](int e) { return e >= 0 && e < a.num_blocks; };
+
+  u32x4 kr[CPT], vr[CPT];
+  auto gload = [&](int st, int (&ent)[NBS]) {
+#pragma unroll
+    for (int j = 0; j < NBS; ++j) ent[j] = NBS * st + j < nb ? pt[NBS * st + j] : -1;
+#pragma unroll
+    for (int n = 0; n < CPT; ++n) {
+      const int q = threadIdx.x + n * NW * kWave;
+      const int kk = q / RPC;
+      const int col = (q - kk * RPC) * 4;
+      const int e = ent[kk >> 4];
+      const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
+      const int64_t off = (((int64_t)blk * a.H + h) * 16 + (kk & 15)) * HD + col;
+      kr[n] = *reinterpret_cast<const u32x4*>(kpool + off);
+      vr[n] = *reinterpret_cast<const u32x4*>(vpool + off);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int n = 0; n < CPT; ++n) {
+      const int q = threadIdx.x + n * NW * kWave;
+      const int kk = q / RPC;
+      const int col = (q - kk * RPC) * 4;
+      *reinterpret_cast<u32x4*>(&sk[buf][kk * RS + col]) = kr[n];
+      *reinterpret_cast<u32x4*>(&sv[buf][kk * RS + col]) = vr[n];
+    }
+  };
+
+  auto compute = [&](int buf, int st, const int (&ent)[NBS]) {
+    // ---- S^T = K Q^T ------------------------------------------------------------------------
+    f32x16 sacc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+    const float* krow = &sk[buf][c * RS + G2 * QH];
+#pragma unroll
+    for (int s = 0; s < QH; s += 4) {
+      const f32x4 kv = *reinterpret_cast<const f32x4*>(krow + s);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[e], qf[s + e], sacc, 0, 0, 0);
+    }
+    // ---- online softmax (keys 8j + 4*G2 + r of this step) --------------------------------------
+    const bool ok0 = ok_blk(ent[0]), ok1 = ok_blk(ent[1]);
+    const bool full = ok0 && ok1 && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
+    float p[16];
+    float mloc = -INFINITY;
+    if (full) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        p[e] = sacc[e];
+        mloc = fmaxf(mloc, p[e]);
+      }
+    } else {
+      const int t0 = st * KS + 4 * G2;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = t0 + 8 * j + r;
+          p[4 * j + r] = ((j < 2 ? ok0 : ok1) && t < n_c) ? sacc[4 * j + r] : -INFINITY;
+          mloc = fmaxf(mloc, p[4 * j + r]);
+        }
+    }
+    mloc = max_xor32(mloc);
+    const bool grow = mloc > m + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float mnew = grow ? mloc : m;
+      const float alpha = fast_exp2(m - mnew);
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < DU; ++d) oacc[d] *= alpha;
+      m = mnew;
+    }
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      p[e] = fast_exp2(p[e] - m);
+      ps += p[e];
+    }
+    l += sum_xor32(ps);
+    // ---- O^T += V^T P^T: four keys (one row group j) at a time ----------------------------------
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float vv[4][DU];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vp = &sv[buf][(8 * j + 4 * G2 + r) * RS + c * DU];
+        if constexpr (DU == 4) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(vp);
+          vv[r][0] = x[0]; vv[r][1] = x[1]; vv[r][2] = x[2]; vv[r][3] = x[3];
+        } else {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
+          vv[r][0] = __uint_as_float(x[0]); vv[r][1] = __uint_as_float(x[1]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int d = 0; d < DU; ++d)
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[r][d], p[4 * j + r], oacc[d], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) {
+    int cur[NBS], nxt[NBS];
+    gload(0, cur);
+    lstore(0);
+    __syncthreads();
+    for (int st = 0; st < nsteps; ++st) {
+      const bool more = st + 1 < nsteps;
+      if (more) gload(st + 1, nxt);
+      if (st < wsteps) compute(st & 1, st, cur);
+      if (more) lstore((st + 1) & 1);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < NBS; ++j) cur[j] = nxt[j];
+    }
+  }
+
+  if (i >= a.T) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_st;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int R = 8 * j + 4 * G2 + r;
+#pragma unroll
+      for (int d = 0; d < DU; ++d) Elem<IO>::store(op + R * DU + d, oacc[d][4 * j + r] * inv);
+    }
+}
+
 bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size) {
-  return kv_dtype == PA_DTYPE_BF16 && block_size == 16 && (head_dim == 64 || head_dim == 128);
+  return (kv_dtype == PA_DTYPE_BF16 || kv_dtype == PA_DTYPE_F32) && block_size == 16 &&
+         (head_dim == 64 || head_dim == 128);
 }
 
 int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len) {
   return (int64_t)batch * num_heads * ((query_len + kWideRows - 1) / kWideRows);
 }
 
-int launch_prefill_wide(const AttnArgs& a, int io_dtype, hipStream_t stream) {
+int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream) {
   const int64_t units = prefill_wide_units(a.B, a.H, a.T);
   if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
   const dim3 grid((unsigned)units), block(kWideWaves * kWave);
-  if (io_dtype == PA_DTYPE_F32) {
+  if (kv_dtype == PA_DTYPE_F32) {
+    if (io_dtype == PA_DTYPE_F32) {
+      if (a.head_dim == 64) prefill_wide_f32_kernel<float, 64><<<grid, block, 0, stream>>>(a);
+      else prefill_wide_f32_kernel<float, 128><<<grid, block, 0, stream>>>(a);
+    } else {
+      if (a.head_dim == 64) prefill_wide_f32_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
+      else prefill_wide_f32_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
+    }
+  } else if (io_dtype == PA_DTYPE_F32) {
     if (a.head_dim == 64) prefill_wide_kernel<float, 64, wide_nsub<64>()><<<grid, block, 0, stream>>>(a);
     else prefill_wide_kernel<float, 128, wide_nsub<128>()><<<grid, block, 0, stream>>>(a);
   } else {

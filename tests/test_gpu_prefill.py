@@ -168,17 +168,18 @@ def test_prefill_split_then_other_shapes_share_the_workspace(device):
 # ---- wide-tile bf16 kernel (128 query rows per workgroup, KV staged through LDS) -------------
 
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
-def test_wide_prefill_forced_small(device, monkeypatch, head_dim, io_dtype):
-    """The wide kernel on ragged requests: contexts 0 / unaligned / long, chunk rows padded
-    (C < T), T not a multiple of 128 nor of 32, an empty request; against the oracle on the same
-    bf16 KV and against the 16-row kernel."""
+@pytest.mark.parametrize("io_dtype,kv_dtype", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+                                               (torch.float32, torch.float32), (torch.bfloat16, torch.float32)])
+def test_wide_prefill_forced_small(device, monkeypatch, head_dim, io_dtype, kv_dtype):
+    """The wide kernels (bf16 and fp32 KV) on ragged requests: contexts 0 / unaligned / long, chunk
+    rows padded (C < T), T not a multiple of 128 nor of 32, an empty request; against the oracle
+    on the same KV values and against the 16-row kernel."""
     ctx = [0, 37, 700, 16, 0, 1200]
     curs = [150, 150, 3, 90, 0, 150]
     T = 150
-    b = make_prefill(device, 31, ctx, curs, T=T, H=3, Hd=head_dim, kv_dtype=torch.bfloat16)
+    b = make_prefill(device, 31, ctx, curs, T=T, H=3, Hd=head_dim, kv_dtype=kv_dtype)
     q = b.q.to(io_dtype)
-    print(f"wide prefill hd={head_dim} io={io_dtype}", flush=True)
+    print(f"wide prefill hd={head_dim} io={io_dtype} kv={kv_dtype}", flush=True)
     monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "wide")
     got = paged_attention_prefill_hip(q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
     monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "tile")
@@ -187,9 +188,12 @@ def test_wide_prefill_forced_small(device, monkeypatch, head_dim, io_dtype):
                                   b.cur_lens, nthreads=NTHREADS)
     err = max_err(got, want)
     print(f"  max err vs oracle {err:.2e}, vs 16-row kernel {float((got - tile).abs().max()):.2e}", flush=True)
-    tol = 2e-2 if io_dtype == torch.float32 else 3e-2  # bf16 output adds one rounding
+    if kv_dtype == torch.float32:
+        tol, tile_tol = (1e-4, 1e-5) if io_dtype == torch.float32 else (1e-2, 1e-2)  # bf16 output rounding
+    else:
+        tol, tile_tol = (2e-2, 5e-3) if io_dtype == torch.float32 else (3e-2, 2e-2)
     assert err <= tol
-    assert float((got.float() - tile.float()).abs().max()) <= (5e-3 if io_dtype == torch.float32 else 2e-2)
+    assert float((got.float() - tile.float()).abs().max()) <= tile_tol
 
 
 def test_wide_prefill_negative_pages_and_strided_views(device, monkeypatch):
@@ -212,6 +216,22 @@ def test_wide_prefill_negative_pages_and_strided_views(device, monkeypatch):
     want = oracle.paged_attention(q[1:].cpu().contiguous(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists[1:],
                                   b.seq_lens[1:], b.cur_lens[1:], nthreads=NTHREADS)
     assert max_err(got[1:], want) <= 2e-2
+
+
+def test_large_prefill_fp32_sampled_parity(device):
+    """The large-prefill workload with fp32 KV (the wide fp32 kernel at this size): one request x
+    four heads against the oracle within 1e-4."""
+    b = workloads.large_prefill(seed=1, device=device, kv_dtype=torch.float32)
+    out = paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    r = 3
+    ids = torch.tensor(b.block_lists[r], device=device, dtype=torch.long)
+    k = b.k_pool.index_select(0, ids)[:, :4].contiguous().cpu()
+    v = b.v_pool.index_select(0, ids)[:, :4].contiguous().cpu()
+    want = oracle.paged_attention(b.q[r:r + 1, :4].cpu(), k, v, [list(range(len(b.block_lists[r])))],
+                                  [b.seq_lens[r]], [b.cur_lens[r]], nthreads=NTHREADS)
+    err = max_err(out[r:r + 1, :4], want)
+    print(f"large fp32 prefill request {r}: max err {err:.2e}", flush=True)
+    assert err <= 1e-4
 
 
 def test_large_prefill_sampled_parity(device):
