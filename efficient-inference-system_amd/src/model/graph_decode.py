@@ -82,19 +82,31 @@ def _signature(pools) -> tuple:
     return tuple(sig)
 
 
-def _lockstep(kv_caches: list[BatchedPagedKVCache]) -> bool:
-    """True when all layers hold identical states and pools (so allocations stay identical)."""
+def _lockstep(kv_caches: list[BatchedPagedKVCache], max_new_blocks: int) -> bool:
+    """True when all layers hold identical states and pools, so this step's allocations are the
+    same in every layer and one metadata pack serves them all. Block lists are compared whole;
+    of the free lists, the lengths and the last max_new_blocks ids: a step pops at most that many
+    ids from the end of each list (LIFO), and deeper ids are compared in a later step before they
+    can be popped (releases push onto the end)."""
     first = kv_caches[0]
     p0 = first.pool
     if p0.k_blocks is None:
         return False
+    f0 = p0.free_block_ids
+    n0 = len(f0)
+    tail0 = f0[n0 - max_new_blocks:] if max_new_blocks < n0 else f0
+    states0 = first.states
     for cache in kv_caches[1:]:
         p = cache.pool
-        if p.k_blocks is None or p.capacity_blocks != p0.capacity_blocks or p.free_block_ids != p0.free_block_ids:
+        if p.k_blocks is None or p.capacity_blocks != p0.capacity_blocks:
             return False
-        if len(cache.states) != len(first.states):
+        f = p.free_block_ids
+        if len(f) != n0 or (f[n0 - max_new_blocks:] if max_new_blocks < n0 else f) != tail0:
             return False
-        for a, b in zip(cache.states, first.states):
+        states = cache.states
+        if len(states) != len(states0):
+            return False
+        for a, b in zip(states, states0):
             if a.seq_len != b.seq_len or a.block_ids != b.block_ids:
                 return False
     return True
@@ -131,21 +143,23 @@ class GraphedStep:
         self.model = model
         self.captured: dict[tuple[int, int], _Captured] = {}
         self.captures = 0
+        self._attns = None
 
     def usable(self, input_ids: torch.Tensor, kv_caches) -> bool:
         m = self.model
-        return (
-            graphs_enabled()
-            and input_ids.is_cuda
-            and input_ids.dim() == 2
-            and bucket_for(input_ids.shape[1]) is not None
-            and not m.training
-            and m.attention_backend == "hip_paged"
-            and all(b.attn.attention_backend == "hip_paged" for b in m.blocks)
-            and isinstance(kv_caches, list) and len(kv_caches) == len(m.blocks)
-            and all(isinstance(c, BatchedPagedKVCache) for c in kv_caches)
-            and _lockstep(kv_caches)
-        )
+        if self._attns is None or len(self._attns) != len(m.blocks):
+            self._attns = [b.attn for b in m.blocks]  # plain attribute reads below, per call
+        if not (graphs_enabled() and input_ids.is_cuda and input_ids.dim() == 2 and not m.training
+                and m.attention_backend == "hip_paged"
+                and all(a.attention_backend == "hip_paged" for a in self._attns)
+                and isinstance(kv_caches, list) and len(kv_caches) == len(self._attns)
+                and all(isinstance(c, BatchedPagedKVCache) for c in kv_caches)):
+            return False
+        B, T = input_ids.shape
+        if bucket_for(T) is None:
+            return False
+        # a request appending up to T tokens opens at most ceil(T / block) + 1 new blocks
+        return _lockstep(kv_caches, B * (-(-T // m.kv_block_size) + 1))
 
     # ------------------------------------------------------------------------------------------
     def _static_forward(self, cap: _Captured, pools) -> torch.Tensor:

@@ -201,3 +201,34 @@ def test_storage_reuse_starts_from_zeroed_blocks():
     assert second.k_blocks.data_ptr() == ptr
     assert float(second.k_blocks.abs().sum()) == 0.0 and float(second.v_blocks.abs().sum()) == 0.0
     assert second.free_block_ids == [0, 1, 2, 3] and second.capacity_blocks == 4
+
+
+def test_graph_lockstep_check():
+    """The graph step's lockstep test over per-layer caches: identical layers pass; a different
+    block list, free-list length or free-list tail (the ids a step may pop) fails; a difference
+    deeper in the free lists than the step can reach is left to later steps."""
+    from src.model.graph_decode import _lockstep
+
+    def layer():
+        pool = LayerBlockPool(block_size=4, initial_blocks=32, growth_factor=2.0)
+        states = [PagedKVCacheState(pool=pool), PagedKVCacheState(pool=pool)]
+        batch = BatchedPagedKVCache(states=states, pool=pool)
+        k = torch.zeros(2, 1, 6, 2)
+        batch.append_batch(k, k.clone(), current_lengths=[6, 3])
+        return batch
+
+    layers = [layer() for _ in range(3)]
+    assert _lockstep(layers, 4)
+    free = layers[2].pool.free_block_ids
+    free[0], free[1] = free[1], free[0]  # deep in the list: no step of <= 4 pops reaches it
+    assert _lockstep(layers, 4)
+    assert not _lockstep(layers, len(free))  # a step that could pop every id sees the difference
+    free[0], free[1] = free[1], free[0]
+    free[-1], free[-2] = free[-2], free[-1]  # the next ids to be popped differ
+    assert not _lockstep(layers, 4)
+    free[-1], free[-2] = free[-2], free[-1]
+    layers[1].states[0].block_ids[0] += 1
+    assert not _lockstep(layers, 4)
+    layers[1].states[0].block_ids[0] -= 1
+    layers[1].pool.free_block_ids.pop()
+    assert not _lockstep(layers, 4)
