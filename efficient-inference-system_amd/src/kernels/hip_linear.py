@@ -71,8 +71,10 @@ def qkv_append_hip(x: torch.Tensor, ln: nn.LayerNorm, attn, k_pool: torch.Tensor
     if out is None:
         out = torch.empty((M, D), dtype=torch.float32, device=x.device)
     nblk, H, bs, Hd = k_pool.shape
-    if slot_mapping.dtype != torch.int32 or slot_mapping.numel() < M:
-        raise ValueError("slot_mapping must be int32 with one entry per row")
+    if slot_mapping.dtype != torch.int32 or slot_mapping.numel() < M or not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be a contiguous int32 tensor with one entry per row")
+    if k_pool.shape != v_pool.shape or k_pool.dtype != v_pool.dtype or not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("K/V pools must be contiguous with equal shapes and dtypes")
     status = _lib.load().pa_qkv_append(
         x.data_ptr(), x.stride(0), M, D,
         _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
@@ -92,6 +94,11 @@ def embed_rows_hip(ids: torch.Tensor, pos_start: torch.Tensor, token_emb: nn.Emb
     """[B*T, d] rows token_emb(ids[b, t]) + pos_emb(min(pos_start[b] + t, max_pos - 1))."""
     if ids.dtype != torch.int64 or pos_start.dtype != torch.int64 or not ids.is_contiguous():
         raise ValueError("ids and pos_start must be int64 (ids contiguous [B, T])")
+    if not (pos_start.is_contiguous() and pos_start.numel() == ids.shape[0]):
+        raise ValueError("pos_start must be a contiguous [B] tensor")
+    for name, t in (("token_emb", token_emb.weight), ("pos_emb", pos_emb.weight)):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} weight must be a contiguous float32 table")
     B, T = ids.shape
     d = token_emb.embedding_dim
     if out is None:

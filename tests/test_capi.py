@@ -71,3 +71,33 @@ def test_argument_errors_are_reported_without_a_device(lib):
     # zero-sized work is a no-op success
     assert lib.pa_prefill(None, 0, 0, 0, None, 0, 0, 0, 0, None, None, 0, 0, None, 0, 0, None, None,
                           0, 8, 4, 64, 16, 1.0, 0, None, 0, None) == _lib.PA_OK
+
+
+def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
+    """pa_linear_rows / pa_qkv_append / pa_embed_rows reject bad arguments before any HIP call
+    (the pointers below are never dereferenced: every case fails or returns on the host)."""
+    A = 0x10000  # a 16-byte aligned stand-in address
+    lin = lib.pa_linear_rows
+    # more than 64 rows
+    assert lin(A, 512, 65, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"rows must be in [0, 64]" in lib.pa_last_error_message()
+    # unknown activation
+    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 2, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # misaligned activations
+    assert lin(A + 4, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # LayerNorm weight without bias
+    assert lin(A, 512, 4, 512, A, None, 512, A, None, 1e-5, 0, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # in_features without a kernel
+    assert lin(A, 96, 4, 96, A, None, 32, None, None, 0.0, 0, None, 0, A, 32, None) == _lib.PA_ERR_UNSUPPORTED
+    assert b"in_features" in lib.pa_last_error_message()
+    # no rows: nothing to do
+    assert lin(None, 0, 0, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 0, None) == _lib.PA_OK
+    # q/k/v: d_model must be heads x head_dim
+    qkv = lib.pa_qkv_append
+    assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 32, 16,
+               None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"d_model" in lib.pa_last_error_message()
+    # embedding rows must be whole 16-byte vectors
+    emb = lib.pa_embed_rows
+    assert emb(A, A, 2, 3, A, 100, A, 64, 6, A, 8, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert emb(A, A, 0, 3, A, 100, A, 64, 8, A, 8, None) == _lib.PA_OK
