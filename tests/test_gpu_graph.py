@@ -80,3 +80,40 @@ def test_graph_decode_matches_eager(device, monkeypatch):
     for re_, rg in zip(per["eager"], per["graph"]):
         for se, sg in zip(re_, rg):
             assert se.block_ids == sg.block_ids and se.seq_len == sg.seq_len
+
+
+def test_graph_decode_bf16_kv_cache_matches_eager(device, monkeypatch):
+    """A model whose pools store bf16 KV (kv_cache_dtype) through the fused decode kernels (K/V
+    rounded to bf16 by the q/k/v + append launch) against the eager forward (torch projections,
+    then the append kernel's rounding): logits within 1e-2 (the two fp32 projections may round a
+    K/V element to neighbouring bf16 values)."""
+    def build():
+        torch.manual_seed(3)
+        return TinyTransformerLM(vocab_size=300, d_model=256, num_heads=4, num_layers=2, d_ff=512, max_seq_len=256,
+                                 attention_backend="hip_paged", kv_block_size=16, kv_pool_initial_blocks=8,
+                                 kv_cache_dtype=torch.bfloat16).to(device).eval()
+    eager, graphed = build(), build()
+    graphed.load_state_dict(eager.state_dict())
+    B = 4
+    prompt = torch.randint(0, 300, (B, 30), device=device)
+    per = {}
+    with torch.no_grad():
+        for name, m in (("eager", eager), ("graph", graphed)):
+            monkeypatch.setenv("PAGED_HIP_GRAPHS", "0")
+            _, caches = m(prompt, use_cache=True, position_offset=0, current_lengths=30)
+            per[name] = [[c.states[r] for c in caches] for r in range(B)]
+        assert graphed.layer_block_pools[0].k_blocks.dtype == torch.bfloat16
+        pos = torch.full((B,), 30, device=device)
+        tok = torch.randint(0, 300, (B, 1), device=device)
+        for step in range(20):
+            outs = {}
+            for name, m in (("eager", eager), ("graph", graphed)):
+                monkeypatch.setenv("PAGED_HIP_GRAPHS", "0" if name == "eager" else "1")
+                logits, _ = m(tok, kv_caches=stack(per[name], list(range(B))), use_cache=True, position_offset=pos)
+                outs[name] = logits
+            err = (outs["eager"] - outs["graph"]).abs().max().item()
+            assert err <= 1e-2, (step, err)
+            pos += 1
+            tok = torch.randint(0, 300, (B, 1), device=device)
+    assert graphed._graph_step is not None and graphed._graph_step.captures >= 1
+    assert any(c.fused for c in graphed._graph_step.captured.values()), "the fused decode kernels were not used"
