@@ -31,6 +31,11 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Keep the compiler from forming packed fp32 instructions (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs instead of AGPRs: with AGPR accumulators the prefill
+    # kernels copied their 64 output accumulators between the two register files every KV step
+    # (around the lazy-rescale branch) and needed 244-296 registers; in VGPR form no copies and
+    # 146-212 registers (large prefill: bf16 417 -> 371 us, fp32 2018 -> 1908 us; others equal).
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 
