@@ -10,6 +10,7 @@
 namespace pa {
 
 constexpr int kWave = 64;
+constexpr int kXcds = 8;  // MI355X: 8 accelerator dies, each with its own L2; workgroup x runs on die x % 8
 constexpr float kLog2e = 1.4426950408889634f;
 // Finite "minus infinity" for running maxima: exp2(kNegBig - x) is 0 for any real x, and
 // exp2(kNegBig - kNegBig) is 1, so an empty state merges without producing NaN.

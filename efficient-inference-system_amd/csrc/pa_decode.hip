@@ -32,8 +32,6 @@
 
 namespace pa {
 
-constexpr int kXcds = 8;  // MI355X: 8 accelerator dies; workgroup x runs on die x % 8
-
 template <bool NT>
 __device__ __forceinline__ u32x4 load16(const u32x4* p) {
   if constexpr (NT) return __builtin_nontemporal_load(p);

@@ -13,11 +13,16 @@
 //   online softmax   lane (G2, c) = (lane / 32, lane % 32) holds query c's scores for keys
 //                    8j + 4*G2 + r (j, r < 4), so the row max / sum are 16 registers plus one
 //                    v_permlane32_swap;
-//   O^T += V^T P^T   the softmax weights of chunk mc (keys 16mc..16mc+15) are, as held, the B
-//                    operand of one MFMA per 32-row output tile (k slot (G2, e) = key
-//                    8*(2mc + e/4) + 4*G2 + e%4). Output tile u row R holds head_dim index
-//                    R*HD/32 + u, so each lane reads HD/32 contiguous values of each of its 16
-//                    key rows from LDS and the A operands are assembled in registers.
+//   O^T += V^T P^T   two MFMAs (mm = 0, 1) per 32-row output tile and 32 keys; the B operand
+//                    is the softmax weights as held, k slot (G2, 2q + hf) = key
+//                    8mm + 4*G2 + q + 16hf (registers 4mm + q and 4mm + 8 + q). Output tile d
+//                    row R is head_dim index 32d + R. V is stored in LDS transposed (one row of
+//                    the step's keys per head_dim index), word 16u + k of a row holding keys
+//                    32u + k and 32u + 16 + k, so the eight keys of slots (G2, 0..7) are four
+//                    adjacent words: each A operand is one 16-byte LDS read. The transpose is
+//                    done once per step by the whole workgroup while storing (a thread packs two
+//                    keys' values of 8 head_dim indices into 8 words with v_perm_b32), not by
+//                    every wavefront on every operand.
 // The QK^T contraction slot (G2, e) of MFMA s is head_dim index G2*HD/2 + 8s + e. A and B of each
 // product use the same slot map, so results do not depend on the hardware's k ordering.
 // Rounding matches the 16-row bf16 kernel: q*scale and the softmax weights are rounded to bf16
@@ -45,6 +50,20 @@ constexpr float kRescaleSlack = 8.f;
 constexpr int kWideWaves = 4;
 constexpr int kWideRows = kWideWaves * 32;  // query rows per workgroup
 
+// Workgroup -> (request, head) pair and query tile. The ntiles workgroups of one pair read the
+// same K/V blocks, and workgroup x runs on die x % kXcds (each die has its own L2), so they take
+// indices congruent modulo kXcds: groups of kXcds pairs own kXcds * ntiles consecutive indices,
+// tile-major, heaviest (last) tile first. The last group may hold fewer pairs.
+__device__ __forceinline__ void wide_unit(int x, int BH, int ntiles, int& bh, int& qt) {
+  const int g = x / (kXcds * ntiles);
+  const int r = x - g * kXcds * ntiles;
+  const int rest = BH - g * kXcds;
+  const int m = rest < kXcds ? rest : kXcds;
+  const int t = r / m;
+  bh = g * kXcds + (r - t * m);
+  qt = ntiles - 1 - t;
+}
+
 // NSUB = 32-key sub-tiles per step: the per-step costs (barrier, mask test, max/sum exchange,
 // lazy-rescale test) are paid once per NSUB * 32 keys. Measured on the large-prefill workload
 // (8 x 32 heads, chunk 512 over 1.8-3.7k contexts), same box: head_dim 128 460 us with NSUB 1,
@@ -61,14 +80,17 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   constexpr int QH = HD / 2;             // head_dim values per lane in the QK^T operands
   constexpr int NQ = HD / 16;            // QK^T MFMAs per sub-tile (k = 16 each)
   constexpr int DU = HD / 32;            // output tiles of 32 head_dim rows
-  constexpr int RS = HD + 8;             // LDS row stride in bf16 elements (16-byte pad)
+  constexpr int RS = HD + 8;             // K tile row stride in bf16 elements (16-byte pad)
+  constexpr int RST = KS + 8;            // V^T tile row stride (16-byte pad)
   constexpr int RPC = HD / 8;            // 16-byte chunks per key row
-  constexpr int CPT = KS * RPC / (NW * kWave);  // chunks per thread per K (or V) step tile
+  constexpr int CPT = KS * RPC / (NW * kWave);  // K chunks per thread per step
   static_assert(CPT >= 1 && KS * RPC == CPT * NW * kWave, "tile split");
-  constexpr int VW = DU / 2 > 0 ? DU / 2 : 1;     // 32-bit words per key row per lane (V reads)
+  constexpr int VCW = RPC / 4;           // wavefronts per 32-key sub-tile when staging V
+  static_assert(VCW >= 1 && NSUB * VCW == NW, "V tile split");
+  static_assert(16 * RPC >= 2 * kWave && (NW * kWave) % (16 * RPC) == 0, "K chunk blocks");
 
   __shared__ __attribute__((aligned(16))) uint16_t sk[2][KS * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t sv[2][KS * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t sv[2][HD * RST];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -76,9 +98,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   const int c = lane & 31;
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
-  const int unit = blockIdx.x;
-  const int qt = ntiles - 1 - unit % ntiles;  // heaviest (last) tiles of each (request, head) first
-  const int bh = unit / ntiles;
+  int bh, qt;
+  wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int i0 = qt * kWideRows;
@@ -126,26 +147,40 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   const uint16_t* kpool = static_cast<const uint16_t*>(a.k_pool);
   const uint16_t* vpool = static_cast<const uint16_t*>(a.v_pool);
   const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
-  auto ok_blk = [&](int e) { return e >= 0 && e < a.num_blocks; };
+  // Page-table entries are int32: one unsigned 32-bit compare checks 0 <= e < num_blocks.
+  const uint32_t nblk = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
+  auto ok_blk = [&](int e) { return (uint32_t)e < nblk; };
 
-  // Cooperative global loads of one step's K and V tiles (thread t: chunks t + 256n); the step's
-  // page-table entries are kept for its compute (-1 past the request's blocks).
-  u32x4 kr[CPT], vr[CPT];
+  // Cooperative global loads of one step's K and V tiles; the step's page-table entries are kept
+  // for its compute (-1 past the request's blocks). Each load instruction of a wavefront reads
+  // one KV block, so its address is a per-wavefront block base plus a fixed lane offset.
+  //   K: thread t loads chunk t + 256n of the step tile (key row, 8 head_dim indices): lane
+  //      offset 8 * (t mod 16*RPC) elements in block (64w + 256n) / (16*RPC).
+  //   V: wavefront w stages sub-tile vu = w / VCW, head_dim chunk vcc = 4 (w mod VCW) + lane/16,
+  //      keys 32vu + vk and 32vu + 16 + vk (vk = lane mod 16) of blocks 2vu and 2vu + 1.
+  const uint32_t klo = 8u * (threadIdx.x % (16 * RPC));
+  const int vu = w / VCW;
+  const int vcc = 4 * (w - vu * VCW) + (lane >> 4);
+  const int vk = lane & 15;
+  const uint32_t vlo = (uint32_t)(vk * HD + 8 * vcc);
+  u32x4 kr[CPT], vr[2];
+  auto block_base = [&](const uint16_t* pool, int e) {
+    const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
+    return pool + ((int64_t)blk * a.H + h) * (16 * HD);
+  };
   auto gload = [&](int st, int (&ent)[NBS]) {
 #pragma unroll
     for (int j = 0; j < NBS; ++j) ent[j] = NBS * st + j < nb ? pt[NBS * st + j] : -1;
 #pragma unroll
     for (int n = 0; n < CPT; ++n) {
-      const int q = threadIdx.x + n * NW * kWave;
-      const int kk = q / RPC;
-      const int col = (q - kk * RPC) * 8;
-      const int e = ent[kk >> 4];
-      const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
-      const int64_t off = (((int64_t)blk * a.H + h) * 16 + (kk & 15)) * HD + col;
-      kr[n] = *reinterpret_cast<const u32x4*>(kpool + off);
-      vr[n] = *reinterpret_cast<const u32x4*>(vpool + off);
+      const int kb = (kWave * w + NW * kWave * n) / (16 * RPC);
+      kr[n] = *reinterpret_cast<const u32x4*>(block_base(kpool, ent[kb]) + klo);
     }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) vr[x] = *reinterpret_cast<const u32x4*>(block_base(vpool, ent[2 * vu + x]) + vlo);
   };
+  // V^T rows (one per head_dim index): word 16u + k (k < 16) of sub-tile u holds keys 32u + k
+  // (low half) and 32u + 16 + k (high half).
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int n = 0; n < CPT; ++n) {
@@ -153,7 +188,12 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
       const int kk = q / RPC;
       const int col = (q - kk * RPC) * 8;
       *reinterpret_cast<u32x4*>(&sk[buf][kk * RS + col]) = kr[n];
-      *reinterpret_cast<u32x4*>(&sv[buf][kk * RS + col]) = vr[n];
+    }
+    uint16_t* vt = &sv[buf][8 * vcc * RST + 32 * vu + 2 * vk];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t wd = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
+      *reinterpret_cast<uint32_t*>(vt + e * RST) = wd;
     }
   };
 
@@ -172,23 +212,13 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + u * 32 * RS + 8 * s);
         sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s], sacc[u], 0, 0, 0);
       }
-    // ---- online softmax (sub-tile u, keys 32u + 8j + 4*G2 + r of this step) -------------------
+    // ---- online softmax (sub-tile u, keys 32u + 8j + 4*G2 + r of this step), in place --------
     bool all_ok = true;
 #pragma unroll
     for (int j = 0; j < NBS; ++j) all_ok = all_ok && ok_blk(ent[j]);
     // Interior steps (every block valid, every key below every row's limit) need no mask.
     const bool full = all_ok && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
-    float p[NSUB][16];
-    float mloc = -INFINITY;
-    if (full) {
-#pragma unroll
-      for (int u = 0; u < NSUB; ++u)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          p[u][e] = sacc[u][e];
-          mloc = fmaxf(mloc, p[u][e]);
-        }
-    } else {
+    if (!full) {
       const int t0 = st * KS + 4 * G2;
 #pragma unroll
       for (int u = 0; u < NSUB; ++u)
@@ -198,11 +228,15 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = t0 + 32 * u + 8 * j + r;
-            p[u][4 * j + r] = (okb && t < n_c) ? sacc[u][4 * j + r] : -INFINITY;
-            mloc = fmaxf(mloc, p[u][4 * j + r]);
+            sacc[u][4 * j + r] = (okb && t < n_c) ? sacc[u][4 * j + r] : -INFINITY;
           }
         }
     }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sacc[u][e]);
     mloc = max_xor32(mloc);
     const bool grow = mloc > m + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -218,47 +252,28 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
     for (int u = 0; u < NSUB; ++u)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        p[u][e] = fast_exp2(p[u][e] - m);
-        ps += p[u][e];
+        sacc[u][e] = fast_exp2(sacc[u][e] - m);
+        ps += sacc[u][e];
       }
     l += sum_xor32(ps);
-    // ---- O^T += V^T P^T, per sub-tile ---------------------------------------------------------
+    // ---- O^T += V^T P^T, per sub-tile: MFMA mm contracts keys 8mm + 4*G2 + q + 16hf at slot
+    // (G2, 2q + hf), i.e. registers 4mm + q and 4mm + 8 + q of the lane ------------------------
 #pragma unroll
-    for (int u2 = 0; u2 < NSUB; ++u2) {
-      // V values of this lane's 16 key rows of the sub-tile, head_dim [c*DU, c*DU + DU).
-      uint32_t vf[16][VW];
+    for (int u2 = 0; u2 < NSUB; ++u2)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint16_t* vp = &sv[buf][(32 * u2 + 8 * j + 4 * G2 + r) * RS + c * DU];
-          if constexpr (DU == 4) {
-            const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
-            vf[4 * j + r][0] = x[0];
-            vf[4 * j + r][1] = x[1];
-          } else {
-            vf[4 * j + r][0] = *reinterpret_cast<const uint32_t*>(vp);
-          }
-        }
-#pragma unroll
-      for (int mc = 0; mc < 2; ++mc) {
+      for (int mm = 0; mm < 2; ++mm) {
         uint32_t pw[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(p[u2][8 * mc + 2 * q], p[u2][8 * mc + 2 * q + 1]);
+        for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(sacc[u2][4 * mm + q], sacc[u2][4 * mm + 8 + q]);
         const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
+        // A: V^T row 32d + c, words 16u2 + 8mm + 4*G2 .. +3
+        const uint16_t* vrow = &sv[buf][c * RST + 32 * u2 + 16 * mm + 8 * G2];
 #pragma unroll
         for (int d = 0; d < DU; ++d) {
-          uint32_t aw[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t x0 = vf[8 * mc + 2 * q][d >> 1], x1 = vf[8 * mc + 2 * q + 1][d >> 1];
-            aw[q] = (d & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
-          }
-          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, (u32x4{aw[0], aw[1], aw[2], aw[3]})), pb, oacc[d], 0, 0, 0);
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vrow + 32 * d * RST);
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[d], 0, 0, 0);
         }
       }
-    }
   };
 
   if (nsteps > 0) {
@@ -277,18 +292,16 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
     }
   }
 
-  // ---- write: lane holds O^T rows 8j + 4*G2 + r (head_dim R*DU + u) of query column c ---------
+  // ---- write: lane holds O^T rows 8j + 4*G2 + r (head_dim 32d + row) of query column c -------
   if (i >= a.T) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_st;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int d = 0; d < DU; ++d)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int R = 8 * j + 4 * G2 + r;
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int u = 0; u < DU; ++u) Elem<IO>::store(op + R * DU + u, oacc[u][4 * j + r] * inv);
-    }
+      for (int r = 0; r < 4; ++r) Elem<IO>::store(op + 32 * d + 8 * j + 4 * G2 + r, oacc[d][4 * j + r] * inv);
 }
 
 // fp32 KV: the same workgroup layout, LDS staging and online softmax, on v_mfma_f32_32x32x2_f32
@@ -322,9 +335,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   const int c = lane & 31;
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
-  const int unit = blockIdx.x;
-  const int qt = ntiles - 1 - unit % ntiles;
-  const int bh = unit / ntiles;
+  int bh, qt;
+  wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int i0 = qt * kWideRows;
@@ -366,7 +378,9 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   const float* kpool = static_cast<const float*>(a.k_pool);
   const float* vpool = static_cast<const float*>(a.v_pool);
   const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
-  auto ok_blk = [&](int e) { return e >= 0 && e < a.num_blocks; };
+  // Page-table entries are int32: one unsigned 32-bit compare checks 0 <= e < num_blocks.
+  const uint32_t nblk = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
+  auto ok_blk = [&](int e) { return (uint32_t)e < nblk; };
 
   u32x4 kr[CPT], vr[CPT];
   auto gload = [&](int st, int (&ent)[NBS]) {
