@@ -64,6 +64,44 @@ __device__ __forceinline__ void wide_unit(int x, int BH, int ntiles, int& bh, in
   qt = ntiles - 1 - t;
 }
 
+// Longest-first order: the (request, query tile) units sorted by descending work (the valid keys
+// of the tile's last row; ties by unit index), heads innermost, so the longest tiles start first
+// and the short ones fill the end of the grid (contexts of different lengths otherwise leave a
+// tail of long tiles running alone). Every workgroup ranks the units itself, one per thread, using
+// `lds` (kWideWaves * kWave + 1 ints) as scratch. Returns false when there are more units than
+// threads; the caller then keeps wide_unit's order.
+constexpr int kOrderMax = kWideWaves * kWave;
+__device__ __forceinline__ bool wide_lpt_unit(const AttnArgs& a, int ntiles, int* lds, int& bh, int& qt) {
+  const int U = a.B * ntiles;
+  if (U > kOrderMax) return false;
+  const int tid = threadIdx.x;
+  int key = 0;
+  if (tid < U) {
+    const int b = tid / ntiles;
+    const int t = tid - b * ntiles;
+    const int last = t * kWideRows + kWideRows - 1 < a.T - 1 ? t * kWideRows + kWideRows - 1 : a.T - 1;
+    key = valid_keys(a.seq_lens[b], a.cur_lens[b], last);
+    lds[tid] = key;
+  }
+  __syncthreads();
+  const int pos = blockIdx.x / a.H;
+  if (tid < U) {
+    int rank = 0;
+    for (int u = 0; u < U; ++u) {
+      const int k2 = lds[u];
+      rank += (k2 > key) || (k2 == key && u < tid);
+    }
+    if (rank == pos) lds[kOrderMax] = tid;
+  }
+  __syncthreads();
+  const int unit = __builtin_amdgcn_readfirstlane(lds[kOrderMax]);
+  __syncthreads();  // the scratch is reused by the caller
+  const int b = unit / ntiles;
+  qt = unit - b * ntiles;
+  bh = b * a.H + (blockIdx.x - pos * a.H);
+  return true;
+}
+
 // NSUB = 32-key sub-tiles per step: the per-step costs (barrier, mask test, max/sum exchange,
 // lazy-rescale test) are paid once per NSUB * 32 keys. Measured on the large-prefill workload
 // (8 x 32 heads, chunk 512 over 1.8-3.7k contexts), same box: head_dim 128 460 us with NSUB 1,
@@ -99,7 +137,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
   int bh, qt;
-  wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
+  static_assert(sizeof(sk) >= (kOrderMax + 1) * sizeof(int), "order scratch");
+  if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(&sk[0][0]), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int i0 = qt * kWideRows;
@@ -336,7 +375,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
   int bh, qt;
-  wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
+  static_assert(sizeof(sk) >= (kOrderMax + 1) * sizeof(int), "order scratch");
+  if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(&sk[0][0]), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int i0 = qt * kWideRows;

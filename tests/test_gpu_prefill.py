@@ -196,6 +196,26 @@ def test_wide_prefill_forced_small(device, monkeypatch, head_dim, io_dtype, kv_d
     assert float((got.float() - tile.float()).abs().max()) <= tile_tol
 
 
+@pytest.mark.parametrize("B,kv_dtype", [(40, torch.bfloat16), (90, torch.bfloat16), (90, torch.float32)])
+def test_wide_prefill_work_orders(device, monkeypatch, B, kv_dtype):
+    """Many ragged requests: with B * tiles <= 256 (40 x 3) every workgroup ranks the (request,
+    tile) units longest-first; above (90 x 3) the kernel keeps its fixed order. Every request and
+    head must be computed exactly once either way: against the oracle and the 16-row kernel."""
+    g = torch.Generator().manual_seed(B)
+    ctx = torch.randint(0, 200, (B,), generator=g).tolist()
+    curs = torch.randint(0, 301, (B,), generator=g).tolist()
+    b = make_prefill(device, 33 + B, ctx, curs, T=300, H=2, Hd=64, kv_dtype=kv_dtype)
+    print(f"wide prefill work order B={B} kv={kv_dtype}", flush=True)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "wide")
+    got = run(b)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "tile")
+    tile = run(b)
+    want = oracle_out(b)
+    tol, tile_tol = (2e-2, 5e-3) if kv_dtype == torch.bfloat16 else (1e-4, 1e-5)
+    assert max_err(got, want) <= tol
+    assert float((got - tile).abs().max()) <= tile_tol
+
+
 def test_wide_prefill_negative_pages_and_strided_views(device, monkeypatch):
     """A -1 page entry skips its 16 keys in the wide kernel as in the 16-row kernel; q/out are
     the model's transposed views; the untouched request matches the oracle."""
