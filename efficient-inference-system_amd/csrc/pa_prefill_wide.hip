@@ -3,9 +3,10 @@
 //
 // One workgroup of 4 wavefronts per (request, head, tile of 128 query rows); wavefront w owns
 // rows 32w..32w+31 of the tile. The workgroup walks the KV blocks in steps of 32 keys (head_dim
-// 128) or 64 keys (head_dim 64): each step's K and V tiles are loaded from HBM once,
-// cooperatively, into double-buffered LDS (the next step's global loads and page-table entries
-// are in flight while the current step is computed), and all four wavefronts read them there.
+// 128) or 64 keys (head_dim 64). Each step's K and V tiles go from HBM straight into LDS with
+// LDS-direct loads (global_load_lds_dwordx4, no staging registers), 2 (head_dim 128) or 1
+// (head_dim 64) steps ahead of their use in a 3- or 2-stage ring; all four wavefronts read them
+// there.
 //
 // Per step and wavefront, with v_mfma_f32_32x32x16_bf16 (fp32 accumulation):
 //   S^T = K Q^T      32 keys x 32 queries; A = K rows from LDS, B = the wavefront's q (bf16,
@@ -13,16 +14,14 @@
 //   online softmax   lane (G2, c) = (lane / 32, lane % 32) holds query c's scores for keys
 //                    8j + 4*G2 + r (j, r < 4), so the row max / sum are 16 registers plus one
 //                    v_permlane32_swap;
-//   O^T += V^T P^T   two MFMAs (mm = 0, 1) per 32-row output tile and 32 keys; the B operand
-//                    is the softmax weights as held, k slot (G2, 2q + hf) = key
-//                    8mm + 4*G2 + q + 16hf (registers 4mm + q and 4mm + 8 + q). Output tile d
-//                    row R is head_dim index 32d + R. V is stored in LDS transposed (one row of
-//                    the step's keys per head_dim index), word 16u + k of a row holding keys
-//                    32u + k and 32u + 16 + k, so the eight keys of slots (G2, 0..7) are four
-//                    adjacent words: each A operand is one 16-byte LDS read. The transpose is
-//                    done once per step by the whole workgroup while storing (a thread packs two
-//                    keys' values of 8 head_dim indices into 8 words with v_perm_b32), not by
-//                    every wavefront on every operand.
+//   O^T += V^T P^T   two MFMAs (mm = 0, 1) per 32-row output tile and 32 keys; the B operand is
+//                    the softmax weights as held (registers 8mm..8mm+7 = keys 16mm + 8jj + 4*G2
+//                    + r at k slot (G2, 4jj + r)). Output tile d row R is head_dim index 32d + R.
+//                    The A operand (V^T, row = head_dim) is read from the key-major V tile with
+//                    two ds_read_b64_tr_b16 (LDS transposing reads): no transposition in
+//                    registers.
+// LDS tiles are unpadded key rows; their 16-byte chunks are XOR-swizzled per row so that both
+// operand reads use every LDS bank once per pass.
 // The QK^T contraction slot (G2, e) of MFMA s is head_dim index G2*HD/2 + 8s + e. A and B of each
 // product use the same slot map, so results do not depend on the hardware's k ordering.
 // Rounding matches the 16-row bf16 kernel: q*scale and the softmax weights are rounded to bf16
@@ -62,6 +61,26 @@ __device__ __forceinline__ void wide_unit(int x, int BH, int ntiles, int& bh, in
   const int t = r / m;
   bh = g * kXcds + (r - t * m);
   qt = ntiles - 1 - t;
+}
+
+// One LDS-direct load (global_load_lds_dwordx4): lane L reads 16 bytes at base + voff and writes
+// them to LDS byte address lds + 16L (lds is the wavefront-uniform M0). Issued as inline
+// assembly so that the compiler does not track it: it would otherwise wait for every such load
+// before any LDS read, also for loads into stages that the read does not touch. The caller
+// waits for these loads itself (s_waitcnt vmcnt) before the barrier that publishes their stage.
+__device__ __forceinline__ void lds_direct_load16(const void* base, uint32_t voff, const void* lds) {
+  const uint32_t m0 = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m0));
+}
+
+// A 4-byte global load that has completed on return (load and s_waitcnt vmcnt(0) in one
+// assembly block, untracked by the compiler like lds_direct_load16: its own wait for a tracked
+// load would be placed before every later use of the register, draining the LDS-direct loads in
+// flight each time).
+__device__ __forceinline__ int load_now(const int32_t* p) {
+  int v;
+  asm volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+  return v;
 }
 
 // Longest-first order: the (request, query tile) units sorted by descending work (the valid keys
@@ -104,13 +123,22 @@ __device__ __forceinline__ bool wide_lpt_unit(const AttnArgs& a, int ntiles, int
 
 // NSUB = 32-key sub-tiles per step: the per-step costs (barrier, mask test, max/sum exchange,
 // lazy-rescale test) are paid once per NSUB * 32 keys. Measured on the large-prefill workload
-// (8 x 32 heads, chunk 512 over 1.8-3.7k contexts), same box: head_dim 128 460 us with NSUB 1,
-// 536 us with 2 (308 registers: one wavefront per SIMD), 516 us with 4; head_dim 64 266 us with 1,
-// 243 us with 2, 340 us with 4.
+// (8 x 32 heads, chunk 512 over 1.8-3.7k contexts), same box, head_dim 64: NSUB 2 with 2 stages
+// 133-137 us, with 3 stages 148-150 us (48 KB of LDS: 3 workgroups per CU instead of 4), NSUB 1
+// 140-146 us. Head_dim 128 (NSUB 1, 164 registers: 3 workgroups per CU either way) uses 3 stages.
+#ifndef WIDE_NSUB64
+#define WIDE_NSUB64 2
+#endif
+#ifndef WIDE_NST64
+#define WIDE_NST64 2
+#endif
 template <int HD>
-constexpr int wide_nsub() { return HD == 64 ? 2 : 1; }
+constexpr int wide_nsub() { return HD == 64 ? WIDE_NSUB64 : 1; }
+// LDS stages of K and V tiles (2 or 3): loads are issued NST - 1 steps ahead of their use.
+template <int HD>
+constexpr int wide_stages() { return HD == 64 ? WIDE_NST64 : 3; }
 
-template <typename IO, int HD, int NSUB>
+template <typename IO, int HD, int NSUB, int NST>
 __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const AttnArgs a) {
   constexpr int NW = kWideWaves;
   constexpr int KS = 32 * NSUB;          // keys per step
@@ -118,17 +146,16 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   constexpr int QH = HD / 2;             // head_dim values per lane in the QK^T operands
   constexpr int NQ = HD / 16;            // QK^T MFMAs per sub-tile (k = 16 each)
   constexpr int DU = HD / 32;            // output tiles of 32 head_dim rows
-  constexpr int RS = HD + 8;             // K tile row stride in bf16 elements (16-byte pad)
-  constexpr int RST = KS + 8;            // V^T tile row stride (16-byte pad)
-  constexpr int RPC = HD / 8;            // 16-byte chunks per key row
-  constexpr int CPT = KS * RPC / (NW * kWave);  // K chunks per thread per step
-  static_assert(CPT >= 1 && KS * RPC == CPT * NW * kWave, "tile split");
-  constexpr int VCW = RPC / 4;           // wavefronts per 32-key sub-tile when staging V
-  static_assert(VCW >= 1 && NSUB * VCW == NW, "V tile split");
-  static_assert(16 * RPC >= 2 * kWave && (NW * kWave) % (16 * RPC) == 0, "K chunk blocks");
+  constexpr int CPR = HD / 8;            // 16-byte chunks per key row
+  constexpr int RPI = kWave / CPR;       // key rows per LDS-direct load instruction (1 KB)
+  constexpr int NDMA = KS / (RPI * NW);  // such instructions per wavefront per K (or V) tile
+  static_assert(NDMA >= 1 && NDMA * RPI * NW == KS && 16 % RPI == 0, "tile split");
+  constexpr int RPB = 128 / HD;          // key rows per 256 bytes (one pass over the LDS banks)
+  constexpr int TILE = KS * HD;          // elements per K (or V) tile
 
-  __shared__ __attribute__((aligned(16))) uint16_t sk[2][KS * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t sv[2][HD * RST];
+  static_assert(NST == 2 || NST == 3, "stages");
+  __shared__ __attribute__((aligned(16))) uint16_t sk0[TILE], sk1[TILE], sk2[NST > 2 ? TILE : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t sv0[TILE], sv1[TILE], sv2[NST > 2 ? TILE : 8];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -137,8 +164,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
   int bh, qt;
-  static_assert(sizeof(sk) >= (kOrderMax + 1) * sizeof(int), "order scratch");
-  if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(&sk[0][0]), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
+  static_assert(sizeof(sk0) >= (kOrderMax + 1) * sizeof(int), "order scratch");
+  if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(sk0), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int i0 = qt * kWideRows;
@@ -189,66 +216,80 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   // Page-table entries are int32: one unsigned 32-bit compare checks 0 <= e < num_blocks.
   const uint32_t nblk = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
   auto ok_blk = [&](int e) { return (uint32_t)e < nblk; };
-
-  // Cooperative global loads of one step's K and V tiles; the step's page-table entries are kept
-  // for its compute (-1 past the request's blocks). Each load instruction of a wavefront reads
-  // one KV block, so its address is a per-wavefront block base plus a fixed lane offset.
-  //   K: thread t loads chunk t + 256n of the step tile (key row, 8 head_dim indices): lane
-  //      offset 8 * (t mod 16*RPC) elements in block (64w + 256n) / (16*RPC).
-  //   V: wavefront w stages sub-tile vu = w / VCW, head_dim chunk vcc = 4 (w mod VCW) + lane/16,
-  //      keys 32vu + vk and 32vu + 16 + vk (vk = lane mod 16) of blocks 2vu and 2vu + 1.
-  const uint32_t klo = 8u * (threadIdx.x % (16 * RPC));
-  const int vu = w / VCW;
-  const int vcc = 4 * (w - vu * VCW) + (lane >> 4);
-  const int vk = lane & 15;
-  const uint32_t vlo = (uint32_t)(vk * HD + 8 * vcc);
-  u32x4 kr[CPT], vr[2];
   auto block_base = [&](const uint16_t* pool, int e) {
     const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
     return pool + ((int64_t)blk * a.H + h) * (16 * HD);
   };
-  auto gload = [&](int st, int (&ent)[NBS]) {
+
+  // LDS tiles hold key rows of HD values unpadded; 16-byte chunk p of key row r holds head_dim
+  // chunk p ^ kswz(r) (K) or p ^ vswz(r) (V). The swizzles make the operand reads below hit all
+  // LDS banks once per pass: the 16 rows of a K read cover 16 distinct chunk positions, and the
+  // 4 key rows x 4 head_dim chunks of a transposing V read cover 16 distinct chunks.
+  auto kswz = [](int r) { return (r / RPB) & (CPR - 1); };
+  auto vswz = [](int r) { return (4 * ((r / RPB) & 3)) & (CPR - 1); };
+
+  // LDS-direct loads (global_load_lds_dwordx4): lane L of a wavefront's instruction writes the 16
+  // bytes at LDS address dst + 16L. Instruction n of wavefront w fills key rows RPI*(w*NDMA + n)
+  // ..+RPI-1 of the step tile, all in one KV block; the lane's source offset in the block is
+  // fixed (kdo / vdo), only the block base changes per step.
+  uint32_t kdo[NDMA], vdo[NDMA];
 #pragma unroll
-    for (int j = 0; j < NBS; ++j) ent[j] = NBS * st + j < nb ? pt[NBS * st + j] : -1;
-#pragma unroll
-    for (int n = 0; n < CPT; ++n) {
-      const int kb = (kWave * w + NW * kWave * n) / (16 * RPC);
-      kr[n] = *reinterpret_cast<const u32x4*>(block_base(kpool, ent[kb]) + klo);
+  for (int n = 0; n < NDMA; ++n) {
+    const int r = (w * NDMA + n) * RPI + lane / CPR;
+    const int p = lane % CPR;
+    kdo[n] = (uint32_t)((r & 15) * HD + 8 * (p ^ kswz(r)));
+    vdo[n] = (uint32_t)((r & 15) * HD + 8 * (p ^ vswz(r)));
+  }
+  // Page-table entries come from a per-wavefront copy of 64 consecutive entries (lane i holds
+  // entry ptb + i), refreshed when a step's blocks leave it (64 is a multiple of NBS): one
+  // vector load per 64 blocks instead of one scalar load and wait per step.
+  int ptc = 0, ptb = -64;
+  auto issue_loads = [&](int st, int (&ent)[NBS], uint16_t* skx, uint16_t* svx) {
+    const int j0 = NBS * st;
+    if (j0 - ptb >= 64) {
+      ptb = j0;
+      const int idx = j0 + lane;
+      ptc = load_now(pt + (idx < nb ? idx : 0));
     }
 #pragma unroll
-    for (int x = 0; x < 2; ++x) vr[x] = *reinterpret_cast<const u32x4*>(block_base(vpool, ent[2 * vu + x]) + vlo);
-  };
-  // V^T rows (one per head_dim index): word 16u + k (k < 16) of sub-tile u holds keys 32u + k
-  // (low half) and 32u + 16 + k (high half).
-  auto lstore = [&](int buf) {
+    for (int j = 0; j < NBS; ++j) ent[j] = j0 + j < nb ? __builtin_amdgcn_readlane(ptc, j0 - ptb + j) : -1;
 #pragma unroll
-    for (int n = 0; n < CPT; ++n) {
-      const int q = threadIdx.x + n * NW * kWave;
-      const int kk = q / RPC;
-      const int col = (q - kk * RPC) * 8;
-      *reinterpret_cast<u32x4*>(&sk[buf][kk * RS + col]) = kr[n];
-    }
-    uint16_t* vt = &sv[buf][8 * vcc * RST + 32 * vu + 2 * vk];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t wd = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
-      *reinterpret_cast<uint32_t*>(vt + e * RST) = wd;
+    for (int n = 0; n < NDMA; ++n) {
+      const int r0 = (w * NDMA + n) * RPI;
+      const int e = ent[r0 >> 4];
+      lds_direct_load16(block_base(kpool, e), 2 * kdo[n], skx + r0 * HD);
+      lds_direct_load16(block_base(vpool, e), 2 * vdo[n], svx + r0 * HD);
     }
   };
 
-  auto compute = [&](int buf, int st, const int (&ent)[NBS]) {
-    // ---- S^T = K Q^T for each 32-key sub-tile (independent MFMA chains, interleaved) ----------
+  // Per-lane LDS element offsets of the operand reads (fixed for the whole walk).
+  //   K (A of S^T = K Q^T, MFMA s, sub-tile u): key row c + 32u, head_dim chunk G2*CPR/2 + s.
+  //   V (A of O^T += V^T P^T, tile d): ds_read_b64_tr_b16 gives lane j of each 16-lane group
+  //   element r = the value at row r' = r, column j of the 4 x 16 block its group addresses
+  //   (lanes 4r' + a' supply the addresses of row r', columns 4a'..4a'+3). Lane (G2, c) reads,
+  //   for 4 keys K0 + r (r = (c mod 16) / 4), head_dim 32d + 16(c / 16) + 4(c mod 4): it then
+  //   holds V[K0 + r][32d + c], r = 0..3 — four k slots of row c of V^T.
+  const int kx = kswz(c);
+  const int vr4 = (c & 15) >> 2;
+  const int vx = vswz(4 * G2 + vr4);
+  auto v_off = [&](int d) {
+    const int hd = 32 * d + 16 * (c >> 4) + 4 * (c & 3);
+    return (4 * G2 + vr4) * HD + 8 * ((hd >> 3) ^ vx) + (hd & 4);
+  };
+
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  auto compute = [&](const uint16_t* skx, const uint16_t* svx, int st, const int (&ent)[NBS]) {
+    // ---- S^T = K Q^T for each 32-key sub-tile ------------------------------------------------
     f32x16 sacc[NSUB];
 #pragma unroll
     for (int u = 0; u < NSUB; ++u)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[u][e] = 0.f;
-    const uint16_t* krow = &sk[buf][c * RS + G2 * QH];
 #pragma unroll
     for (int s = 0; s < NQ; ++s)
 #pragma unroll
       for (int u = 0; u < NSUB; ++u) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + u * 32 * RS + 8 * s);
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(skx + (c + 32 * u) * HD + 8 * ((G2 * (CPR / 2) + s) ^ kx));
         sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s], sacc[u], 0, 0, 0);
       }
     // ---- online softmax (sub-tile u, keys 32u + 8j + 4*G2 + r of this step), in place --------
@@ -295,39 +336,56 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
         ps += sacc[u][e];
       }
     l += sum_xor32(ps);
-    // ---- O^T += V^T P^T, per sub-tile: MFMA mm contracts keys 8mm + 4*G2 + q + 16hf at slot
-    // (G2, 2q + hf), i.e. registers 4mm + q and 4mm + 8 + q of the lane ------------------------
+    // ---- O^T += V^T P^T: MFMA (u2, mm, d) contracts keys 32u2 + 16mm + 8jj + 4*G2 + r at slot
+    // (G2, 4jj + r), i.e. the lane's registers 8mm + 4jj + r ----------------------------------
 #pragma unroll
     for (int u2 = 0; u2 < NSUB; ++u2)
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
         uint32_t pw[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(sacc[u2][4 * mm + q], sacc[u2][4 * mm + 8 + q]);
+        for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(sacc[u2][8 * mm + 2 * q], sacc[u2][8 * mm + 2 * q + 1]);
         const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
-        // A: V^T row 32d + c, words 16u2 + 8mm + 4*G2 .. +3
-        const uint16_t* vrow = &sv[buf][c * RST + 32 * u2 + 16 * mm + 8 * G2];
 #pragma unroll
         for (int d = 0; d < DU; ++d) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vrow + 32 * d * RST);
+          const uint16_t* vp = svx + v_off(d) + (32 * u2 + 16 * mm) * HD;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(vp));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(vp + 8 * HD));
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
           oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[d], 0, 0, 0);
         }
       }
   };
 
+  // NST-stage pipeline: the loads of step st + NST - 1 are issued once every wavefront is past
+  // step st - 1 (whose stage they reuse), NST - 1 steps ahead of their use. Before computing step
+  // st a wavefront waits for its own loads of step st (vmcnt: those of the later steps may still
+  // be in flight) and the barrier makes every wavefront's loads of step st visible.
   if (nsteps > 0) {
-    int cur[NBS], nxt[NBS];
-    gload(0, cur);
-    lstore(0);
-    __syncthreads();
-    for (int st = 0; st < nsteps; ++st) {
-      const bool more = st + 1 < nsteps;
-      if (more) gload(st + 1, nxt);
-      if (st < wsteps) compute(st & 1, st, cur);
-      if (more) lstore((st + 1) & 1);
+    int e0[NBS], e1[NBS], e2[NBS];  // page-table entries of the steps in stages 0, 1, 2
+    issue_loads(0, e0, sk0, sv0);
+    if (NST > 2 && nsteps > 1) issue_loads(1, e1, sk1, sv1);
+    auto iteration = [&](int st, const int (&ec)[NBS], int (&en)[NBS], const uint16_t* skc, const uint16_t* svc,
+                         uint16_t* skn, uint16_t* svn) {
+      if (NST > 2 && st + 1 < nsteps) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NDMA));  // vmcnt(2 * NDMA)
+      else __builtin_amdgcn_s_waitcnt(0x0F70);                                           // vmcnt(0)
       __syncthreads();
-#pragma unroll
-      for (int j = 0; j < NBS; ++j) cur[j] = nxt[j];
+      if (st + NST - 1 < nsteps) issue_loads(st + NST - 1, en, skn, svn);
+      if (st < wsteps) compute(skc, svc, st, ec);
+    };
+    if constexpr (NST == 3) {
+      for (int st = 0; st < nsteps; st += 3) {
+        iteration(st, e0, e2, sk0, sv0, sk2, sv2);
+        if (st + 1 < nsteps) iteration(st + 1, e1, e0, sk1, sv1, sk0, sv0);
+        if (st + 2 < nsteps) iteration(st + 2, e2, e1, sk2, sv2, sk1, sv1);
+      }
+    } else {
+      for (int st = 0; st < nsteps; st += 2) {
+        iteration(st, e0, e1, sk0, sv0, sk1, sv1);
+        if (st + 1 < nsteps) iteration(st + 1, e1, e0, sk1, sv1, sk0, sv0);
+      }
     }
   }
 
@@ -574,11 +632,11 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
       else prefill_wide_f32_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
     }
   } else if (io_dtype == PA_DTYPE_F32) {
-    if (a.head_dim == 64) prefill_wide_kernel<float, 64, wide_nsub<64>()><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<float, 128, wide_nsub<128>()><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<float, 64, wide_nsub<64>(), wide_stages<64>()><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<float, 128, wide_nsub<128>(), wide_stages<128>()><<<grid, block, 0, stream>>>(a);
   } else {
-    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64, wide_nsub<64>()><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<uint16_t, 128, wide_nsub<128>()><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64, wide_nsub<64>(), wide_stages<64>()><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<uint16_t, 128, wide_nsub<128>(), wide_stages<128>()><<<grid, block, 0, stream>>>(a);
   }
   PA_CHECK_LAUNCH("wide prefill kernel");
   return PA_OK;
