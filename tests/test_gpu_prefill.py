@@ -216,6 +216,28 @@ def test_wide_prefill_work_orders(device, monkeypatch, B, kv_dtype):
     assert float((got - tile).abs().max()) <= tile_tol
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_wide_prefill_long_page_tables(device, monkeypatch, head_dim):
+    """Contexts of 2-5k tokens (130-330 blocks: the wide kernel reads its page-table entries 64 at
+    a time, so every request crosses several of those windows), with -1 entries in different
+    windows: against the 16-row kernel everywhere and the oracle on one request."""
+    ctx = [5000, 2100, 4000]
+    curs = [150, 40, 130]
+    b = make_prefill(device, 34 + head_dim, ctx, curs, T=150, H=2, Hd=head_dim, kv_dtype=torch.bfloat16)
+    pt = b.page_table.clone()
+    for r, cols in ((0, (3, 70, 200, 311)), (2, (64, 65, 190))):
+        pt[r, list(cols)] = -1
+    print(f"wide prefill long page tables hd={head_dim}", flush=True)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "wide")
+    got = paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, pt, b.seq_lens_t, b.cur_lens_t)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "tile")
+    tile = paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, pt, b.seq_lens_t, b.cur_lens_t)
+    assert float((got - tile).abs().max()) <= 5e-3
+    want = oracle.paged_attention(b.q[1:2].cpu(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists[1:2],
+                                  b.seq_lens[1:2], b.cur_lens[1:2], nthreads=NTHREADS)
+    assert max_err(got[1:2], want) <= 2e-2
+
+
 def test_wide_prefill_negative_pages_and_strided_views(device, monkeypatch):
     """A -1 page entry skips its 16 keys in the wide kernel as in the 16-row kernel; q/out are
     the model's transposed views; the untouched request matches the oracle."""
