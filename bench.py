@@ -21,7 +21,9 @@ Also reported on the same line:
   continuous_batching  the end-to-end run: decoder LM (vocab 5000, d_model 512, 8 heads,
                  6 layers, d_ff 2048, KV block 16, fp32, weights N(0, 0.02)), 200 Poisson requests
                  at 32 req/s, max batch 8, prefill chunk 256, 1536-token iteration budget, greedy;
-                 tokens/s and p50 TTFT on the scheduler's virtual clock, plus wall time.
+                 tokens/s and p50 TTFT on the scheduler's virtual clock, plus wall time;
+  continuous_batching_bf16_model  the same trace and weights with the model in bf16 (weights,
+                 activations and KV; the decode steps through the bf16 fused kernels), GPU only.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-e2e]
                        [--no-secondary] [--no-decode] [--calibrate-copy]
 (--no-decode skips the headline decode measurement; it is for profiling the other workloads alone.)
@@ -267,8 +269,9 @@ def init_weights_normal(model, std: float = 0.02) -> None:
                 mod.bias.zero_()
 
 
-def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True) -> dict:
-    """The end-to-end benchmark trace through the continuous scheduler on `device`."""
+def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True, dtype=None) -> dict:
+    """The end-to-end benchmark trace through the continuous scheduler on `device` (model weights
+    and activations in `dtype`, default fp32)."""
     import torch
 
     from src.config import benchmark_serving_request_mix
@@ -284,6 +287,8 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True)
                               attention_backend=backend, kv_block_size=16, kv_pool_initial_blocks=64,
                               kv_pool_growth_factor=2.0).to(device).eval()
     init_weights_normal(model)
+    if dtype is not None:
+        model = model.to(dtype)
     graphs_prepared = 0
     if warmup:  # as the reference harness: one batched generate, then fresh pools
         generate_with_cache(model, torch.randint(0, 5000, (8, 512), device=device), max_new_tokens=[2] * 8)
@@ -420,6 +425,10 @@ def main() -> int:
     if not args.no_e2e:
         log("end-to-end continuous batching (200 requests, 32 req/s)")
         result["continuous_batching"] = continuous_batching_pair(dev, with_cpu=not args.no_cpu_baseline)
+        log("end-to-end continuous batching with the model in bf16")
+        bf = continuous_batching(dev, dtype=torch.bfloat16)
+        bf["model_dtype"] = "bf16 (weights, activations, KV pools; fp32 accumulation)"
+        result["continuous_batching_bf16_model"] = bf
     print(json.dumps(result), flush=True)
     return 0
 

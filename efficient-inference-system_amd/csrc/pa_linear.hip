@@ -1,47 +1,50 @@
-// Small-M fp32 linear layers for the decode step of the paged-attention model (gfx950).
+// Small-M linear layers for the decode step of the paged-attention model (gfx950), with fp32 or
+// bf16 weights and activations (fp32 accumulation either way).
 //
 // A decode step (or a short prefill chunk) multiplies at most 64 token rows by each weight matrix,
-// so the work is a stream of the weights (N x K fp32) against a few rows of activations. Library
-// GEMMs tile such shapes into a few tens of workgroups; here one workgroup of 8 (16 at K = 2048)
+// so the work is a stream of the weights (N x K) against a few rows of activations. Library GEMMs
+// tile such shapes into a few tens of workgroups; here one workgroup of 8 (16 at K = 2048)
 // wavefronts owns a 16-row x 16-column tile of the output (grid x: column tiles, y: row tiles),
-// its wavefronts split K, and each wavefront accumulates the 16 (rows) x 16 (columns) tile with
-// v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation) over its K range; the partial tiles
-// are summed in LDS and the epilogue is applied once. Every global load of a workgroup (weights,
-// activations, LayerNorm parameters, bias, residual) is issued at its start, so a launch costs
-// one memory round trip.
-//   A (16 x 4): lane (G, c) holds x[row r0 + c][k(G, s)]  (rows >= M are zero)
-//   B (4 x 16): lane (G, c) holds W[col n0 + c][k(G, s)] (torch Linear weight, row-major [N, K])
-// with the contraction slot of MFMA s mapped to k(G, s) = k_wave + G*KL + s, so every lane reads
-// KL contiguous floats of one activation row and of one weight row (16-byte loads).
+// its wavefronts split K, and each wavefront accumulates the 16 (rows) x 16 (columns) tile over
+// its K range, with v_mfma_f32_16x16x4_f32 (fp32 products, like torch's fp32 GEMM) or
+// v_mfma_f32_16x16x16_bf16 (bf16 products); the partial tiles are summed in LDS and the epilogue
+// is applied once. Every global load of a workgroup (weights, activations, LayerNorm parameters,
+// bias, residual) is issued at its start, so a launch costs one memory round trip.
+//   A: lane (G, c) holds x[row r0 + c][k(G, s, e)]  (rows >= M are zero)
+//   B: lane (G, c) holds W[col n0 + c][k(G, s, e)] (torch Linear weight, row-major [N, K])
+// with the contraction slot (G, e) of MFMA s mapped to k = k_wave + G*KL + E*s + e (E = 1 for
+// fp32, 4 for bf16), so every lane reads KL contiguous values of one activation row and of one
+// weight row (8- or 16-byte loads), and A and B use the same slot map.
 // Fusions:
-//   prologue  LayerNorm of the activation rows (biased variance, like torch.nn.LayerNorm),
-//             computed from the slices the lanes already hold (no second pass over memory);
-//   epilogue  bias, exact (erf) GELU, residual add; or, for the K/V projections, a scatter of
-//             each row's head_dim vectors into its KV-pool slot (the append of the decode step).
+//   prologue  LayerNorm of the activation rows (biased variance, like torch.nn.LayerNorm; fp32
+//             statistics, bf16 rows rounded to bf16 after normalisation as torch's bf16 LayerNorm
+//             output is), computed from the slices the lanes already hold;
+//   epilogue  bias, exact (erf) GELU, residual add, one rounding to the output type; or, for the
+//             K/V projections, a scatter of each row's head_dim vectors into its KV-pool slot (the
+//             append of the decode step).
 #include <math.h>
 
 #include "pa_attention.h"
 
 namespace pa {
 
-
 constexpr int kLinRows = 16;     // activation rows per workgroup (MFMA tile height)
 constexpr int kLinMaxRows = 64;  // rows per call: up to four row tiles (grid y)
 
 struct LinArgs {
-  const float* x;
+  const void* x;      // [M, K] rows of type T
   int64_t x_stride;
   int32_t M, K;
-  const float* ln_w;  // null: no LayerNorm
-  const float* ln_b;
+  const void* ln_w;   // null: no LayerNorm
+  const void* ln_b;
   float ln_eps;
-  const float* w[3];  // segment weights, each [seg_n, K]
-  const float* b[3];  // segment biases (null: none)
+  const void* w[3];   // segment weights, each [seg_n, K]
+  const void* b[3];   // segment biases (null: none)
   int32_t seg_n, nseg;
   int32_t act;        // 0 none, 1 GELU (erf)
-  const float* res;   // residual rows (null: none), same columns as out
+  const void* res;    // residual rows (null: none), same columns as out
   int64_t res_stride;
-  float* out;         // segment 0's rows (and all segments' when there is no pool)
+  void* out;          // segment 0's rows (and all segments' when there is no pool)
   int64_t out_stride;
   void* k_pool;       // when set: segments 1 and 2 are scattered into the K / V pools
   void* v_pool;
@@ -49,6 +52,7 @@ struct LinArgs {
   int64_t num_blocks;
   const int32_t* slots;  // per row: block * block_size + offset, < 0 = skip
   int32_t H, Hd, bs;
+  int32_t bf16;       // T = bf16 (else fp32)
 };
 
 // Wavefronts per workgroup (they split K): 16 at K = 2048 keeps more of the 128 KB weight tile in
@@ -56,12 +60,47 @@ struct LinArgs {
 template <int K>
 constexpr int lin_waves() { return K >= 2048 ? 16 : 8; }
 
-template <int K, bool LN>
+// Element access of a lane's slice held as 32-bit words (1 fp32 or 2 bf16 per word).
+template <typename T> struct LinT;
+template <> struct LinT<float> {
+  static constexpr int EPW = 1;
+  __device__ static __forceinline__ float get(const uint32_t* w, int e) { return __uint_as_float(w[e]); }
+};
+template <> struct LinT<uint16_t> {
+  static constexpr int EPW = 2;
+  __device__ static __forceinline__ float get(const uint32_t* w, int e) {
+    return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+  }
+};
+
+// NWD consecutive 32-bit words from p (16-byte loads, or one 8-byte load when NWD == 2); zeros
+// when !ok.
+template <int NWD>
+__device__ __forceinline__ void load_words(uint32_t (&dst)[NWD], const void* p, bool ok) {
+  const uint32_t* q = static_cast<const uint32_t*>(p);
+  if constexpr (NWD % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < NWD; i += 4) {
+      const u32x4 t = ok ? *reinterpret_cast<const u32x4*>(q + i) : u32x4{0u, 0u, 0u, 0u};
+      dst[i] = t[0]; dst[i + 1] = t[1]; dst[i + 2] = t[2]; dst[i + 3] = t[3];
+    }
+  } else {
+    static_assert(NWD == 2, "8- or 16-byte slices");
+    const u32x2 t = ok ? *reinterpret_cast<const u32x2*>(q) : u32x2{0u, 0u};
+    dst[0] = t[0]; dst[1] = t[1];
+  }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+template <int K, bool LN, typename T>
 __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(const LinArgs a) {
+  constexpr bool BF = sizeof(T) == 2;
   constexpr int kLinWaves = lin_waves<K>();
   constexpr int KW = K / kLinWaves;  // K range of one wavefront
   constexpr int KL = KW / 4;         // contiguous k values per lane
-  static_assert(KL % 4 == 0, "16-byte loads");
+  constexpr int NWD = KL / LinT<T>::EPW;  // 32-bit words per lane per row slice
+  static_assert(KL % 4 == 0 && (NWD % 4 == 0 || NWD == 2), "whole 8- or 16-byte slices");
 
   __shared__ float sm_part[kLinWaves][16][17];
   __shared__ float sm_red[2][kLinWaves][kLinRows];
@@ -74,39 +113,24 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   const int tiles_per_seg = (a.seg_n + 15) / 16;
   const int seg = blockIdx.x / tiles_per_seg;
   const int n0 = (blockIdx.x - seg * tiles_per_seg) * 16;
-  const float* W = a.w[seg];
+  const T* W = static_cast<const T*>(a.w[seg]);
   const int kb = w * KW + G * KL;
   const int r0 = blockIdx.y * kLinRows;  // first activation row of this workgroup
   const bool row_ok = r0 + c < a.M;
 
-  // ---- every global load first: weight row n0 + c and activation row c over k(G, 0..KL), the
+  // ---- every global load first: weight row n0 + c and activation row c over k(G, ...), the
   // LayerNorm parameters of those k, and the epilogue operands of thread (m, n0 + cc) ----------
-  // LayerNorm parameters are preloaded with the rest up to K = 1024; at K = 2048 they would not
-  // fit the register budget and are read after the statistics.
-  constexpr bool PRE = LN && KL <= 32;
-  float wb[KL], xa[KL], lg[PRE ? KL : 1], lb[PRE ? KL : 1];
+  // LayerNorm parameters are preloaded with the rest, except for fp32 at 16 wavefronts (K = 2048,
+  // 128 registers per lane) where they are read after the statistics, 16 bytes at a time.
+  constexpr bool PRE = LN && (BF || kLinWaves < 16);
+  uint32_t wv[NWD], xv[NWD], lgv[PRE ? NWD : 1], lbv[PRE ? NWD : 1];
   {
     const int n = n0 + c < a.seg_n ? n0 + c : a.seg_n - 1;  // clamp: the column is discarded
-    const float* wr = W + (int64_t)n * a.K + kb;
-    const float* xr = a.x + (int64_t)(row_ok ? r0 + c : 0) * a.x_stride + kb;
-#pragma unroll
-    for (int e = 0; e < KL; e += 4) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(wr + e);
-      wb[e] = t[0]; wb[e + 1] = t[1]; wb[e + 2] = t[2]; wb[e + 3] = t[3];
-    }
-#pragma unroll
-    for (int e = 0; e < KL; e += 4) {
-      const f32x4 t = row_ok ? *reinterpret_cast<const f32x4*>(xr + e) : f32x4{0.f, 0.f, 0.f, 0.f};
-      xa[e] = t[0]; xa[e + 1] = t[1]; xa[e + 2] = t[2]; xa[e + 3] = t[3];
-    }
+    load_words(wv, W + (int64_t)n * a.K + kb, true);
+    load_words(xv, static_cast<const T*>(a.x) + (int64_t)(row_ok ? r0 + c : 0) * a.x_stride + kb, row_ok);
     if constexpr (PRE) {
-#pragma unroll
-      for (int e = 0; e < KL; e += 4) {
-        const f32x4 g = *reinterpret_cast<const f32x4*>(a.ln_w + kb + e);
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(a.ln_b + kb + e);
-        lg[e] = g[0]; lg[e + 1] = g[1]; lg[e + 2] = g[2]; lg[e + 3] = g[3];
-        lb[e] = bb[0]; lb[e + 1] = bb[1]; lb[e + 2] = bb[2]; lb[e + 3] = bb[3];
-      }
+      load_words(lgv, static_cast<const T*>(a.ln_w) + kb, true);
+      load_words(lbv, static_cast<const T*>(a.ln_b) + kb, true);
     }
   }
   const int ml = (threadIdx.x >> 4) & 15;  // row within the tile
@@ -116,16 +140,19 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   const bool live = threadIdx.x < 256 && m < a.M && n < a.seg_n;
   float bias_v = 0.f, res_v = 0.f;
   if (live) {
-    if (a.b[seg] != nullptr) bias_v = a.b[seg][n];
-    if (a.res != nullptr) res_v = a.res[(int64_t)m * a.res_stride + seg * a.seg_n + n];
+    if (a.b[seg] != nullptr) bias_v = Elem<T>::load(static_cast<const T*>(a.b[seg]) + n);
+    if (a.res != nullptr) res_v = Elem<T>::load(static_cast<const T*>(a.res) + (int64_t)m * a.res_stride + seg * a.seg_n + n);
   }
 
   // ---- LayerNorm of row c from the loaded slices: the row is spread over the 4 lane groups of
-  // each of the 8 wavefronts, so the sums reduce with two permlane swaps and one LDS exchange ---
+  // each wavefront, so the sums reduce with two permlane swaps and one LDS exchange ------------
   if constexpr (LN) {
+    float xf[KL];
+#pragma unroll
+    for (int e = 0; e < KL; ++e) xf[e] = LinT<T>::get(xv, e);
     float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < KL; ++e) s += xa[e];
+    for (int e = 0; e < KL; ++e) s += xf[e];
     s = sum_xor32(sum_xor16(s));
     if (G == 0) sm_red[0][w][c] = s;
     __syncthreads();
@@ -135,7 +162,7 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
     const float mean = tot / K;
     float q = 0.f;
 #pragma unroll
-    for (int e = 0; e < KL; ++e) q = fmaf(xa[e] - mean, xa[e] - mean, q);
+    for (int e = 0; e < KL; ++e) q = fmaf(xf[e] - mean, xf[e] - mean, q);
     q = sum_xor32(sum_xor16(q));
     if (G == 0) sm_red[1][w][c] = q;
     __syncthreads();
@@ -143,17 +170,31 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
 #pragma unroll
     for (int ww = 0; ww < kLinWaves; ++ww) var += sm_red[1][ww][c];
     const float rstd = 1.f / sqrtf(var / K + a.ln_eps);
-    if constexpr (PRE) {
+    constexpr int CH = NWD % 4 == 0 ? 4 : 2;  // words per parameter load
+    constexpr int EPW = LinT<T>::EPW;
 #pragma unroll
-      for (int e = 0; e < KL; ++e) xa[e] = row_ok ? fmaf((xa[e] - mean) * rstd, lg[e], lb[e]) : 0.f;
-    } else {
+    for (int i0 = 0; i0 < NWD; i0 += CH) {
+      uint32_t gw[CH], bw[CH];
+      if constexpr (PRE) {
 #pragma unroll
-      for (int e = 0; e < KL; e += 4) {
-        const f32x4 g = *reinterpret_cast<const f32x4*>(a.ln_w + kb + e);
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(a.ln_b + kb + e);
-#pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) xa[e + q2] = row_ok ? fmaf((xa[e + q2] - mean) * rstd, g[q2], bb[q2]) : 0.f;
+        for (int i = 0; i < CH; ++i) {
+          gw[i] = lgv[i0 + i];
+          bw[i] = lbv[i0 + i];
+        }
+      } else {
+        load_words(gw, static_cast<const T*>(a.ln_w) + kb + i0 * EPW, true);
+        load_words(bw, static_cast<const T*>(a.ln_b) + kb + i0 * EPW, true);
       }
+#pragma unroll
+      for (int e = 0; e < CH * EPW; ++e) {
+        const int ee = i0 * EPW + e;
+        xf[ee] = row_ok ? fmaf((xf[ee] - mean) * rstd, LinT<T>::get(gw, e), LinT<T>::get(bw, e)) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) {
+      if constexpr (BF) xv[i] = (uint32_t)f32_to_bf16(xf[2 * i]) | ((uint32_t)f32_to_bf16(xf[2 * i + 1]) << 16);
+      else xv[i] = __float_as_uint(xf[i]);
     }
   }
 
@@ -161,8 +202,18 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   f32x4 acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (BF) {
 #pragma unroll
-  for (int s = 0; s < KL; ++s) acc[s & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s], wb[s], acc[s & 3], 0, 0, 0);
+    for (int s = 0; s < KL / 4; ++s) {
+      const s16x4 av = __builtin_bit_cast(s16x4, (u32x2{xv[2 * s], xv[2 * s + 1]}));
+      const s16x4 bv = __builtin_bit_cast(s16x4, (u32x2{wv[2 * s], wv[2 * s + 1]}));
+      acc[s & 3] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, acc[s & 3], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < KL; ++s)
+      acc[s & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(xv[s]), __uint_as_float(wv[s]), acc[s & 3], 0, 0, 0);
+  }
   const f32x4 d = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   // lane (G, c) holds D[4G + i][c]: rows 4G..4G+3 of output column n0 + c
 #pragma unroll
@@ -189,7 +240,7 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
       static_cast<float*>(pool)[off] = v;
     return;
   }
-  a.out[(int64_t)m * a.out_stride + seg * a.seg_n + n] = v + res_v;
+  Elem<T>::store(static_cast<T*>(a.out) + (int64_t)m * a.out_stride + seg * a.seg_n + n, v + res_v);
 }
 
 static bool small_linear_k_supported(int32_t K) {
@@ -201,10 +252,15 @@ static int launch_small_linear(const LinArgs& a, hipStream_t stream) {
   if (tiles > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
   const dim3 grid((unsigned)tiles, (unsigned)((a.M + kLinRows - 1) / kLinRows));
   const bool ln = a.ln_w != nullptr;
-#define PA_LIN_CASE(KK)                                                                   \
-  case KK:                                                                                \
-    if (ln) small_linear_kernel<KK, true><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a); \
-    else small_linear_kernel<KK, false><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a);   \
+#define PA_LIN_CASE(KK)                                                                                   \
+  case KK:                                                                                                \
+    if (a.bf16) {                                                                                         \
+      if (ln) small_linear_kernel<KK, true, uint16_t><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a);   \
+      else small_linear_kernel<KK, false, uint16_t><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a);     \
+    } else {                                                                                              \
+      if (ln) small_linear_kernel<KK, true, float><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a);      \
+      else small_linear_kernel<KK, false, float><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a);        \
+    }                                                                                                     \
     break;
   switch (a.K) {
     PA_LIN_CASE(128)
@@ -222,23 +278,38 @@ static int launch_small_linear(const LinArgs& a, hipStream_t stream) {
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Token + position embedding of a [B, T] step: row b*T + t = tok[ids[b, t]] + pos[min(p0[b] + t,
-// max_pos - 1)]; an id outside the vocabulary gives a zero token row. One workgroup per row.
-__global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* ids, const int64_t* pos0, int32_t T,
-                                                        const float* tok, int64_t vocab, const float* pos_tab,
-                                                        int32_t max_pos, int32_t d, float* out, int64_t out_stride) {
+// max_pos - 1)]; an id outside the vocabulary gives a zero token row. One workgroup per row;
+// 16-byte vectors (4 fp32 or 8 bf16 values), the sum in fp32, rounded once for bf16.
+template <typename T>
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* ids, const int64_t* pos0, int32_t T_len,
+                                                        const T* tok, int64_t vocab, const T* pos_tab,
+                                                        int32_t max_pos, int32_t d, T* out, int64_t out_stride) {
+  constexpr int EPV = 16 / sizeof(T);
   const int row = blockIdx.x;
-  const int b = row / T, t = row - b * T;
+  const int b = row / T_len, t = row - b * T_len;
   const int64_t id = ids[row];
   int64_t p = pos0[b] + t;
   p = p < max_pos - 1 ? p : max_pos - 1;
   p = p > 0 ? p : 0;
   const bool ok = id >= 0 && id < vocab;
-  const f32x4* tr = reinterpret_cast<const f32x4*>(tok + (ok ? id : 0) * d);
-  const f32x4* pr = reinterpret_cast<const f32x4*>(pos_tab + p * d);
-  f32x4* o = reinterpret_cast<f32x4*>(out + (int64_t)row * out_stride);
-  for (int k = threadIdx.x; k < d / 4; k += 256) {
-    const f32x4 tv = ok ? tr[k] : f32x4{0.f, 0.f, 0.f, 0.f};
-    o[k] = tv + pr[k];
+  const u32x4* tr = reinterpret_cast<const u32x4*>(tok + (ok ? id : 0) * d);
+  const u32x4* pr = reinterpret_cast<const u32x4*>(pos_tab + p * d);
+  u32x4* o = reinterpret_cast<u32x4*>(out + (int64_t)row * out_stride);
+  for (int k = threadIdx.x; k < d / EPV; k += 256) {
+    const u32x4 tv = ok ? tr[k] : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 pv = pr[k];
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (sizeof(T) == 4) {
+        r[i] = __float_as_uint(__uint_as_float(tv[i]) + __uint_as_float(pv[i]));
+      } else {
+        const float lo = bf16_to_f32((uint16_t)(tv[i] & 0xffffu)) + bf16_to_f32((uint16_t)(pv[i] & 0xffffu));
+        const float hi = bf16_to_f32((uint16_t)(tv[i] >> 16)) + bf16_to_f32((uint16_t)(pv[i] >> 16));
+        r[i] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+      }
+    }
+    o[k] = r;
   }
 }
 
@@ -246,20 +317,26 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* ids, con
 
 using namespace pa;
 
-extern "C" int pa_linear_rows(const float* x, int64_t x_stride, int32_t rows, int32_t in_features,
-                              const float* weight, const float* bias, int32_t out_features,
-                              const float* ln_weight, const float* ln_bias, float ln_eps,
-                              int32_t activation, const float* residual, int64_t residual_stride,
-                              float* out, int64_t out_stride, void* stream) {
+// Activations, weights, biases, LayerNorm parameters and outputs share one element type (dtype).
+static bool lin_dtype_ok(int dtype) { return dtype == PA_DTYPE_F32 || dtype == PA_DTYPE_BF16; }
+static int elems_per_16b(int dtype) { return dtype == PA_DTYPE_BF16 ? 8 : 4; }
+
+extern "C" int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int32_t in_features,
+                              const void* weight, const void* bias, int32_t out_features,
+                              const void* ln_weight, const void* ln_bias, float ln_eps,
+                              int32_t activation, const void* residual, int64_t residual_stride,
+                              void* out, int64_t out_stride, int dtype, void* stream) {
   pa_host::clear_error();
   PA_CHECK_ARG(rows >= 0 && rows <= kLinMaxRows, "rows must be in [0, %d], got %d", kLinMaxRows, rows);
   PA_CHECK_ARG(out_features > 0 && in_features > 0, "bad sizes: in=%d out=%d", in_features, out_features);
   PA_CHECK_ARG(activation == 0 || activation == 1, "bad activation %d", activation);
+  PA_CHECK_ARG(lin_dtype_ok(dtype), "bad dtype %d", dtype);
   if (rows == 0) return PA_OK;
   PA_CHECK_ARG(x && weight && out, "null x/weight/out");
   PA_CHECK_ARG((ln_weight == nullptr) == (ln_bias == nullptr), "LayerNorm needs both weight and bias");
-  PA_CHECK_ARG(aligned16(x) && aligned16(weight) && x_stride % 4 == 0 && (!ln_weight || (aligned16(ln_weight) &&
-               aligned16(ln_bias))), "x, weight and LayerNorm parameters must be 16-byte aligned with x_stride % 4 == 0");
+  const int vec = elems_per_16b(dtype);
+  PA_CHECK_ARG(aligned16(x) && aligned16(weight) && x_stride % vec == 0 && (!ln_weight || (aligned16(ln_weight) &&
+               aligned16(ln_bias))), "x, weight and LayerNorm parameters must be 16-byte aligned, x_stride a multiple of %d", vec);
   PA_CHECK_ARG(x_stride >= in_features && out_stride >= out_features &&
                (residual == nullptr || residual_stride >= out_features), "row strides smaller than the rows");
   LinArgs a{};
@@ -267,29 +344,31 @@ extern "C" int pa_linear_rows(const float* x, int64_t x_stride, int32_t rows, in
   a.ln_w = ln_weight; a.ln_b = ln_bias; a.ln_eps = ln_eps;
   a.w[0] = weight; a.b[0] = bias; a.seg_n = out_features; a.nseg = 1;
   a.act = activation; a.res = residual; a.res_stride = residual_stride;
-  a.out = out; a.out_stride = out_stride;
+  a.out = out; a.out_stride = out_stride; a.bf16 = dtype == PA_DTYPE_BF16;
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int32_t d_model,
-                             const float* ln_weight, const float* ln_bias, float ln_eps,
-                             const float* wq, const float* bq, const float* wk, const float* bk,
-                             const float* wv, const float* bv,
-                             float* q_out, int64_t q_stride,
+extern "C" int pa_qkv_append(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,
+                             const void* ln_weight, const void* ln_bias, float ln_eps,
+                             const void* wq, const void* bq, const void* wk, const void* bk,
+                             const void* wv, const void* bv,
+                             void* q_out, int64_t q_stride,
                              void* k_pool, void* v_pool, int pool_dtype, int64_t num_blocks,
                              const int32_t* slot_mapping, int32_t num_heads, int32_t head_dim,
-                             int32_t block_size, void* stream) {
+                             int32_t block_size, int dtype, void* stream) {
   pa_host::clear_error();
   PA_CHECK_ARG(rows >= 0 && rows <= kLinMaxRows, "rows must be in [0, %d], got %d", kLinMaxRows, rows);
   PA_CHECK_ARG(num_heads > 0 && head_dim > 0 && block_size > 0 && d_model == num_heads * head_dim,
                "d_model must equal num_heads * head_dim");
   PA_CHECK_ARG(pool_dtype == PA_DTYPE_F32 || pool_dtype == PA_DTYPE_BF16, "bad pool dtype %d", pool_dtype);
+  PA_CHECK_ARG(lin_dtype_ok(dtype), "bad dtype %d", dtype);
   if (rows == 0) return PA_OK;
   PA_CHECK_ARG(x && wq && wk && wv && q_out && k_pool && v_pool && slot_mapping, "null pointer argument");
   PA_CHECK_ARG((ln_weight == nullptr) == (ln_bias == nullptr), "LayerNorm needs both weight and bias");
-  PA_CHECK_ARG(aligned16(x) && aligned16(wq) && aligned16(wk) && aligned16(wv) && x_stride % 4 == 0 &&
+  const int vec = elems_per_16b(dtype);
+  PA_CHECK_ARG(aligned16(x) && aligned16(wq) && aligned16(wk) && aligned16(wv) && x_stride % vec == 0 &&
                (!ln_weight || (aligned16(ln_weight) && aligned16(ln_bias))),
-               "x, weights and LayerNorm parameters must be 16-byte aligned with x_stride % 4 == 0");
+               "x, weights and LayerNorm parameters must be 16-byte aligned, x_stride a multiple of %d", vec);
   PA_CHECK_ARG(x_stride >= d_model && q_stride >= d_model, "row strides smaller than the rows");
   LinArgs a{};
   a.x = x; a.x_stride = x_stride; a.M = rows; a.K = d_model;
@@ -297,28 +376,36 @@ extern "C" int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int
   a.w[0] = wq; a.w[1] = wk; a.w[2] = wv; a.b[0] = bq; a.b[1] = bk; a.b[2] = bv;
   a.seg_n = d_model; a.nseg = 3;
   a.act = 0; a.res = nullptr; a.res_stride = 0;
-  a.out = q_out; a.out_stride = q_stride;
+  a.out = q_out; a.out_stride = q_stride; a.bf16 = dtype == PA_DTYPE_BF16;
   a.k_pool = k_pool; a.v_pool = v_pool; a.pool_bf16 = pool_dtype == PA_DTYPE_BF16; a.num_blocks = num_blocks;
   a.slots = slot_mapping; a.H = num_heads; a.Hd = head_dim; a.bs = block_size;
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int pa_embed_rows(const int64_t* ids, const int64_t* pos_start, int32_t batch, int32_t query_len,
-                             const float* token_table, int64_t vocab, const float* pos_table, int32_t max_pos,
-                             int32_t d_model, float* out, int64_t out_stride, void* stream) {
+                             const void* token_table, int64_t vocab, const void* pos_table, int32_t max_pos,
+                             int32_t d_model, void* out, int64_t out_stride, int dtype, void* stream) {
   pa_host::clear_error();
-  PA_CHECK_ARG(batch >= 0 && query_len >= 0 && vocab > 0 && max_pos > 0 && d_model > 0 && d_model % 4 == 0,
+  PA_CHECK_ARG(lin_dtype_ok(dtype), "bad dtype %d", dtype);
+  const int vec = elems_per_16b(dtype);
+  PA_CHECK_ARG(batch >= 0 && query_len >= 0 && vocab > 0 && max_pos > 0 && d_model > 0 && d_model % vec == 0,
                "bad sizes: batch=%d query_len=%d vocab=%lld max_pos=%d d_model=%d", batch, query_len,
                (long long)vocab, max_pos, d_model);
   const int64_t rows = (int64_t)batch * query_len;
   if (rows == 0) return PA_OK;
   PA_CHECK_ARG(ids && pos_start && token_table && pos_table && out, "null pointer argument");
-  PA_CHECK_ARG(aligned16(token_table) && aligned16(pos_table) && aligned16(out) && out_stride % 4 == 0 &&
-               out_stride >= d_model, "tables and out must be 16-byte aligned with out_stride % 4 == 0");
+  PA_CHECK_ARG(aligned16(token_table) && aligned16(pos_table) && aligned16(out) && out_stride % vec == 0 &&
+               out_stride >= d_model, "tables and out must be 16-byte aligned, out_stride a multiple of %d", vec);
   if (rows > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  embed_rows_kernel<<<dim3((unsigned)rows), dim3(256), 0, st>>>(ids, pos_start, query_len, token_table, vocab,
-                                                                 pos_table, max_pos, d_model, out, out_stride);
+  if (dtype == PA_DTYPE_BF16)
+    embed_rows_kernel<uint16_t><<<dim3((unsigned)rows), dim3(256), 0, st>>>(
+        ids, pos_start, query_len, static_cast<const uint16_t*>(token_table), vocab,
+        static_cast<const uint16_t*>(pos_table), max_pos, d_model, static_cast<uint16_t*>(out), out_stride);
+  else
+    embed_rows_kernel<float><<<dim3((unsigned)rows), dim3(256), 0, st>>>(
+        ids, pos_start, query_len, static_cast<const float*>(token_table), vocab,
+        static_cast<const float*>(pos_table), max_pos, d_model, static_cast<float*>(out), out_stride);
   PA_CHECK_LAUNCH("embedding kernel");
   return PA_OK;
 }

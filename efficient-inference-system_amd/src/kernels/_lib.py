@@ -78,7 +78,7 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _c_void_p, _i32,  # weight, bias, out_features
          _c_void_p, _c_void_p, _f32,  # LayerNorm weight, bias, eps
          _i32, _c_void_p, _i64,  # activation, residual, stride
-         _c_void_p, _i64, _c_void_p],  # out, stride, stream
+         _c_void_p, _i64, _int, _c_void_p],  # out, stride, dtype, stream
     ),
     "pa_qkv_append": (
         _int,
@@ -87,13 +87,13 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # wq, bq, wk, bk, wv, bv
          _c_void_p, _i64,  # q_out, stride
          _c_void_p, _c_void_p, _int, _i64,  # k pool, v pool, pool dtype, num_blocks
-         _c_void_p, _i32, _i32, _i32, _c_void_p],  # slots, heads, head_dim, block_size, stream
+         _c_void_p, _i32, _i32, _i32, _int, _c_void_p],  # slots, heads, head_dim, block_size, dtype, stream
     ),
     "pa_embed_rows": (
         _int,
         [_c_void_p, _c_void_p, _i32, _i32,  # ids, pos_start, batch, query_len
          _c_void_p, _i64, _c_void_p, _i32,  # token table, vocab, position table, max_pos
-         _i32, _c_void_p, _i64, _c_void_p],  # d_model, out, out stride, stream
+         _i32, _c_void_p, _i64, _int, _c_void_p],  # d_model, out, out stride, dtype, stream
     ),
     "pa_zero_blocks": (
         _int,

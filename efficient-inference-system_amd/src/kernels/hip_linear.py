@@ -1,4 +1,4 @@
-"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32, <= 64 rows).
+"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32 or bf16, <= 64 rows).
 
   linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
   qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
@@ -7,7 +7,9 @@
 
 They stand in for the nn.LayerNorm / nn.Linear / nn.GELU calls and the append of the
 reference's cached forward (src/model/transformer.py:30-35, src/model/attention.py:46-64) on
-one-token steps and short prefill chunks. All work is enqueued on torch's current stream; tensors must be on a HIP device.
+one-token steps and short prefill chunks, for a model in fp32 or in bf16 (weights and activations of
+one dtype; products accumulate in fp32). All work is enqueued on torch's current stream; tensors
+must be on a HIP device.
 """
 from __future__ import annotations
 
@@ -28,36 +30,53 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return t.data_ptr() if t is not None else None
 
 
-def _rows(x: torch.Tensor, name: str) -> None:
-    if not x.is_cuda or x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
-        raise ValueError(f"{name} must be a float32 [rows, features] tensor with unit column stride on a HIP device")
+DTYPES = (torch.float32, torch.bfloat16)
+
+
+def _rows(x: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> None:
+    if not x.is_cuda or x.dtype not in DTYPES or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError(f"{name} must be a float32 or bfloat16 [rows, features] tensor with unit column stride "
+                         "on a HIP device")
+    if dtype is not None and x.dtype != dtype:
+        raise ValueError(f"{name} is {x.dtype}, the layer computes in {dtype}")
+
+
+def _same_dtype(dtype: torch.dtype, *tensors) -> None:
+    for t in tensors:
+        if t is not None and t.dtype != dtype:
+            raise ValueError(f"all operands must be {dtype}, got a {t.dtype} tensor")
 
 
 def supported(linear: nn.Linear) -> bool:
-    return (linear.weight.dtype == torch.float32 and linear.weight.is_contiguous()
+    return (linear.weight.dtype in DTYPES and linear.weight.is_contiguous()
+            and (linear.bias is None or linear.bias.dtype == linear.weight.dtype)
             and linear.in_features in SUPPORTED_FEATURES)
 
 
 def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | None = None, gelu: bool = False,
                     residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 64)."""
+    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 64); x, the layer's
+    parameters, residual and out share one dtype (float32 or bfloat16)."""
     _rows(x, "x")
+    dt = x.dtype
     M, K = x.shape
     if K != linear.in_features:
         raise ValueError(f"x has {K} features, the layer takes {linear.in_features}")
+    _same_dtype(dt, linear.weight, linear.bias, ln.weight if ln is not None else None,
+                ln.bias if ln is not None else None)
     N = linear.out_features
     if out is None:
-        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
-    _rows(out, "out")
+        out = torch.empty((M, N), dtype=dt, device=x.device)
+    _rows(out, "out", dt)
     if residual is not None:
-        _rows(residual, "residual")
+        _rows(residual, "residual", dt)
     status = _lib.load().pa_linear_rows(
         x.data_ptr(), x.stride(0), M, K,
         linear.weight.data_ptr(), _ptr(linear.bias), N,
         _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
         float(ln.eps) if ln is not None else 0.0,
         1 if gelu else 0, _ptr(residual), residual.stride(0) if residual is not None else 0,
-        out.data_ptr(), out.stride(0), _stream(x.device),
+        out.data_ptr(), out.stride(0), _lib.dtype_code(dt), _stream(x.device),
     )
     _lib.check(status, "pa_linear_rows")
     return out
@@ -65,11 +84,16 @@ def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | No
 
 def qkv_append_hip(x: torch.Tensor, ln: nn.LayerNorm, attn, k_pool: torch.Tensor, v_pool: torch.Tensor,
                    slot_mapping: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """q = LN(x) Wq^T + bq for the rows of x; the K and V rows go straight into their pool slots."""
+    """q = LN(x) Wq^T + bq for the rows of x; the K and V rows go straight into their pool slots
+    (converted to the pool dtype). x, the projections, LayerNorm and q share one dtype."""
     _rows(x, "x")
+    dt = x.dtype
     M, D = x.shape
+    _same_dtype(dt, ln.weight if ln is not None else None, ln.bias if ln is not None else None,
+                *(t for l in (attn.q_proj, attn.k_proj, attn.v_proj) for t in (l.weight, l.bias)))
     if out is None:
-        out = torch.empty((M, D), dtype=torch.float32, device=x.device)
+        out = torch.empty((M, D), dtype=dt, device=x.device)
+    _rows(out, "out", dt)
     nblk, H, bs, Hd = k_pool.shape
     if slot_mapping.dtype != torch.int32 or slot_mapping.numel() < M or not slot_mapping.is_contiguous():
         raise ValueError("slot_mapping must be a contiguous int32 tensor with one entry per row")
@@ -83,7 +107,7 @@ def qkv_append_hip(x: torch.Tensor, ln: nn.LayerNorm, attn, k_pool: torch.Tensor
         attn.v_proj.weight.data_ptr(), _ptr(attn.v_proj.bias),
         out.data_ptr(), out.stride(0),
         k_pool.data_ptr(), v_pool.data_ptr(), _lib.dtype_code(k_pool.dtype), nblk,
-        slot_mapping.data_ptr(), H, Hd, bs, _stream(x.device),
+        slot_mapping.data_ptr(), H, Hd, bs, _lib.dtype_code(dt), _stream(x.device),
     )
     _lib.check(status, "pa_qkv_append")
     return out
@@ -96,23 +120,30 @@ def embed_rows_hip(ids: torch.Tensor, pos_start: torch.Tensor, token_emb: nn.Emb
         raise ValueError("ids and pos_start must be int64 (ids contiguous [B, T])")
     if not (pos_start.is_contiguous() and pos_start.numel() == ids.shape[0]):
         raise ValueError("pos_start must be a contiguous [B] tensor")
+    dt = token_emb.weight.dtype
     for name, t in (("token_emb", token_emb.weight), ("pos_emb", pos_emb.weight)):
-        if t.dtype != torch.float32 or not t.is_contiguous():
-            raise ValueError(f"{name} weight must be a contiguous float32 table")
+        if t.dtype not in DTYPES or t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"{name} weight must be a contiguous float32 or bfloat16 table (both of one dtype)")
     B, T = ids.shape
     d = token_emb.embedding_dim
     if out is None:
-        out = torch.empty((B * T, d), dtype=torch.float32, device=ids.device)
+        out = torch.empty((B * T, d), dtype=dt, device=ids.device)
+    _rows(out, "out", dt)
     status = _lib.load().pa_embed_rows(
         ids.data_ptr(), pos_start.data_ptr(), B, T, token_emb.weight.data_ptr(), token_emb.num_embeddings,
-        pos_emb.weight.data_ptr(), pos_emb.num_embeddings, d, out.data_ptr(), out.stride(0), _stream(ids.device),
+        pos_emb.weight.data_ptr(), pos_emb.num_embeddings, d, out.data_ptr(), out.stride(0), _lib.dtype_code(dt),
+        _stream(ids.device),
     )
     _lib.check(status, "pa_embed_rows")
     return out
 
 
 def model_supported(model) -> bool:
-    """True when every linear layer of the model's cached step fits the fused decode kernels."""
+    """True when every linear layer of the model's cached step fits the fused decode kernels (all
+    parameters of one dtype, float32 or bfloat16)."""
+    dt = model.lm_head.weight.dtype
+    if any(p.dtype != dt for p in model.parameters()):
+        return False
     for blk in model.blocks:
         a = blk.attn
         fc1, act, fc2 = blk.mlp[0], blk.mlp[1], blk.mlp[2]
@@ -128,4 +159,5 @@ def model_supported(model) -> bool:
 
 def _ln_supported(n) -> bool:
     return (isinstance(n, nn.LayerNorm) and n.elementwise_affine and n.bias is not None
-            and n.weight.dtype == torch.float32 and tuple(n.normalized_shape) == (n.weight.numel(),))
+            and n.weight.dtype in DTYPES and n.bias.dtype == n.weight.dtype
+            and tuple(n.normalized_shape) == (n.weight.numel(),))

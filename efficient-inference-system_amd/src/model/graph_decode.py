@@ -131,8 +131,10 @@ class _Captured:
         # stays valid for the graph's lifetime.
         self.ws = _workspace(device, ws_bytes) if ws_bytes else None
         self.fused = B * Tb <= hip_linear.MAX_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
-        self.embed_fused = (fused_decode_enabled() and model.token_emb.weight.dtype == torch.float32
-                            and model.pos_emb.weight.dtype == torch.float32 and model.token_emb.embedding_dim % 4 == 0)
+        emb_dt = model.token_emb.weight.dtype
+        self.embed_fused = (fused_decode_enabled() and emb_dt in hip_linear.DTYPES
+                            and model.pos_emb.weight.dtype == emb_dt
+                            and model.token_emb.embedding_dim % (4 if emb_dt == torch.float32 else 8) == 0)
         self.signature = _signature(pools)
         self.graph = None
         self.logits = None

@@ -163,46 +163,52 @@ int pa_zero_blocks(void* k_pool, void* v_pool, int pool_dtype, int64_t num_block
  * a few rows against every weight matrix.
  *
  * pa_linear_rows: out[m, :] = act(LN(x[m, :]) W^T + bias) + residual[m, :] for m < rows (<= 64).
+ *   dtype (PA_DTYPE_F32 or PA_DTYPE_BF16) is the element type of x, weight, bias, LayerNorm
+ *   parameters, residual and out alike; products accumulate in fp32 (bf16: LN(x) is rounded to
+ *   bf16 before the product, as torch's bf16 LayerNorm output is, and out is rounded once);
  *   weight is torch's [out_features, in_features] row-major; in_features must be 128, 256, 512,
  *   1024 or 2048;
  *   ln_weight/ln_bias NULL skips the LayerNorm (biased variance, eps ln_eps, like
  *   torch.nn.LayerNorm); bias and residual may be NULL; activation 0 = none, 1 = exact (erf)
- *   GELU (torch.nn.GELU()). x, weight and LayerNorm parameters 16-byte aligned.
+ *   GELU (torch.nn.GELU()). x, weight and LayerNorm parameters 16-byte aligned, x_stride a
+ *   multiple of 16 bytes.
  */
-int pa_linear_rows(const float* x, int64_t x_stride, int32_t rows, int32_t in_features,
-                   const float* weight, const float* bias, int32_t out_features,
-                   const float* ln_weight, const float* ln_bias, float ln_eps,
-                   int32_t activation, const float* residual, int64_t residual_stride,
-                   float* out, int64_t out_stride, void* stream);
+int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int32_t in_features,
+                   const void* weight, const void* bias, int32_t out_features,
+                   const void* ln_weight, const void* ln_bias, float ln_eps,
+                   int32_t activation, const void* residual, int64_t residual_stride,
+                   void* out, int64_t out_stride, int dtype, void* stream);
 
 /*
  * pa_qkv_append: the three projections of a cached attention layer in one launch, with the
  * LayerNorm before them and the KV append after them: q_out[m, :] = LN(x[m, :]) wq^T + bq, and
  * the rows LN(x[m, :]) wk^T + bk and LN(x[m, :]) wv^T + bv are written, split into num_heads
  * vectors of head_dim, into pool slot slot_mapping[m] of the K and V pools (converted to the pool
- * dtype; slot < 0 or a block outside [0, num_blocks) skips the row). Replaces
+ * dtype; slot < 0 or a block outside [0, num_blocks) skips the row). dtype is the element type of
+ * x, the weights, biases, LayerNorm parameters and q_out (as pa_linear_rows). Replaces
  * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 64 and
  * d_model in {128, 256, 512, 1024, 2048}.
  */
-int pa_qkv_append(const float* x, int64_t x_stride, int32_t rows, int32_t d_model,
-                  const float* ln_weight, const float* ln_bias, float ln_eps,
-                  const float* wq, const float* bq, const float* wk, const float* bk,
-                  const float* wv, const float* bv,
-                  float* q_out, int64_t q_stride,
+int pa_qkv_append(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,
+                  const void* ln_weight, const void* ln_bias, float ln_eps,
+                  const void* wq, const void* bq, const void* wk, const void* bk,
+                  const void* wv, const void* bv,
+                  void* q_out, int64_t q_stride,
                   void* k_pool, void* v_pool, int pool_dtype, int64_t num_blocks,
                   const int32_t* slot_mapping, int32_t num_heads, int32_t head_dim,
-                  int32_t block_size, void* stream);
+                  int32_t block_size, int dtype, void* stream);
 
 /*
  * pa_embed_rows: x[b*T + t, :] = token_table[ids[b, t], :] + pos_table[min(pos_start[b] + t,
- * max_pos - 1), :] for a [batch, query_len] step (ids and pos_start int64, tables fp32 row-major
- * [vocab, d_model] / [max_pos, d_model]); an id outside [0, vocab) gives a zero token row. Replaces
- * the position arithmetic and the two nn.Embedding lookups of the reference's forward
+ * max_pos - 1), :] for a [batch, query_len] step (ids and pos_start int64, tables row-major
+ * [vocab, d_model] / [max_pos, d_model] of element type dtype, fp32 or bf16, like out; the sum is
+ * formed in fp32); an id outside [0, vocab) gives a zero token row. Replaces the position
+ * arithmetic and the two nn.Embedding lookups of the reference's forward
  * (src/model/transformer.py:144-150) in one launch.
  */
 int pa_embed_rows(const int64_t* ids, const int64_t* pos_start, int32_t batch, int32_t query_len,
-                  const float* token_table, int64_t vocab, const float* pos_table, int32_t max_pos,
-                  int32_t d_model, float* out, int64_t out_stride, void* stream);
+                  const void* token_table, int64_t vocab, const void* pos_table, int32_t max_pos,
+                  int32_t d_model, void* out, int64_t out_stride, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

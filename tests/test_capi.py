@@ -77,27 +77,37 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     """pa_linear_rows / pa_qkv_append / pa_embed_rows reject bad arguments before any HIP call
     (the pointers below are never dereferenced: every case fails or returns on the host)."""
     A = 0x10000  # a 16-byte aligned stand-in address
+    F32, BF16 = _lib.PA_DTYPE_F32, _lib.PA_DTYPE_BF16
     lin = lib.pa_linear_rows
     # more than 64 rows
-    assert lin(A, 512, 65, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 512, 65, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"rows must be in [0, 64]" in lib.pa_last_error_message()
     # unknown activation
-    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 2, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 2, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # unknown element type
+    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, 7, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"bad dtype" in lib.pa_last_error_message()
     # misaligned activations
-    assert lin(A + 4, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A + 4, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # bf16 rows must start on 16-byte boundaries: a row stride of 516 bf16 values does not
+    assert lin(A, 516, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, BF16, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"multiple of 8" in lib.pa_last_error_message()
     # LayerNorm weight without bias
-    assert lin(A, 512, 4, 512, A, None, 512, A, None, 1e-5, 0, None, 0, A, 512, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 512, 4, 512, A, None, 512, A, None, 1e-5, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # in_features without a kernel
-    assert lin(A, 96, 4, 96, A, None, 32, None, None, 0.0, 0, None, 0, A, 32, None) == _lib.PA_ERR_UNSUPPORTED
+    assert lin(A, 96, 4, 96, A, None, 32, None, None, 0.0, 0, None, 0, A, 32, F32, None) == _lib.PA_ERR_UNSUPPORTED
     assert b"in_features" in lib.pa_last_error_message()
     # no rows: nothing to do
-    assert lin(None, 0, 0, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 0, None) == _lib.PA_OK
+    assert lin(None, 0, 0, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 0, BF16, None) == _lib.PA_OK
     # q/k/v: d_model must be heads x head_dim
     qkv = lib.pa_qkv_append
     assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 32, 16,
-               None) == _lib.PA_ERR_INVALID_ARGUMENT
+               F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"d_model" in lib.pa_last_error_message()
-    # embedding rows must be whole 16-byte vectors
+    assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 64, 16,
+               5, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # embedding rows must be whole 16-byte vectors: 4 fp32 or 8 bf16 values
     emb = lib.pa_embed_rows
-    assert emb(A, A, 2, 3, A, 100, A, 64, 6, A, 8, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert emb(A, A, 0, 3, A, 100, A, 64, 8, A, 8, None) == _lib.PA_OK
+    assert emb(A, A, 2, 3, A, 100, A, 64, 6, A, 8, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert emb(A, A, 2, 3, A, 100, A, 64, 12, A, 16, BF16, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert emb(A, A, 0, 3, A, 100, A, 64, 8, A, 8, F32, None) == _lib.PA_OK

@@ -146,3 +146,118 @@ def test_linear_rows_layernorm_every_width(device, K):
     x = torch.randn(M, K, device=device) * torch.linspace(0.1, 10, M, device=device).view(M, 1) + 3.0
     got = hip_linear.linear_rows_hip(x, lin, ln=ln, gelu=True)
     assert (got.double().cpu() - ref_linear(x, lin, ln, True)).abs().max().item() <= 5e-5
+
+
+# ---- bf16 weights and activations ------------------------------------------------------------
+
+def bf16_round(t):
+    return t.to(torch.bfloat16).double()
+
+
+def ref_linear_bf16(x, lin, ln=None, gelu=False, residual=None):
+    """fp64 arithmetic on the bf16 operands, with the rounding points of the fused kernel: the
+    LayerNorm output rounded to bf16 (as torch's bf16 LayerNorm), one rounding of the result."""
+    x = x.double().cpu()
+    if ln is not None:
+        x = bf16_round(nn.functional.layer_norm(x, (x.shape[1],), ln.weight.double().cpu(), ln.bias.double().cpu(),
+                                                ln.eps))
+    y = x @ lin.weight.double().cpu().t()
+    if lin.bias is not None:
+        y = y + lin.bias.double().cpu()
+    if gelu:
+        y = nn.functional.gelu(y)
+    if residual is not None:
+        y = y + residual.double().cpu()
+    return y
+
+
+def assert_bf16_close(got, want):
+    """Within one bf16 rounding of the result (2^-8 relative) plus fp32-accumulation slack."""
+    err = (got.double().cpu() - want).abs()
+    bound = 2.0 ** -8 * want.abs() + 2e-3 * want.abs().max().clamp_min(1e-3)
+    assert bool((err <= bound).all()), float((err - bound).max())
+
+
+@pytest.mark.parametrize("K", [128, 256, 512, 1024, 2048])
+@pytest.mark.parametrize("M", [1, 16, 40, 64])
+def test_linear_rows_bf16_shapes(device, K, M):
+    torch.manual_seed(100 + K + M)
+    N = 300
+    lin = nn.Linear(K, N).to(device).to(torch.bfloat16)
+    x = torch.randn(M, K, device=device).to(torch.bfloat16)
+    got = hip_linear.linear_rows_hip(x, lin)
+    assert got.dtype == torch.bfloat16
+    assert_bf16_close(got, ref_linear_bf16(x, lin))
+
+
+@pytest.mark.parametrize("K", [128, 512, 2048])
+@pytest.mark.parametrize("use_ln,gelu,res", [(True, False, False), (True, True, False), (False, False, True),
+                                             (True, True, True)])
+def test_linear_rows_bf16_fusions(device, K, use_ln, gelu, res):
+    torch.manual_seed(7 + K)
+    M, N = 9, 1000
+    lin = nn.Linear(K, N).to(device).to(torch.bfloat16)
+    ln = nn.LayerNorm(K).to(device)
+    with torch.no_grad():
+        ln.weight.normal_(1.0, 0.1)
+        ln.bias.normal_(0.0, 0.1)
+    ln = ln.to(torch.bfloat16)
+    x = (torch.randn(M, K, device=device) * 3 + 0.5).to(torch.bfloat16)
+    r = torch.randn(M, N, device=device).to(torch.bfloat16) if res else None
+    got = hip_linear.linear_rows_hip(x, lin, ln=ln if use_ln else None, gelu=gelu, residual=r)
+    assert_bf16_close(got, ref_linear_bf16(x, lin, ln if use_ln else None, gelu, r))
+
+
+def test_linear_rows_rejects_mixed_dtypes(device):
+    lin = nn.Linear(128, 32).to(device).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        hip_linear.linear_rows_hip(torch.randn(2, 128, device=device), lin)  # fp32 rows, bf16 weights
+
+
+@pytest.mark.parametrize("pool_dtype", [torch.float32, torch.bfloat16])
+def test_qkv_append_bf16(device, pool_dtype):
+    torch.manual_seed(19)
+    d, h, M, bs, nblk = 512, 8, 22, 16, 12
+    attn = _Attn(d, h).to(device).to(torch.bfloat16)
+    ln = nn.LayerNorm(d).to(device).to(torch.bfloat16)
+    x = torch.randn(M, d, device=device).to(torch.bfloat16)
+    k_pool = torch.zeros(nblk, h, bs, d // h, device=device, dtype=pool_dtype)
+    v_pool = torch.zeros_like(k_pool)
+    slots = torch.tensor([5 * bs + 3, -1, 0, 11 * bs + 15, 12 * bs, 2 * bs + 7] + [6 * bs + i for i in range(16)],
+                         dtype=torch.int32, device=device)
+    q = hip_linear.qkv_append_hip(x, ln, attn, k_pool, v_pool, slots)
+    assert q.dtype == torch.bfloat16
+    assert_bf16_close(q, ref_linear_bf16(x, attn.q_proj, ln))
+    kref = ref_linear_bf16(x, attn.k_proj, ln)
+    vref = ref_linear_bf16(x, attn.v_proj, ln)
+    for m, s in enumerate(slots.tolist()):
+        if s < 0 or s // bs >= nblk:
+            continue
+        for pool, ref in ((k_pool, kref), (v_pool, vref)):
+            got = pool[s // bs, :, s % bs].reshape(-1).unsqueeze(0)
+            assert_bf16_close(got, ref[m].unsqueeze(0))
+    written = (k_pool.float().abs().sum(dim=(1, 3)) > 0).cpu()
+    want = torch.zeros(nblk, bs, dtype=torch.bool)
+    for s in slots.tolist():
+        if 0 <= s and s // bs < nblk:
+            want[s // bs, s % bs] = True
+    assert torch.equal(written, want)
+
+
+def test_embed_rows_bf16(device):
+    """bf16 tables: each row is the fp32 sum of the two bf16 vectors, rounded once (bit-exact)."""
+    torch.manual_seed(11)
+    tok = nn.Embedding(300, 128).to(device).to(torch.bfloat16)
+    pos = nn.Embedding(64, 128).to(device).to(torch.bfloat16)
+    ids = torch.randint(0, 300, (2, 9), device=device)
+    ids[0, 3] = -1
+    p0 = torch.tensor([0, 60], device=device)
+    got = hip_linear.embed_rows_hip(ids, p0, tok, pos).cpu()
+    assert got.dtype == torch.bfloat16
+    want = torch.empty(18, 128, dtype=torch.bfloat16)
+    for b in range(2):
+        for t in range(9):
+            i = int(ids[b, t])
+            row = tok.weight[i].float().cpu() if 0 <= i < 300 else torch.zeros(128)
+            want[b * 9 + t] = (row + pos.weight[min(int(p0[b]) + t, 63)].float().cpu()).to(torch.bfloat16)
+    assert torch.equal(got, want)
