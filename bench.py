@@ -25,7 +25,7 @@ Also reported on the same line:
   continuous_batching_bf16_model  the same trace and weights with the model in bf16 (weights,
                  activations and KV; the decode steps through the bf16 fused kernels), GPU only.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-e2e]
-                       [--no-secondary] [--no-decode] [--calibrate-copy]
+                       [--no-secondary] [--no-decode] [--calibrate-copy] [--e2e-model fp32|bf16|both]
 (--no-decode skips the headline decode measurement; it is for profiling the other workloads alone.)
 """
 from __future__ import annotations
@@ -355,6 +355,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the headline decode (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true", help="also run a copy kernel of known size")
+    ap.add_argument("--e2e-model", choices=("fp32", "bf16", "both"), default="both",
+                    help="end-to-end runs: the fp32 model (with its CPU baseline), the bf16 model, or both")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -423,12 +425,14 @@ def main() -> int:
         log("secondary workloads (ragged fp32 decode, chunked prefill, large prefill)")
         result["secondary"] = secondary_workloads(dev, args.steps)
     if not args.no_e2e:
-        log("end-to-end continuous batching (200 requests, 32 req/s)")
-        result["continuous_batching"] = continuous_batching_pair(dev, with_cpu=not args.no_cpu_baseline)
-        log("end-to-end continuous batching with the model in bf16")
-        bf = continuous_batching(dev, dtype=torch.bfloat16)
-        bf["model_dtype"] = "bf16 (weights, activations, KV pools; fp32 accumulation)"
-        result["continuous_batching_bf16_model"] = bf
+        if args.e2e_model in ("fp32", "both"):
+            log("end-to-end continuous batching (200 requests, 32 req/s)")
+            result["continuous_batching"] = continuous_batching_pair(dev, with_cpu=not args.no_cpu_baseline)
+        if args.e2e_model in ("bf16", "both"):
+            log("end-to-end continuous batching with the model in bf16")
+            bf = continuous_batching(dev, dtype=torch.bfloat16)
+            bf["model_dtype"] = "bf16 (weights, activations, KV pools; fp32 accumulation)"
+            result["continuous_batching_bf16_model"] = bf
     print(json.dumps(result), flush=True)
     return 0
 
