@@ -53,6 +53,7 @@ struct LinArgs {
   const int32_t* slots;  // per row: block * block_size + offset, < 0 = skip
   int32_t H, Hd, bs;
   int32_t bf16;       // T = bf16 (else fp32)
+  int32_t cw_log2;    // output columns per workgroup: 1 << cw_log2 (4, 8 or 16)
 };
 
 // Wavefronts per workgroup (they split K): 16 at K = 2048 keeps more of the 128 KB weight tile in
@@ -110,9 +111,13 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   const int G = lane >> 4;
   const int c = lane & 15;
 
-  const int tiles_per_seg = (a.seg_n + 15) / 16;
+  // CW = 1 << cw_log2 output columns per workgroup (16, or 8 / 4 to spread a narrow layer over more
+  // compute units: a launch is limited by how fast each workgroup can pull its weight tile); the
+  // MFMA tile is always 16 wide, lanes c >= CW carry zero weights and load nothing.
+  const int cw = 1 << a.cw_log2;
+  const int tiles_per_seg = (a.seg_n + cw - 1) >> a.cw_log2;
   const int seg = blockIdx.x / tiles_per_seg;
-  const int n0 = (blockIdx.x - seg * tiles_per_seg) * 16;
+  const int n0 = (blockIdx.x - seg * tiles_per_seg) << a.cw_log2;
   const T* W = static_cast<const T*>(a.w[seg]);
   const int kb = w * KW + G * KL;
   const int r0 = blockIdx.y * kLinRows;  // first activation row of this workgroup
@@ -126,18 +131,18 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   uint32_t wv[NWD], xv[NWD], lgv[PRE ? NWD : 1], lbv[PRE ? NWD : 1];
   {
     const int n = n0 + c < a.seg_n ? n0 + c : a.seg_n - 1;  // clamp: the column is discarded
-    load_words(wv, W + (int64_t)n * a.K + kb, true);
+    load_words(wv, W + (int64_t)n * a.K + kb, c < cw);
     load_words(xv, static_cast<const T*>(a.x) + (int64_t)(row_ok ? r0 + c : 0) * a.x_stride + kb, row_ok);
     if constexpr (PRE) {
       load_words(lgv, static_cast<const T*>(a.ln_w) + kb, true);
       load_words(lbv, static_cast<const T*>(a.ln_b) + kb, true);
     }
   }
-  const int ml = (threadIdx.x >> 4) & 15;  // row within the tile
+  const int ml = (threadIdx.x >> a.cw_log2) & 15;  // epilogue thread (row ml, column cc) of the tile
   const int m = r0 + ml;
-  const int cc = threadIdx.x & 15;
+  const int cc = threadIdx.x & (cw - 1);
   const int n = n0 + cc;
-  const bool live = threadIdx.x < 256 && m < a.M && n < a.seg_n;
+  const bool live = (int)threadIdx.x < (kLinRows << a.cw_log2) && m < a.M && n < a.seg_n;
   float bias_v = 0.f, res_v = 0.f;
   if (live) {
     if (a.b[seg] != nullptr) bias_v = Elem<T>::load(static_cast<const T*>(a.b[seg]) + n);
@@ -247,8 +252,29 @@ static bool small_linear_k_supported(int32_t K) {
   return K == 128 || K == 256 || K == 512 || K == 1024 || K == 2048;
 }
 
-static int launch_small_linear(const LinArgs& a, hipStream_t stream) {
-  const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + 15) / 16);
+#ifndef PA_LIN_FORCE_CW_LOG2
+#define PA_LIN_FORCE_CW_LOG2 0
+#endif
+
+// Column tile width: the widest of 16, 8, 4 columns whose grid still has 192 workgroups with a
+// LayerNorm prologue (each workgroup normalises its rows again) or 128 without (else 4).
+// Measured inside graphs at 8 rows, fp32 / bf16 (us): fc2 (K 2048, N 512) 8.2 / 4.8 with 16
+// columns, 7.2 / 4.2 with 4; out_proj (K 512, N 512) 3.6 / 2.6 -> 3.3 / 2.7; LayerNorm + fc1
+// (N 2048) 4.9 / 3.9 with 16, 4.7 / 4.0 with 8, 6.4 / 5.3 with 4; lm_head (N 5000) best with 16.
+static int lin_cw_log2(const LinArgs& a) {
+  if (PA_LIN_FORCE_CW_LOG2) return PA_LIN_FORCE_CW_LOG2;
+  const int64_t target = a.ln_w != nullptr ? 192 : 128;
+  const int64_t row_tiles = (a.M + kLinRows - 1) / kLinRows;
+  for (int l2 = 4; l2 > 2; --l2) {
+    const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + (1 << l2) - 1) >> l2) * row_tiles;
+    if (tiles >= target) return l2;
+  }
+  return 2;
+}
+
+static int launch_small_linear(LinArgs a, hipStream_t stream) {
+  a.cw_log2 = lin_cw_log2(a);
+  const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + (1 << a.cw_log2) - 1) >> a.cw_log2);
   if (tiles > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
   const dim3 grid((unsigned)tiles, (unsigned)((a.M + kLinRows - 1) / kLinRows));
   const bool ln = a.ln_w != nullptr;
