@@ -14,10 +14,12 @@ Also reported on the same line:
   cpu_baseline   the oracle (C restatement of the reference's paged attention, fp64
                  accumulation) over the same batch on this host's cores, plus the rate of the
                  reference's own per-token torch loop on a small slice of it;
-  secondary      the ragged fp32 decode (8 requests x 6 layers), the chunked prefill (4 requests,
-                 fp32 and bf16 KV) and the large prefill (8 requests x 32 heads x 128, 512-token
-                 chunks over 1-4k contexts, bf16 and fp32 KV); MFMA utilisation against the fp32 /
-                 bf16 matrix peaks;
+  secondary      the single fp32 decode (1 request, 128 tokens), the ragged fp32 decode (8 requests
+                 x 6 layers), the chunked prefill (4 requests, fp32 and bf16 KV) and the large
+                 prefill (8 requests x 32 heads x 128, 512-token chunks over 1-4k contexts, bf16 and
+                 fp32 KV); MFMA utilisation against the fp32 / bf16 matrix peaks; for the first three
+                 also the same-run CPU times of one call (the oracle, and the reference's per-key
+                 torch loop, whole or on a scaled sample);
   continuous_batching  the end-to-end run: decoder LM (vocab 5000, d_model 512, 8 heads,
                  6 layers, d_ff 2048, KV block 16, fp32, weights N(0, 0.02)), 200 Poisson requests
                  at 32 req/s, max batch 8, prefill chunk 256, 1536-token iteration budget, greedy;
@@ -157,6 +159,61 @@ def reference_loop_rate(batch, tokens: int = 256) -> dict:
             "extrapolated_GBps": batch.decode_bytes() / whole / 1e9, "threads": torch.get_num_threads()}
 
 
+def _median_s(fn, reps: int = 3) -> float:
+    """One untimed call, then the median wall time of `reps` calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _attended(seq_lens, cur_lens, T: int) -> int:
+    """(query row, key) pairs the reference loop visits per head: row i of request b attends the
+    keys t <= L_b - C_b + i, all L_b keys for padded rows."""
+    return sum(min(L, L - C + i + 1) for L, C in zip(seq_lens, cur_lens) for i in range(T))
+
+
+def cpu_call_times(q, k_pool, v_pool, block_lists, seq_lens, cur_lens, loop_request: int | None = None) -> dict:
+    """Same-run CPU timings of one attention call on host copies of its inputs: the oracle (C
+    restatement, fp64 accumulation, all host threads) and the reference's own per-key torch loop,
+    each one untimed call then the median of 3. With `loop_request` set, the loop runs on that
+    request's head 0 only and its time is scaled by the ratio of attended (row, key) pairs."""
+    import torch
+
+    import oracle
+    from oracle.reference_loop import paged_attention_loop
+
+    nthreads = cpu_threads()
+    torch.set_num_threads(nthreads)
+    q, k_pool, v_pool = q.cpu(), k_pool.cpu(), v_pool.cpu()
+    B, H, T, _ = q.shape
+    kn, vn = oracle._np(k_pool), oracle._np(v_pool)
+    oracle_s = _median_s(lambda: oracle.paged_attention(q, kn, vn, block_lists, seq_lens, cur_lens,
+                                                        nthreads=nthreads))
+    total_pairs = H * _attended(seq_lens, cur_lens, T)
+    if loop_request is None:
+        loop_s = _median_s(lambda: paged_attention_loop(q, k_pool, v_pool, block_lists, seq_lens, cur_lens))
+        sample = "the whole call"
+        scale = 1.0
+    else:
+        r = loop_request
+        qs, ks, vs = q[r:r + 1, :1], k_pool[:, :1], v_pool[:, :1]
+        lists, sl, cl = [block_lists[r]], [seq_lens[r]], [cur_lens[r]]
+        loop_s = _median_s(lambda: paged_attention_loop(qs, ks, vs, lists, sl, cl))
+        part = _attended(sl, cl, T)
+        scale = total_pairs / part
+        sample = f"request {r}, head 0 ({part} of {total_pairs} row-key pairs), scaled by the pair count"
+    return {
+        "oracle_ms": round(1e3 * oracle_s, 3),
+        "reference_loop_ms": round(1e3 * loop_s * scale, 1),
+        "reference_loop_sample": sample,
+        "threads": nthreads,
+    }
+
+
 def time_call(fn, steps: int, warmup: int = 2) -> float:
     import torch
 
@@ -173,8 +230,38 @@ def time_call(fn, steps: int, warmup: int = 2) -> float:
     return e0.elapsed_time(e1) / steps
 
 
-def secondary_workloads(device, steps: int) -> dict:
-    """Ragged fp32 decode (8 requests x 6 layers) and chunked prefill (fp32 and bf16 KV)."""
+def time_graph_call(fn, calls: int = 20, replays: int = 5) -> float:
+    """Milliseconds per call of `fn` replayed from one HIP graph of `calls` back-to-back calls (the
+    way the serving loop replays its decode steps): no Python or launch cost per call."""
+    import torch
+
+    fn()  # eager first: workspaces are allocated outside the capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (replays * calls)
+
+
+def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
+    """Single decode, ragged fp32 decode (8 requests x 6 layers), chunked prefill (fp32 and bf16
+    KV) and large prefill; with `with_cpu`, the same-run CPU timings of the first three."""
     import torch
 
     from src import workloads
@@ -182,19 +269,48 @@ def secondary_workloads(device, steps: int) -> dict:
         kv_append_hip, pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
 
     res = {}
-    per_layer = []
+    b = workloads.single_decode(seed=0, device=device)
+    call = lambda: paged_attention_decode_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    ms = time_call(call, steps)
+    gms = time_graph_call(call)
+    res["single_decode_fp32"] = {
+        "workload": "1 request, 8 heads x 64, 128 cached tokens in 8 of 64 shuffled blocks, fp32",
+        "us_per_call": round(1e3 * ms, 2), "us_per_call_graph": round(1e3 * gms, 2),
+        "bytes_per_call": b.decode_bytes(), "GBps_graph": round(b.decode_bytes() / (gms * 1e-3) / 1e9, 1),
+        "note": "us_per_call: eager back-to-back calls through the Python wrapper (host-bound at this size); "
+                "us_per_call_graph: the same call replayed from a HIP graph",
+    }
+    if with_cpu:
+        log("CPU timings: single decode")
+        res["single_decode_fp32"]["cpu"] = cpu_call_times(b.q, b.k_pool, b.v_pool, b.block_lists, b.seq_lens,
+                                                          b.cur_lens)
+    per_layer, cpu_layers = [], []
     for layer in range(6):
         b = workloads.ragged_decode(seed=0, layer=layer, device=device)
-        ms = time_call(lambda: paged_attention_decode_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t,
-                                                          b.cur_lens_t), steps)
-        per_layer.append((ms, b.decode_bytes()))
-    ms_tot = sum(m for m, _ in per_layer)
-    by_tot = sum(x for _, x in per_layer)
+        call = lambda: paged_attention_decode_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+        ms = time_call(call, steps)
+        gms = time_graph_call(call)
+        per_layer.append((ms, b.decode_bytes(), gms))
+        if with_cpu:
+            log(f"CPU timings: ragged decode layer {layer}")
+            cpu_layers.append(cpu_call_times(b.q, b.k_pool, b.v_pool, b.block_lists, b.seq_lens, b.cur_lens))
+        del b
+    ms_tot = sum(m for m, _, _ in per_layer)
+    by_tot = sum(x for _, x, _ in per_layer)
+    g_tot = sum(g for _, _, g in per_layer)
     res["ragged_decode_fp32_6_layers"] = {
         "workload": "8 requests, 8 heads x 64, lengths U[128,1024], 4096-block pool, fp32, one call per layer",
         "us_per_layer": round(1e3 * ms_tot / 6, 2), "GBps": round(by_tot / (ms_tot * 1e-3) / 1e9, 1),
+        "us_per_layer_graph": round(1e3 * g_tot / 6, 2), "GBps_graph": round(by_tot / (g_tot * 1e-3) / 1e9, 1),
         "bytes_per_layer": by_tot // 6,
     }
+    if with_cpu:
+        res["ragged_decode_fp32_6_layers"]["cpu"] = {
+            "oracle_ms_per_layer": round(sum(c["oracle_ms"] for c in cpu_layers) / 6, 3),
+            "reference_loop_ms_per_layer": round(sum(c["reference_loop_ms"] for c in cpu_layers) / 6, 1),
+            "reference_loop_sample": "every layer's whole call",
+            "threads": cpu_layers[0]["threads"],
+        }
     for kv_dtype, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16kv")):
         w = workloads.chunked_prefill(seed=0, device=device, kv_dtype=kv_dtype)
         B = len(w["prev_lens"])
@@ -221,6 +337,11 @@ def secondary_workloads(device, steps: int) -> dict:
             "useful_gflop": round(flops / 1e9, 4), "TFLOPs": round(tfs, 2),
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
         }
+        if with_cpu:  # the pools already hold the appended chunks
+            log(f"CPU timings: chunked prefill ({tag})")
+            res[f"chunked_prefill_{tag}"]["cpu"] = cpu_call_times(
+                w["q"], w["k_pool"], w["v_pool"], lists, w["seq_lens"], w["chunk_lens"], loop_request=0)
+        del w
     for kv_dtype, tag in ((torch.bfloat16, "bf16kv"), (torch.float32, "fp32")):
         b = workloads.large_prefill(seed=0, device=device, kv_dtype=kv_dtype)
         H, Hd = b.q.shape[1], b.q.shape[3]
@@ -422,8 +543,8 @@ def main() -> int:
     if args.calibrate_copy:
         calibration_copy(dev)
     if not args.no_secondary:
-        log("secondary workloads (ragged fp32 decode, chunked prefill, large prefill)")
-        result["secondary"] = secondary_workloads(dev, args.steps)
+        log("secondary workloads (single and ragged fp32 decode, chunked prefill, large prefill)")
+        result["secondary"] = secondary_workloads(dev, args.steps, with_cpu=not args.no_cpu_baseline)
     if not args.no_e2e:
         if args.e2e_model in ("fp32", "both"):
             log("end-to-end continuous batching (200 requests, 32 req/s)")

@@ -275,30 +275,58 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
   }
 }
 
-// Merge the partial records of each (request, head) written by its active splits (the number a
-// split computes from the request's length): one wavefront per pair.
+// Merge the partial records (m, l, acc[HD]) of each (request, head) written by its active splits
+// (the number a split computes from the request's length): one wavefront per pair. The loads are
+// spread over the lanes and issued together: lane s reads split s's (m, l) for the maximum and
+// the denominator, and each lane's head_dim element is summed over the splits with the weights
+// broadcast from the lane that computed them, eight independent loads at a time. (A loop over
+// the splits with one dependent load chain per split cost 4-10 us at 4-8 splits.)
 template <typename IO>
 __global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh % a.H;
   const int HD = a.head_dim;
+  const int lane = threadIdx.x;
   int nb = (valid_keys(a.seq_lens[b], a.cur_lens[b], 0) + 15) / 16;
   nb = nb < a.max_pages ? nb : a.max_pages;
   const int nact = nb > 0 ? (nb + a.split_blocks - 1) / a.split_blocks : 1;
   if (nact == 1) return;  // the split wrote the output itself
-  const float* base = a.ws + (int64_t)bh * a.num_splits * (HD + 2);
-  float M = kNegBig;
-  for (int s = 0; s < nact; ++s) M = fmaxf(M, base[(int64_t)s * (HD + 2)]);
+  const int64_t R = HD + 2;
+  const float* base = a.ws + (int64_t)bh * a.num_splits * R;
+  // Lane s holds split s's (m, l) for the first 64 splits; more splits are read in further passes.
+  float m0 = kNegBig, l0 = 0.f;
+  if (lane < nact) {
+    m0 = base[lane * R];
+    l0 = base[lane * R + 1];
+  }
+  float M = m0;
+  for (int s = lane + kWave; s < nact; s += kWave) M = fmaxf(M, base[s * R]);
+  M = wave_max(M);
+  const float f0 = lane < nact ? fast_exp2(m0 - M) : 0.f;  // weight of split `lane`, 0 past the splits
+  float lsum = l0 * f0;
+  for (int s = lane + kWave; s < nact; s += kWave) lsum = fmaf(base[s * R + 1], fast_exp2(base[s * R] - M), lsum);
+  lsum = wave_sum(lsum);
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
-  for (int d = threadIdx.x; d < HD; d += kWave) {
-    float lsum = 0.f, A = 0.f;
-    for (int s = 0; s < nact; ++s) {
-      const float* rec = base + (int64_t)s * (HD + 2);
-      const float f = fast_exp2(rec[0] - M);
-      lsum = fmaf(rec[1], f, lsum);
-      A = fmaf(rec[2 + d], f, A);
+  for (int d = lane; d - lane < HD; d += kWave) {
+    const int dd = d < HD ? d : HD - 1;  // every lane takes part in the broadcasts
+    float A = 0.f;
+    for (int s0 = 0; s0 < nact; s0 += kWave) {
+      const int n = nact - s0 < kWave ? nact - s0 : kWave;
+      const float f = s0 == 0 ? f0 : (lane < n ? fast_exp2(base[(s0 + lane) * R] - M) : 0.f);
+      const float* rec = base + s0 * R + 2 + dd;
+      // 8 loads in flight: indices past the last split are clamped to it (a valid record) and
+      // get weight 0 (lane j0 + jj <= 63 since j0 <= n - 1 rounded down to a multiple of 8).
+      for (int j0 = 0; j0 < n; j0 += 8) {
+        float x[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) x[jj] = rec[(j0 + jj < n ? j0 + jj : n - 1) * R];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          A = fmaf(x[jj], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), j0 + jj)), A);
+      }
     }
-    Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
+    if (d < HD) Elem<IO>::store(op + d, A * inv);
   }
 }
 

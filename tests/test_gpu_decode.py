@@ -96,6 +96,23 @@ def test_split_path_matches_oracle_and_unsplit(device, split_blocks):
     assert torch.equal(got, run(b, split_blocks=split_blocks))
 
 
+@pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("split_blocks", [1, 5, 64])
+def test_split_path_hd128_bf16_kv(device, split_blocks, io_dtype):
+    # 1-block splits give 190 records for the longest request (merged 64 per pass), 64-block
+    # splits one or two; lengths 0 and 16 leave a single split that writes the output itself
+    lens = [0, 16, 17, 1023, 3031]
+    b = make_batch(device, 11, lens, [1] * 5, H=4, Hd=128, kv_dtype=torch.bfloat16, io_dtype=io_dtype)
+    print(f"split decode hd128 bf16 KV split_blocks={split_blocks} io={io_dtype}", flush=True)
+    got = run(b, split_blocks=split_blocks)
+    want = oracle.paged_attention(b.q.float().cpu(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists, b.seq_lens,
+                                  b.cur_lens, nthreads=NTHREADS)
+    tol = 1e-4 if io_dtype == torch.float32 else 1e-2
+    assert max_err(got, want) <= tol
+    assert max_err(got, run(b, split_blocks=0).float().cpu().numpy()) <= (1e-5 if io_dtype == torch.float32 else 1e-2)
+    assert torch.count_nonzero(got[0]).item() == 0
+
+
 @pytest.mark.parametrize("Hd,bs", [(16, 8), (32, 16), (96, 16), (64, 32), (80, 4)])
 def test_generic_kernel_shapes(device, Hd, bs):
     lens = [1, 9, 40, 130]
