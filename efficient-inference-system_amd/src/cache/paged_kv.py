@@ -27,6 +27,7 @@ BatchedPagedKVCache.device_metadata().
 """
 from __future__ import annotations
 
+import itertools
 import math
 from dataclasses import dataclass, field
 
@@ -365,7 +366,8 @@ class BatchedPagedKVCache:
         buf[B + 1:2 * B + 1] = prev
         buf[2 * B + 1:3 * B + 1] = app
         if total:
-            buf[3 * B + 1:] = np.fromiter((i for s in self.states for i in s.block_ids), dtype=np.int32, count=total)
+            buf[3 * B + 1:] = np.fromiter(itertools.chain.from_iterable([s.block_ids for s in self.states]),
+                                          dtype=np.int32, count=total)
         return buf, max(counts, default=0)
 
     def _append_batch_device(self, k_new: torch.Tensor, v_new: torch.Tensor, lengths: list[int]) -> torch.Tensor:

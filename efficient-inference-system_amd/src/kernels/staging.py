@@ -3,78 +3,115 @@
 Allocating fresh pinned memory for every upload (torch's `pin_memory()`) costs far more than the
 copy itself when the previous buffers are still in flight. Here each device owns a ring of pinned
 slots; an upload copies into the next slot, enqueues an asynchronous copy on the current stream
-and records an event, and a slot is reused only after its event has completed (normally long
-before the ring wraps).
+and records the slot's event, and a slot is reused only after its event has completed (normally
+long before the ring wraps).
+
+The copy and the event go straight to the HIP runtime that torch has loaded (hipMemcpyAsync,
+hipEventRecord on raw pointers, one event per slot created once): through torch tensor views,
+`copy_` and a new event per upload, the per-step metadata upload of the serving loop cost about
+16 us of host time.
 """
 from __future__ import annotations
+
+import ctypes
+import os
 
 import numpy as np
 import torch
 
 _SLOT_BYTES = 256 * 1024
 _SLOTS = 32
+_H2D = 1  # hipMemcpyHostToDevice
+_EVENT_DISABLE_TIMING = 0x2
+
+
+class _Hip:
+    """The entry points of torch's HIP runtime (torch/lib/libamdhip64.so) that the ring uses."""
+
+    def __init__(self):
+        path = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
+        lib = ctypes.CDLL(path)
+        vp = ctypes.c_void_p
+        for name, args in (("hipMemcpyAsync", [vp, vp, ctypes.c_size_t, ctypes.c_int, vp]),
+                           ("hipEventCreateWithFlags", [ctypes.POINTER(vp), ctypes.c_uint]),
+                           ("hipEventRecord", [vp, vp]),
+                           ("hipEventSynchronize", [vp])):
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        self.memcpy_async = lib.hipMemcpyAsync
+        self.event_create = lib.hipEventCreateWithFlags
+        self.event_record = lib.hipEventRecord
+        self.event_sync = lib.hipEventSynchronize
+
+
+_hip: _Hip | None = None
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed with HIP error {status}")
 
 
 class _PinnedRing:
     def __init__(self, device: torch.device):
+        global _hip
+        if _hip is None:
+            _hip = _Hip()
         self.device = device
         self.host = torch.empty(_SLOTS * _SLOT_BYTES, dtype=torch.uint8, pin_memory=True)
         self.host_np = self.host.numpy()
-        self.events: list[torch.cuda.Event | None] = [None] * _SLOTS
+        self.host_ptr = self.host.data_ptr()
+        with torch.cuda.device(device):
+            self.events = []
+            for _ in range(_SLOTS):
+                ev = ctypes.c_void_p()
+                _check(_hip.event_create(ctypes.byref(ev), _EVENT_DISABLE_TIMING), "hipEventCreateWithFlags")
+                self.events.append(ev)
+        self.pending = [False] * _SLOTS
         self.next = 0
 
     def upload_into(self, arr: np.ndarray, dst: torch.Tensor) -> None:
-        """Asynchronous copy of arr into the first arr.nbytes bytes of the device tensor dst
-        (contiguous), through the next pinned slot."""
+        """Asynchronous copy of the contiguous array arr into the leading bytes of the contiguous
+        device tensor dst on the current stream, through the next pinned slot (arrays larger
+        than a slot through torch's own pinned copy, which tracks that buffer's lifetime)."""
         nbytes = arr.nbytes
         if nbytes > _SLOT_BYTES:
-            dst.view(-1).view(torch.uint8)[:nbytes].copy_(torch.from_numpy(arr.view(np.uint8).reshape(-1)).pin_memory(),
-                                                          non_blocking=True)
+            src = torch.from_numpy(arr.view(np.uint8).reshape(-1)).pin_memory()
+            dst.view(-1).view(torch.uint8)[:nbytes].copy_(src, non_blocking=True)
             return
+        stream = torch.cuda.current_stream(self.device).cuda_stream
         i = self.next
         self.next = (i + 1) % _SLOTS
         ev = self.events[i]
-        if ev is not None:
-            ev.synchronize()
-        self.host_np[i * _SLOT_BYTES:i * _SLOT_BYTES + nbytes] = arr.view(np.uint8).reshape(-1)
-        dst.view(-1).view(torch.uint8)[:nbytes].copy_(self.host[i * _SLOT_BYTES:i * _SLOT_BYTES + nbytes],
-                                                      non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
-        self.events[i] = ev
-
-    def upload(self, arr: np.ndarray) -> torch.Tensor:
-        nbytes = arr.nbytes
-        if nbytes > _SLOT_BYTES:
-            return torch.from_numpy(arr).pin_memory().to(self.device, non_blocking=True)
-        i = self.next
-        self.next = (i + 1) % _SLOTS
-        ev = self.events[i]
-        if ev is not None:
-            ev.synchronize()
-        view = self.host_np[i * _SLOT_BYTES:i * _SLOT_BYTES + nbytes]
-        view[:] = arr.view(np.uint8).reshape(-1)
-        src = self.host[i * _SLOT_BYTES:i * _SLOT_BYTES + nbytes]
-        out = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-        out.copy_(src, non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
-        self.events[i] = ev
-        return out.view(torch.from_numpy(arr[:0]).dtype)
+        if self.pending[i]:
+            _check(_hip.event_sync(ev), "hipEventSynchronize")
+        off = i * _SLOT_BYTES
+        self.host_np[off:off + nbytes] = arr.view(np.uint8).reshape(-1)
+        _check(_hip.memcpy_async(dst.data_ptr(), self.host_ptr + off, nbytes, _H2D, stream), "hipMemcpyAsync")
+        _check(_hip.event_record(ev, stream), "hipEventRecord")
+        self.pending[i] = True
 
 
 _rings: dict[int, _PinnedRing] = {}
+
+
+def _ring(device: torch.device) -> _PinnedRing:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ring = _rings.get(idx)
+    if ring is None:
+        ring = _rings[idx] = _PinnedRing(torch.device("cuda", idx))
+    return ring
 
 
 def upload(arr: np.ndarray, device: torch.device) -> torch.Tensor:
     """Asynchronously copy a contiguous numpy array to `device`; returns a flat device tensor of
     the same dtype, valid in stream order on the current stream."""
     arr = np.ascontiguousarray(arr)
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    ring = _rings.get(idx)
-    if ring is None:
-        ring = _rings[idx] = _PinnedRing(torch.device("cuda", idx))
-    return ring.upload(arr)
+    out = torch.empty(arr.size, dtype=torch.from_numpy(arr[:0]).dtype, device=device)
+    if arr.nbytes:
+        _ring(out.device).upload_into(arr, out)
+    return out
 
 
 def upload_into(arr: np.ndarray, dst: torch.Tensor) -> None:
@@ -83,9 +120,5 @@ def upload_into(arr: np.ndarray, dst: torch.Tensor) -> None:
     arr = np.ascontiguousarray(arr)
     if not dst.is_contiguous() or dst.numel() * dst.element_size() < arr.nbytes:
         raise ValueError("upload_into: destination must be contiguous and large enough")
-    device = dst.device
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    ring = _rings.get(idx)
-    if ring is None:
-        ring = _rings[idx] = _PinnedRing(torch.device("cuda", idx))
-    ring.upload_into(arr, dst)
+    if arr.nbytes:
+        _ring(dst.device).upload_into(arr, dst)
