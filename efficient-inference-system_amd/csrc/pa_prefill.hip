@@ -77,6 +77,29 @@ struct PrefillShape {
 template <typename KV>
 constexpr int prefill_waves() { return std::is_same<KV, float>::value ? 8 : 4; }
 
+// KV tiles each wavefront keeps in flight ahead of the one it folds. Measured in graph replay
+// (16-row kernel): at head_dim 64 one tile is best (chunked workload 4 x 8 heads, bf16 KV 13.6 us
+// at 1, 14.5 at 2, 15.0 at 3; fp32 22.8 us at 1, 29.5 at 2, where the registers cost a
+// wavefront per SIMD); at head_dim 128, 4 requests x 32 heads, 256-token chunks over ~1k
+// contexts, bf16 KV 109.6 us at 1, 102-105 at 2 or 3; fp32 KV spills beyond 1.
+#ifndef PA_PREFILL_DEPTH_F32_64
+#define PA_PREFILL_DEPTH_F32_64 1
+#endif
+#ifndef PA_PREFILL_DEPTH_F32_128
+#define PA_PREFILL_DEPTH_F32_128 1
+#endif
+#ifndef PA_PREFILL_DEPTH_BF16_64
+#define PA_PREFILL_DEPTH_BF16_64 1
+#endif
+#ifndef PA_PREFILL_DEPTH_BF16_128
+#define PA_PREFILL_DEPTH_BF16_128 2
+#endif
+template <typename KV, int HD>
+constexpr int prefill_depth() {
+  return std::is_same<KV, float>::value ? (HD == 64 ? PA_PREFILL_DEPTH_F32_64 : PA_PREFILL_DEPTH_F32_128)
+                                        : (HD == 64 ? PA_PREFILL_DEPTH_BF16_64 : PA_PREFILL_DEPTH_BF16_128);
+}
+
 template <typename KV, typename IO, int HD>
 __global__ __launch_bounds__(prefill_waves<KV>() * kWave) void prefill_mfma_kernel(const AttnArgs a) {
   constexpr int BS = 16;
@@ -231,31 +254,38 @@ __global__ __launch_bounds__(prefill_waves<KV>() * kWave) void prefill_mfma_kern
   };
 
   // This wave's blocks j = jb + w + k*NW, k < mine, in chunks of one page-table entry per lane.
-  // The next block's tile loads into the second register set while the current one is folded;
-  // the steady-state loop issues its loads unconditionally so the compiler's wait counts stay
-  // exact, and the tail is peeled.
+  // D tiles load into a ring of D + 1 register sets while the oldest one is folded; the
+  // steady-state loop issues its loads unconditionally so the compiler's wait counts stay exact,
+  // and the tail is peeled (the prologue's guarded loads also cover walks of at most D tiles).
   const int span = je - jb;
   const int mine = span > w ? (span - w + NW - 1) / NW : 0;
+  constexpr int D = prefill_depth<KV, HD>();  // tiles in flight ahead of the one being folded
+  constexpr int S = D + 1;                // register slots
   for (int c0 = 0; c0 < mine; c0 += kWave) {
     const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
     int ids = -1;
     if (lane < cnt) ids = pt[jb + w + (c0 + lane) * NW];
     auto jidx = [&](int k) { return jb + w + (c0 + k) * NW; };
-    Tile t0, t1;
-    issue(t0, __builtin_amdgcn_readlane(ids, 0));
+    auto put = [&](Tile& t, int k) { issue(t, __builtin_amdgcn_readlane(ids, k)); };
+    Tile t[S];
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+      if (k < cnt) put(t[k], k);
     int k = 0;
-    for (; k + 2 < cnt; k += 2) {
-      issue(t1, __builtin_amdgcn_readlane(ids, k + 1));
-      fold(t0, jidx(k));
-      issue(t0, __builtin_amdgcn_readlane(ids, k + 2));
-      fold(t1, jidx(k + 1));
+    for (; k + D + S - 1 < cnt; k += S) {
+#pragma unroll
+      for (int u = 0; u < S; ++u) {
+        put(t[(u + D) % S], k + u + D);
+        fold(t[u], jidx(k + u));
+      }
     }
-    if (k + 1 < cnt) {
-      issue(t1, __builtin_amdgcn_readlane(ids, k + 1));
-      fold(t0, jidx(k));
-      fold(t1, jidx(k + 1));
-    } else {
-      fold(t0, jidx(k));
+    // Drain: at most S + D - 1 tiles remain; k % S == 0 here, so tile k + u sits in slot u % S.
+#pragma unroll
+    for (int u = 0; u < S + D - 1; ++u) {
+      if (k + u < cnt) {
+        if (k + u + D < cnt) put(t[(u + D) % S], k + u + D);
+        fold(t[u % S], jidx(k + u));
+      }
     }
   }
 
