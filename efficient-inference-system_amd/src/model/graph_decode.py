@@ -48,6 +48,7 @@ from src.kernels.hip_paged_attention import (
 from src.kernels.staging import upload_into
 
 T_BUCKETS = (16, 32, 64, 128, 256)
+FP32_WIDE_ROWS = 32  # fp32 fused steps above this many rows use torch for fc2 and lm_head
 
 
 def graphs_enabled() -> bool:
@@ -198,9 +199,16 @@ class GraphedStep:
         return m.lm_head(m.ln_f(x))
 
     def _fused_layers(self, cap: _Captured, pools, x, pt, seq32, slots) -> torch.Tensor:
-        """The layers of a step through the fused kernels; x is [B * Tb, d_model] (<= 64 rows)."""
+        """The layers of a step through the fused kernels; x is [B * Tb, d_model] (<= 64 rows).
+        fp32 steps of more than FP32_WIDE_ROWS rows run fc2 and LayerNorm + lm_head through torch:
+        the fused kernel reads its weight tile once per 16 rows, and for those two layers (the
+        largest weights per output column) torch's GEMM wins there. Measured in graph replay at
+        48 / 64 rows: fc2 + residual 9.9 / 12.3 us fused vs 9.1 / 9.3 torch, LayerNorm + lm_head
+        14.3 / 18.3 vs 12.4 / 12.3; at 32 rows and below, and for the other layers and bf16, the
+        fused kernels are faster (e.g. LayerNorm + q/k/v + append 8.5 vs 28.9 us at 64 rows)."""
         m = self.model
         B, Tb = cap.B, cap.Tb
+        torch_wide = B * Tb > FP32_WIDE_ROWS and x.dtype == torch.float32
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
@@ -212,8 +220,14 @@ class GraphedStep:
                 o = paged_attention_prefill_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
             x1 = hip_linear.linear_rows_hip(o.transpose(1, 2).reshape(B * Tb, a.d_model), a.out_proj, residual=x)
             h = hip_linear.linear_rows_hip(x1, blk.mlp[0], ln=blk.ln2, gelu=True)
-            x = hip_linear.linear_rows_hip(h, blk.mlp[2], residual=x1)
-        logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
+            if torch_wide:
+                x = blk.mlp[2](h) + x1
+            else:
+                x = hip_linear.linear_rows_hip(h, blk.mlp[2], residual=x1)
+        if torch_wide:
+            logits = m.lm_head(m.ln_f(x))
+        else:
+            logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
         return logits.view(B, Tb, -1)
 
     def _capture(self, cap: _Captured, pools) -> None:
