@@ -1,4 +1,4 @@
-"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32 or bf16, <= 64 rows).
+"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32 or bf16, <= 1024 rows).
 
   linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
   qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
@@ -18,7 +18,7 @@ import torch.nn as nn
 
 from src.kernels import _lib
 
-MAX_ROWS = 64
+MAX_ROWS = 1024  # rows per call accepted by the library (16-row tiles)
 SUPPORTED_FEATURES = (128, 256, 512, 1024, 2048)
 
 
@@ -55,7 +55,7 @@ def supported(linear: nn.Linear) -> bool:
 
 def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | None = None, gelu: bool = False,
                     residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 64); x, the layer's
+    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 1024); x, the layer's
     parameters, residual and out share one dtype (float32 or bfloat16)."""
     _rows(x, "x")
     dt = x.dtype

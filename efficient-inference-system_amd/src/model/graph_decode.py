@@ -14,12 +14,13 @@ whole step once per (batch size, query-length bucket) and replays it:
                              kernel otherwise), output projection, MLP and residuals; final
                              LayerNorm and lm_head.
 
-Steps of at most 64 rows (B * bucketed T: every decode step of up to 64 requests, short prefill
-chunks) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
+Steps of at most FUSED_STEP_ROWS rows (B * bucketed T: every decode step, and prefill chunks up
+to 384 rows) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
 shapes allow: per layer one launch for LayerNorm + q/k/v projections + KV append, the attention
 (decode or chunked prefill kernel), one for the output projection + residual, one for LayerNorm +
-fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. Set PAGED_HIP_FUSED_DECODE=0 to use
-the torch layers instead.
+fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. A fused launch reads its weight tile
+once per 16 rows, so above a per-layer row count (FUSED_ROWS) that layer runs through torch
+instead. Set PAGED_HIP_FUSED_DECODE=0 to use the torch layers throughout.
 
 Query lengths T > 1 are padded up to a bucket (16, 32, 64, 128, 256) with token id 0 and the
 logits of the real rows are returned. Padded rows are never appended to the cache (their slots
@@ -48,7 +49,23 @@ from src.kernels.hip_paged_attention import (
 from src.kernels.staging import upload_into
 
 T_BUCKETS = (16, 32, 64, 128, 256)
-FP32_WIDE_ROWS = 32  # fp32 fused steps above this many rows use torch for fc2 and lm_head
+
+# Largest step (rows = B * bucketed T) for which each fused launch beats torch's layers, per
+# dtype. Measured in HIP-graph replay on MI355X (fused vs torch, us), d_model 512, d_ff 2048,
+# vocab 5000:
+#   LayerNorm + q/k/v + append  fp32 8.5 vs 28.9 at 64 rows, 20.4 vs 27.0 at 256, 26.7 vs 27.7 at 384
+#   out_proj + residual         fp32 6.3 vs 8.2 at 256, 8.2 vs 8.3 at 384; bf16 6.2 vs 7.4 at 512
+#   LayerNorm + fc1 + GELU      fp32 14.1 vs 14.3 at 128, 19.3 vs 15.2 at 192; bf16 11.9 vs 13.5 at
+#                               192, 14.8 vs 13.9 at 256
+#   fc2 + residual              fp32 9.4 vs 10.4 at 32, 9.9 vs 9.1 at 48; bf16 6.5 vs 7.8 at 128,
+#                               9.7 vs 8.9 at 192
+#   LayerNorm + lm_head         fp32 11.0 vs 11.7 at 32, 14.3 vs 12.4 at 48; bf16 9.1 vs 10.7 at 48,
+#                               11.2 vs 11.0 at 64
+FUSED_ROWS = {
+    torch.float32: {"qkv": 384, "out_proj": 384, "fc1": 128, "fc2": 32, "lm_head": 32},
+    torch.bfloat16: {"qkv": 384, "out_proj": 384, "fc1": 192, "fc2": 128, "lm_head": 48},
+}
+FUSED_STEP_ROWS = 384  # steps above this run the torch layers (q/k/v and out_proj limits)
 
 
 def graphs_enabled() -> bool:
@@ -131,7 +148,7 @@ class _Captured:
         # Allocated outside the capture and referenced here, so the address the graph records
         # stays valid for the graph's lifetime.
         self.ws = _workspace(device, ws_bytes) if ws_bytes else None
-        self.fused = B * Tb <= hip_linear.MAX_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
+        self.fused = B * Tb <= FUSED_STEP_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
         emb_dt = model.token_emb.weight.dtype
         self.embed_fused = (fused_decode_enabled() and emb_dt in hip_linear.DTYPES
                             and model.pos_emb.weight.dtype == emb_dt
@@ -199,16 +216,13 @@ class GraphedStep:
         return m.lm_head(m.ln_f(x))
 
     def _fused_layers(self, cap: _Captured, pools, x, pt, seq32, slots) -> torch.Tensor:
-        """The layers of a step through the fused kernels; x is [B * Tb, d_model] (<= 64 rows).
-        fp32 steps of more than FP32_WIDE_ROWS rows run fc2 and LayerNorm + lm_head through torch:
-        the fused kernel reads its weight tile once per 16 rows, and for those two layers (the
-        largest weights per output column) torch's GEMM wins there. Measured in graph replay at
-        48 / 64 rows: fc2 + residual 9.9 / 12.3 us fused vs 9.1 / 9.3 torch, LayerNorm + lm_head
-        14.3 / 18.3 vs 12.4 / 12.3; at 32 rows and below, and for the other layers and bf16, the
-        fused kernels are faster (e.g. LayerNorm + q/k/v + append 8.5 vs 28.9 us at 64 rows)."""
+        """The layers of a step through the fused kernels; x is [B * Tb, d_model] with at most
+        FUSED_STEP_ROWS rows. Layers whose FUSED_ROWS limit the step exceeds run through torch."""
         m = self.model
         B, Tb = cap.B, cap.Tb
-        torch_wide = B * Tb > FP32_WIDE_ROWS and x.dtype == torch.float32
+        lim = FUSED_ROWS[x.dtype]
+        rows = B * Tb
+        fc1_fused, fc2_fused, head_fused = rows <= lim["fc1"], rows <= lim["fc2"], rows <= lim["lm_head"]
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
@@ -218,16 +232,19 @@ class GraphedStep:
                 o = paged_attention_decode_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
             else:
                 o = paged_attention_prefill_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
-            x1 = hip_linear.linear_rows_hip(o.transpose(1, 2).reshape(B * Tb, a.d_model), a.out_proj, residual=x)
-            h = hip_linear.linear_rows_hip(x1, blk.mlp[0], ln=blk.ln2, gelu=True)
-            if torch_wide:
-                x = blk.mlp[2](h) + x1
+            x1 = hip_linear.linear_rows_hip(o.transpose(1, 2).reshape(rows, a.d_model), a.out_proj, residual=x)
+            if fc1_fused:
+                h = hip_linear.linear_rows_hip(x1, blk.mlp[0], ln=blk.ln2, gelu=True)
             else:
+                h = blk.mlp[1](blk.mlp[0](blk.ln2(x1)))
+            if fc2_fused:
                 x = hip_linear.linear_rows_hip(h, blk.mlp[2], residual=x1)
-        if torch_wide:
-            logits = m.lm_head(m.ln_f(x))
-        else:
+            else:
+                x = blk.mlp[2](h) + x1
+        if head_fused:
             logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
+        else:
+            logits = m.lm_head(m.ln_f(x))
         return logits.view(B, Tb, -1)
 
     def _capture(self, cap: _Captured, pools) -> None:

@@ -159,10 +159,11 @@ int pa_zero_blocks(void* k_pool, void* v_pool, int pool_dtype, int64_t num_block
  * Decode-step linear layers of the model around the paged attention (fp32, at most 64 token rows).
  * No reference counterpart as entry points: they replace the torch nn.Linear / nn.LayerNorm /
  * nn.GELU calls of the reference's cached forward (src/model/transformer.py:30-35,
- * src/model/attention.py:46-48,64) on one-token steps and short prefill chunks, where a step is
- * a few rows against every weight matrix.
+ * src/model/attention.py:46-48,64) on one-token steps and prefill chunks, where a step is a
+ * few rows against every weight matrix. A workgroup reads its weight tile once per 16 rows, so
+ * they pay off up to 32-512 rows depending on the layer; rows is at most 1024.
  *
- * pa_linear_rows: out[m, :] = act(LN(x[m, :]) W^T + bias) + residual[m, :] for m < rows (<= 64).
+ * pa_linear_rows: out[m, :] = act(LN(x[m, :]) W^T + bias) + residual[m, :] for m < rows.
  *   dtype (PA_DTYPE_F32 or PA_DTYPE_BF16) is the element type of x, weight, bias, LayerNorm
  *   parameters, residual and out alike; products accumulate in fp32 (bf16: LN(x) is rounded to
  *   bf16 before the product, as torch's bf16 LayerNorm output is, and out is rounded once);
@@ -186,7 +187,7 @@ int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int32_t in_fea
  * vectors of head_dim, into pool slot slot_mapping[m] of the K and V pools (converted to the pool
  * dtype; slot < 0 or a block outside [0, num_blocks) skips the row). dtype is the element type of
  * x, the weights, biases, LayerNorm parameters and q_out (as pa_linear_rows). Replaces
- * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 64 and
+ * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 1024 and
  * d_model in {128, 256, 512, 1024, 2048}.
  */
 int pa_qkv_append(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,

@@ -79,9 +79,9 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     A = 0x10000  # a 16-byte aligned stand-in address
     F32, BF16 = _lib.PA_DTYPE_F32, _lib.PA_DTYPE_BF16
     lin = lib.pa_linear_rows
-    # more than 64 rows
-    assert lin(A, 512, 65, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert b"rows must be in [0, 64]" in lib.pa_last_error_message()
+    # more than 1024 rows
+    assert lin(A, 512, 1025, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"rows must be in [0, 1024]" in lib.pa_last_error_message()
     # unknown activation
     assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 2, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # unknown element type
@@ -104,6 +104,9 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 32, 16,
                F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"d_model" in lib.pa_last_error_message()
+    assert qkv(A, 512, 1025, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 64, 16,
+               F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"rows must be in [0, 1024]" in lib.pa_last_error_message()
     assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 64, 16,
                5, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # embedding rows must be whole 16-byte vectors: 4 fp32 or 8 bf16 values

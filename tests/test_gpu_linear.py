@@ -1,6 +1,6 @@
 """Decode-step linear kernels (pa_linear_rows, pa_qkv_append) against float64 torch on the CPU:
 LayerNorm prologue, bias / GELU / residual epilogues, every supported in_features, ragged
-out_features, 1..64 rows (1-4 row tiles), and the K/V scatter into fp32 and bf16 pools (bit-exact placement,
+out_features, 1..1024 rows (1-64 row tiles), and the K/V scatter into fp32 and bf16 pools (bit-exact placement,
 skipped slots untouched)."""
 import pytest
 import torch
@@ -26,7 +26,7 @@ def ref_linear(x, lin, ln=None, gelu=False, residual=None):
 
 
 @pytest.mark.parametrize("K", [128, 256, 512, 1024, 2048])
-@pytest.mark.parametrize("M", [1, 3, 16, 17, 40, 64])
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 40, 64, 200, 1024])
 def test_linear_rows_shapes(device, K, M):
     torch.manual_seed(K + M)
     N = 300 if K != 512 else 5000  # out_features not a multiple of 16 (partial last tile)
@@ -72,7 +72,7 @@ def test_linear_rows_rejects_bad_shapes(device):
         hip_linear.linear_rows_hip(torch.randn(2, 96, device=device), lin)  # in_features 96 unsupported
     lin = nn.Linear(128, 32).to(device)
     with pytest.raises(ValueError):
-        hip_linear.linear_rows_hip(torch.randn(65, 128, device=device), lin)  # more than 64 rows
+        hip_linear.linear_rows_hip(torch.randn(1025, 128, device=device), lin)  # more than 1024 rows
 
 
 class _Attn(nn.Module):
@@ -83,17 +83,19 @@ class _Attn(nn.Module):
 
 
 @pytest.mark.parametrize("pool_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("d,h", [(512, 8), (128, 2)])
-def test_qkv_append(device, pool_dtype, d, h):
+@pytest.mark.parametrize("d,h,M", [(512, 8, 22), (128, 2, 22), (512, 8, 300)])
+def test_qkv_append(device, pool_dtype, d, h, M):
     torch.manual_seed(9)
-    M, bs, nblk = 22, 16, 12  # two row tiles
+    bs = 16
+    nblk = 12 if M <= 22 else 40  # 22 rows: two row tiles; 300 rows: 19, the last one partial
     attn = _Attn(d, h).to(device)
     ln = nn.LayerNorm(d).to(device)
     x = torch.randn(M, d, device=device)
     k_pool = torch.zeros(nblk, h, bs, d // h, device=device, dtype=pool_dtype)
     v_pool = torch.zeros_like(k_pool)
-    slots = torch.tensor([5 * bs + 3, -1, 0, 11 * bs + 15, 12 * bs, 2 * bs + 7] + [6 * bs + i for i in range(16)],
-                         dtype=torch.int32, device=device)
+    head = [5 * bs + 3, -1, 0, 11 * bs + 15, 12 * bs, 2 * bs + 7]  # 12 * bs: outside a 12-block pool
+    rest = [6 * bs + i for i in range(16)] if M == 22 else [13 * bs + i for i in range(M - len(head))]
+    slots = torch.tensor(head + rest, dtype=torch.int32, device=device)
     q = hip_linear.qkv_append_hip(x, ln, attn, k_pool, v_pool, slots)
     xn = nn.functional.layer_norm(x.double().cpu(), (d,), ln.weight.double().cpu(), ln.bias.double().cpu(), ln.eps)
     assert (q.double().cpu() - ref_linear(xn, attn.q_proj)).abs().max().item() <= 2e-5
@@ -179,7 +181,7 @@ def assert_bf16_close(got, want):
 
 
 @pytest.mark.parametrize("K", [128, 256, 512, 1024, 2048])
-@pytest.mark.parametrize("M", [1, 16, 40, 64])
+@pytest.mark.parametrize("M", [1, 16, 40, 64, 200])
 def test_linear_rows_bf16_shapes(device, K, M):
     torch.manual_seed(100 + K + M)
     N = 300
