@@ -1,7 +1,8 @@
 """Build libpaged_hip.so (the C-ABI paged-attention library) for gfx950 with hipcc.
 
 Every `csrc/*.hip` file is compiled to an object under `_build/` and linked into
-`libpaged_hip.so` next to this file. The library links against the HIP runtime that torch bundles
+`libpaged_hip.so` next to this file; `csrc/host/paged_host.cpp` becomes the CPython module
+`src/cache/_paged_host` (native host bookkeeping of graph steps). The library links against the HIP runtime that torch bundles
 (rpath to torch/lib), so a process that imports torch and then loads the library maps a single
 HIP runtime. Usage: `python build_lib.py [--verbose]`.
 """
@@ -71,8 +72,25 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(msg, flush=True)
 
 
+HOST_SRC = CSRC / "host" / "paged_host.cpp"
+HOST_DIR = PKG_DIR / "src" / "cache"
+
+
+def build_host(verbose: bool = False) -> Path:
+    """Compile the native host bookkeeping module (CPython extension, plain g++ against this
+    interpreter's headers) to src/cache/_paged_host<EXT_SUFFIX>; returns its path."""
+    import sysconfig
+
+    out = HOST_DIR / ("_paged_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    _run([cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wextra",
+          f"-I{sysconfig.get_paths()['include']}", str(HOST_SRC), "-o", str(out) + ".tmp"], verbose)
+    os.replace(str(out) + ".tmp", out)
+    return out
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile all sources and link the library; returns the library path."""
+    """Compile all sources and link the library (and the host module); returns the library path."""
     hipcc = _hipcc()
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
@@ -94,6 +112,7 @@ def build(verbose: bool = False) -> Path:
         link += [f"-L{tlib}", f"-Wl,-rpath,{tlib}"]
     _run(link, verbose)
     os.replace(str(LIB_PATH) + ".tmp", LIB_PATH)
+    build_host(verbose)
     return LIB_PATH
 
 

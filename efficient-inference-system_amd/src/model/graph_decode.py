@@ -48,6 +48,11 @@ from src.kernels.hip_paged_attention import (
     pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
 from src.kernels.staging import upload_into
 
+try:  # native host bookkeeping (csrc/host/paged_host.cpp): same results as the Python below
+    from src.cache import _paged_host as _host
+except ImportError:  # not built: the Python versions run
+    _host = None
+
 T_BUCKETS = (16, 32, 64, 128, 256)
 
 # Largest step (rows = B * bucketed T) for which each fused launch beats torch's layers, per
@@ -101,6 +106,13 @@ def _signature(pools) -> tuple:
 
 
 def _lockstep(kv_caches: list[BatchedPagedKVCache], max_new_blocks: int) -> bool:
+    """_lockstep_py through the native module when it is built."""
+    if _host is not None:
+        return _host.lockstep(kv_caches, max_new_blocks)
+    return _lockstep_py(kv_caches, max_new_blocks)
+
+
+def _lockstep_py(kv_caches: list[BatchedPagedKVCache], max_new_blocks: int) -> bool:
     """True when all layers hold identical states and pools, so this step's allocations are the
     same in every layer and one metadata pack serves them all. Block lists are compared whole;
     of the free lists, the lengths and the last max_new_blocks ids: a step pops at most that many
@@ -274,11 +286,16 @@ class GraphedStep:
         device = input_ids.device
         pools = [c.pool for c in kv_caches]
         app = [max(min(c, T), 0) for c in current_lengths]
-        prev = None
-        for cache in kv_caches:
-            p = cache.host_append(app, T, m.num_heads, m.head_dim, pools[0].dtype, device)
-            prev = p if prev is None else prev
-        buf, max_pages = kv_caches[0].csr_buffer(prev, app)
+        if _host is not None:
+            prev = _host.host_append(kv_caches, app, m.num_heads, m.head_dim, pools[0].dtype, device)
+            raw, max_pages = _host.csr(kv_caches[0].states, prev, app)
+            buf = np.frombuffer(raw, dtype=np.int32)
+        else:
+            prev = None
+            for cache in kv_caches:
+                p = cache.host_append(app, T, m.num_heads, m.head_dim, pools[0].dtype, device)
+                prev = p if prev is None else prev
+            buf, max_pages = kv_caches[0].csr_buffer(prev, app)
         pages = max(math.ceil(m.max_seq_len / m.kv_block_size), max_pages)
         sig = _signature(pools)
         key = (B, Tb)
