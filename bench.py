@@ -25,7 +25,9 @@ Also reported on the same line:
                  at 32 req/s, max batch 8, prefill chunk 256, 1536-token iteration budget, greedy;
                  tokens/s and p50 TTFT on the scheduler's virtual clock, plus wall time;
   continuous_batching_bf16_model  the same trace and weights with the model in bf16 (weights,
-                 activations and KV; the decode steps through the bf16 fused kernels), GPU only.
+                 activations and KV; the decode steps through the bf16 fused kernels), GPU only;
+  continuous_batching_saturated  the fp32 model on the same request mix with every request
+                 arriving at once (the serving path's capacity at max batch 8), GPU only.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-e2e]
                        [--no-secondary] [--no-decode] [--calibrate-copy] [--e2e-model fp32|bf16|both]
 (--no-decode skips the headline decode measurement; it is for profiling the other workloads alone.)
@@ -390,9 +392,10 @@ def init_weights_normal(model, std: float = 0.02) -> None:
                 mod.bias.zero_()
 
 
-def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True, dtype=None) -> dict:
+def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True, dtype=None,
+                        rate: float = 32.0) -> dict:
     """The end-to-end benchmark trace through the continuous scheduler on `device` (model weights
-    and activations in `dtype`, default fp32)."""
+    and activations in `dtype`, default fp32; Poisson arrivals at `rate` requests per second)."""
     import torch
 
     from src.config import benchmark_serving_request_mix
@@ -419,7 +422,7 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True,
         # capture the HIP graphs of cached steps (batch sizes 1..8, chunk buckets, decode) here,
         # outside the timed run
         graphs_prepared = model.prepare_graphs(8, device)
-    reqs = generate_requests(200, 32.0, 5000, workload_profiles=benchmark_serving_request_mix(), seed=42)
+    reqs = generate_requests(200, rate, 5000, workload_profiles=benchmark_serving_request_mix(), seed=42)
     sched = ContinuousBatchingScheduler(max_batch_size=8, prefill_chunk_size=256, max_tokens_per_iteration=1536)
     dev = str(device) if device.type == "cuda" else "cpu"
     t0 = time.perf_counter()
@@ -431,7 +434,7 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True,
             release_request_cache=lambda r: model.release_request_caches(r.kv_caches),
         )
     wall = time.perf_counter() - t0
-    s = summarize_run(done, events, 32.0, 8, 0.0, "continuous", 256, 0)
+    s = summarize_run(done, events, rate, 8, 0.0, "continuous", 256, 0)
     return {
         "tokens_per_s": s["throughput_tokens_per_s"],
         "p50_ttft_ms": s["p50_first_token_latency_ms"],
@@ -554,6 +557,14 @@ def main() -> int:
             bf = continuous_batching(dev, dtype=torch.bfloat16)
             bf["model_dtype"] = "bf16 (weights, activations, KV pools; fp32 accumulation)"
             result["continuous_batching_bf16_model"] = bf
+        if args.e2e_model in ("fp32", "both"):
+            # The benchmark rate (32 req/s) bounds the GPU's tokens/s by the arrivals; with every
+            # request arriving at once the same scheduler (max batch 8) shows the serving path's
+            # capacity, comparable with the CPU baseline's compute-bound rate above.
+            log("end-to-end continuous batching, saturated (200 requests arriving at once)")
+            sat = continuous_batching(dev, rate=1.0e6)
+            sat["arrivals"] = "the same 200-request mix, Poisson at 1e6 req/s (all within ~1 ms)"
+            result["continuous_batching_saturated"] = sat
     print(json.dumps(result), flush=True)
     return 0
 
