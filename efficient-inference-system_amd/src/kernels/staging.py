@@ -30,7 +30,9 @@ class _Hip:
 
     def __init__(self):
         path = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
-        lib = ctypes.CDLL(path)
+        # a torch built against the system ROCm has no bundled copy: the runtime it loaded is
+        # found by its soname
+        lib = ctypes.CDLL(path if os.path.exists(path) else "libamdhip64.so")
         vp = ctypes.c_void_p
         for name, args in (("hipMemcpyAsync", [vp, vp, ctypes.c_size_t, ctypes.c_int, vp]),
                            ("hipEventCreateWithFlags", [ctypes.POINTER(vp), ctypes.c_uint]),
