@@ -378,7 +378,11 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
       if (NST > 2 && st + 1 < nsteps) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NDMA));  // vmcnt(2 * NDMA)
       else __builtin_amdgcn_s_waitcnt(0x0F70);                                           // vmcnt(0)
       __syncthreads();
+      // The next stage's loads are issued at raised priority too, so they start right after
+      // the barrier (286.0 -> 278.2 us, head_dim 128, three interleaved runs).
+      __builtin_amdgcn_s_setprio(1);
       if (st + NST - 1 < nsteps) issue_loads(st + NST - 1, en, skn, svn);
+      __builtin_amdgcn_s_setprio(0);
       if (st < wsteps) compute(skc, svc, st, ec);
     };
     if constexpr (NST == 3) {
