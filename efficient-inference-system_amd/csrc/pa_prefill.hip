@@ -73,7 +73,8 @@ struct PrefillShape {
 
 // Wavefronts per workgroup of the 16-row kernel (they split each tile's KV blocks). Measured on
 // the chunked-prefill workload (4 x 8 heads x 64, up to 58 blocks per tile): fp32 KV 26.6 us with
-// 4, 24.3 us with 8, 39.7 us with 2; bf16 KV 15.3 us with 4 or 8, 19.4 us with 2.
+// 4, 24.3 us with 8, 39.7 us with 2, 30.4 us with 16 (and spills at head_dim 128); bf16 KV 15.3 us
+// with 4 or 8, 19.4 us with 2.
 template <typename KV>
 constexpr int prefill_waves() { return std::is_same<KV, float>::value ? 8 : 4; }
 
