@@ -87,18 +87,18 @@ __device__ __forceinline__ int load_now(const int32_t* p) {
 // of the tile's last row; ties by unit index), heads innermost, so the longest tiles start first
 // and the short ones fill the end of the grid (contexts of different lengths otherwise leave a
 // tail of long tiles running alone). Every workgroup ranks the units itself, one per thread, using
-// `lds` (kWideWaves * kWave + 1 ints) as scratch. Returns false when there are more units than
-// threads; the caller then keeps wide_unit's order.
-constexpr int kOrderMax = kWideWaves * kWave;
-__device__ __forceinline__ bool wide_lpt_unit(const AttnArgs& a, int ntiles, int* lds, int& bh, int& qt) {
+// `lds` (NTH + 1 ints) as scratch. Returns false when there are more units than threads; the
+// caller then keeps wide_unit's order. ROWS = query rows per tile, NTH = threads per workgroup.
+template <int ROWS, int NTH>
+__device__ __forceinline__ bool tile_lpt_unit(const AttnArgs& a, int ntiles, int* lds, int& bh, int& qt) {
   const int U = a.B * ntiles;
-  if (U > kOrderMax) return false;
+  if (U > NTH) return false;
   const int tid = threadIdx.x;
   int key = 0;
   if (tid < U) {
     const int b = tid / ntiles;
     const int t = tid - b * ntiles;
-    const int last = t * kWideRows + kWideRows - 1 < a.T - 1 ? t * kWideRows + kWideRows - 1 : a.T - 1;
+    const int last = t * ROWS + ROWS - 1 < a.T - 1 ? t * ROWS + ROWS - 1 : a.T - 1;
     key = valid_keys(a.seq_lens[b], a.cur_lens[b], last);
     lds[tid] = key;
   }
@@ -110,15 +110,19 @@ __device__ __forceinline__ bool wide_lpt_unit(const AttnArgs& a, int ntiles, int
       const int k2 = lds[u];
       rank += (k2 > key) || (k2 == key && u < tid);
     }
-    if (rank == pos) lds[kOrderMax] = tid;
+    if (rank == pos) lds[NTH] = tid;
   }
   __syncthreads();
-  const int unit = __builtin_amdgcn_readfirstlane(lds[kOrderMax]);
+  const int unit = __builtin_amdgcn_readfirstlane(lds[NTH]);
   __syncthreads();  // the scratch is reused by the caller
   const int b = unit / ntiles;
   qt = unit - b * ntiles;
   bh = b * a.H + (blockIdx.x - pos * a.H);
   return true;
+}
+constexpr int kOrderMax = kWideWaves * kWave;
+__device__ __forceinline__ bool wide_lpt_unit(const AttnArgs& a, int ntiles, int* lds, int& bh, int& qt) {
+  return tile_lpt_unit<kWideRows, kOrderMax>(a, ntiles, lds, bh, qt);
 }
 
 // NSUB = 32-key sub-tiles per step: the per-step costs (barrier, mask test, max/sum exchange,
