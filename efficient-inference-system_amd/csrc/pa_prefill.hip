@@ -1,7 +1,7 @@
 // Chunked causal prefill attention over paged KV for gfx950, on matrix cores.
 //
-// Work unit = (request, head, tile of 16 query rows). One workgroup of 8 (fp32 KV) or 4 (bf16 KV)
-// wavefronts per unit and KV split; the wavefronts take the split's KV blocks round-robin and
+// Work unit = (request, head, tile of 16 query rows). One workgroup of 4 wavefronts per unit and
+// KV split; the wavefronts take the split's KV blocks round-robin and
 // merge their online-softmax states in LDS at the end. For each 16-token KV block a wavefront
 // computes the transposed score tile S^T = K Q^T (16 keys x 16 queries) and accumulates the
 // transposed output O^T += V^T P^T.
@@ -87,18 +87,21 @@ struct PrefillShape {
   static constexpr int VW = kBf16 ? DT / 2 : DT;  // 32-bit words per V row per lane per block
 };
 
-// Wavefronts per workgroup of the 16-row kernel (they split each tile's KV blocks). Measured on
-// the chunked-prefill workload (4 x 8 heads x 64, up to 58 blocks per tile): fp32 KV 26.6 us with
-// 4, 24.3 us with 8, 39.7 us with 2, 30.4 us with 16 (and spills at head_dim 128); bf16 KV 15.3 us
-// with 4 or 8, 19.4 us with 2.
+// Wavefronts per workgroup of the 16-row kernel (they split each tile's KV blocks). Measured in
+// graph replay with the die-aware unit order: fp32 KV 20.4 us with 4, 22.5 us with 8, 27.8 us with
+// 8 and two tiles in flight, 29.2 us with 16 on the chunked-prefill workload (4 x 8 heads x 64);
+// 217 against 252 us with 8 on 4 x 32 heads x 128, 256-token chunks over 0.6-1.2k contexts; within
+// 0.4 us either way on single requests. bf16 KV: 12.3-12.7 us with 4, 13.4-13.8 with 8, 19.0 with
+// 16 (chunked workload), 99 against 128 us with 8 (4 x 32 heads x 128).
 template <typename KV>
-constexpr int prefill_waves() { return std::is_same<KV, float>::value ? 8 : 4; }
+constexpr int prefill_waves() { return 4; }
 
 // KV tiles each wavefront keeps in flight ahead of the one it folds. Measured in graph replay
 // (16-row kernel): at head_dim 64 one tile is best (chunked workload 4 x 8 heads, bf16 KV 13.6 us
 // at 1, 14.5 at 2, 15.0 at 3; fp32 22.8 us at 1, 29.5 at 2, where the registers cost a
-// wavefront per SIMD); at head_dim 128, 4 requests x 32 heads, 256-token chunks over ~1k
-// contexts, bf16 KV 109.6 us at 1, 102-105 at 2 or 3; fp32 KV spills beyond 1.
+// wavefront per SIMD; with 4 wavefronts per workgroup and the die-aware order, 20.0 at 1 and 20.9
+// at 2); at head_dim 128, 4 requests x 32 heads, 256-token chunks over ~1k contexts, bf16 KV
+// 109.6 us at 1, 102-105 at 2 or 3; fp32 KV spills beyond 1.
 #ifndef PA_PREFILL_DEPTH_F32_64
 #define PA_PREFILL_DEPTH_F32_64 1
 #endif
@@ -117,8 +120,14 @@ constexpr int prefill_depth() {
                                         : (HD == 64 ? PA_PREFILL_DEPTH_BF16_64 : PA_PREFILL_DEPTH_BF16_128);
 }
 
-template <typename KV, typename IO, int HD>
-__global__ __launch_bounds__(prefill_waves<KV>() * kWave) void prefill_mfma_kernel(const AttnArgs a) {
+// OCC4: registers capped at 128 so that 4 wavefronts share a SIMD (4 workgroups per CU instead of
+// 3). Only fp32 KV at head_dim 64 is near the cap (129 registers unconstrained, 128 and two
+// spilled values capped); the launch takes the capped build when the grid would not fit on the
+// GPU at 3 workgroups per CU (8 x 8 heads x 256 rows, 1024 workgroups: 39.3 -> 33.3 us), and the
+// unconstrained one otherwise (chunked workload, 512 workgroups: 20.4 us against 21.3 capped).
+template <typename KV, typename IO, int HD, bool OCC4 = false>
+__global__ __launch_bounds__(prefill_waves<KV>() * kWave) __attribute__((amdgpu_waves_per_eu(OCC4 ? 4 : 1)))
+void prefill_mfma_kernel(const AttnArgs a) {
   constexpr int BS = 16;
   constexpr int NW = prefill_waves<KV>();
   using Sh = PrefillShape<KV, HD>;
@@ -388,7 +397,16 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
 template <typename KV, typename IO>
 static bool dispatch_prefill_io(const AttnArgs& a, dim3 grid, hipStream_t stream) {
   constexpr int threads = prefill_waves<KV>() * kWave;
-  if (a.head_dim == 64) { prefill_mfma_kernel<KV, IO, 64><<<grid, threads, 0, stream>>>(a); return true; }
+  if (a.head_dim == 64) {
+    if constexpr (std::is_same<KV, float>::value) {
+      if ((int64_t)grid.x > 3 * (int64_t)pa_host::device_cu_count()) {
+        prefill_mfma_kernel<KV, IO, 64, true><<<grid, threads, 0, stream>>>(a);
+        return true;
+      }
+    }
+    prefill_mfma_kernel<KV, IO, 64><<<grid, threads, 0, stream>>>(a);
+    return true;
+  }
   if (a.head_dim == 128) { prefill_mfma_kernel<KV, IO, 128><<<grid, threads, 0, stream>>>(a); return true; }
   return false;
 }
