@@ -421,14 +421,29 @@ static bool prefill_fast_shape(int32_t head_dim, int32_t block_size) {
   return block_size == 16 && (head_dim == 64 || head_dim == 128);
 }
 
-// Kernel choice: the wide-tile kernel when its (request, head, 128-row tile) units fill the GPU
-// at least twice over, else the 16-row kernel. PAGED_HIP_PREFILL_KERNEL=wide / tile
-// forces one of them (tests use it to cover both at small sizes).
-static bool use_wide_prefill(int32_t batch, int32_t num_heads, int32_t query_len) {
+// Kernel choice between the wide-tile kernel (128 query rows per workgroup) and the 16-row one, by
+// the wide kernel's unit count U = B * H * ceil(T / 128) against the CU count, graph replay on
+// MI355X (16-row / wide, us):
+//   bf16 KV   U = 256: 102.7 / 49.7 (4 x 32 heads x 128, T 256, ~1k contexts), 172.6 / 75.1
+//             (2 x 32, T 512, ~2k), 278.0 / 111.7 (1 x 32, T 1024, 3k), 61.1 / 30.5 (head_dim 64);
+//             U = 128: 147.3 / 114.4 (2 x 32 x 128, T 256, 3-4k contexts), 19.8 / 20.6 (8 x 8 x 64,
+//             T 256, 0-700 contexts);
+//   fp32 KV   U = 256, head_dim 128: 227.6 / 214.6, 416.6 / 351.3, 688.8 / 556.1; head_dim 64:
+//             112.7 / 132.6; U = 128: 365.1 / 582.0 (head_dim 128), 34.3 / 83.3 (64).
+// So: the wide kernel from U >= 2 CUs always; for bf16 KV from U >= CUs, or U >= CUs / 2 when the
+// page table spans at least 128 blocks (2048-token contexts, the host's bound on the longest
+// request); for fp32 KV at head_dim 128 from U >= CUs. PAGED_HIP_PREFILL_KERNEL=wide / tile forces
+// one of them (tests use it to cover both at small sizes).
+static bool use_wide_prefill(int kv_dtype, int32_t head_dim, int32_t batch, int32_t num_heads, int32_t query_len,
+                             int32_t max_pages) {
   const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
   if (env != nullptr && strcmp(env, "wide") == 0) return true;
   if (env != nullptr && strcmp(env, "tile") == 0) return false;
-  return prefill_wide_units(batch, num_heads, query_len) >= 2 * (int64_t)pa_host::device_cu_count();
+  const int64_t units = prefill_wide_units(batch, num_heads, query_len);
+  const int64_t cus = pa_host::device_cu_count();
+  if (units >= 2 * cus) return true;
+  if (kv_dtype == PA_DTYPE_BF16) return units >= cus || (2 * units >= cus && max_pages >= 128);
+  return head_dim == 128 && units >= cus;
 }
 
 static int prefill_num_splits(int32_t max_pages, int32_t split_blocks) {
@@ -485,7 +500,7 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 
   if (!prefill_fast_shape(head_dim, block_size)) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
   if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
-      use_wide_prefill(batch, num_heads, query_len))
+      use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len, max_pages))
     return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
 
   const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);
