@@ -181,6 +181,19 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
   const int h = u / nsplit;
   const int b = a.order ? a.order[bi] : bi;
 
+  // The first chunk of this wave's page-table entries (block jb0 + w + lane * NW) does not depend
+  // on the request's length: load it now, clamped into the row, so that it travels with the
+  // length loads instead of after them (one dependent memory round trip less before the first
+  // KV tile; graph replay: single decode 3.27 -> 3.19 us, ragged 8 x 8 heads 9.16 -> 9.08 us per
+  // layer). Entries past the request's blocks are discarded below.
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+  const int jb0 = nsplit > 1 ? split * a.split_blocks : 0;
+  int ids0 = -1;
+  if (a.max_pages > 0) {
+    const int idx = jb0 + w + lane * NW;
+    ids0 = pt[idx < a.max_pages ? idx : a.max_pages - 1];
+  }
+
   const int L = a.seq_lens[b];
   const int C = a.cur_lens[b];
   const int n = valid_keys(L, C, 0);
@@ -214,7 +227,6 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
   const int64_t tile_elems = (int64_t)BS * HD;
   const int64_t head_off = (int64_t)h * tile_elems;
   const int64_t blk_stride = (int64_t)a.H * tile_elems;
-  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
 
   // This wave's blocks: j = jb + w + k*NW for k < mine, in chunks of one page-table entry per lane.
   const int span = je - jb;
@@ -222,7 +234,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
   for (int c0 = 0; c0 < mine; c0 += kWave) {
     const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
     int ids = -1;
-    if (lane < cnt) ids = pt[jb + w + (c0 + lane) * NW];
+    if (lane < cnt) ids = c0 == 0 ? ids0 : pt[jb + w + (c0 + lane) * NW];
     stream_tiles<KV, HD, BS, PA_DECODE_DEPTH, PA_DECODE_NT != 0, R>(
         cnt, ids, (jb + w + c0 * NW) * BS + g, NW * BS, kpool, vpool, blk_stride, head_off, a.num_blocks, lane,
         qv, n, m, l, acc);
