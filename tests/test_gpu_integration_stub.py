@@ -1,5 +1,6 @@
-"""The ctypes binding shown in INTEGRATION.md (the stub a maintainer of the reference would add)
-is executed verbatim and checked against the oracle, so the documented binding stays correct."""
+"""The ctypes binding a maintainer of the reference would add (the "Option B" Python block of the
+integration guide at the repository root, read from that file) is executed verbatim and checked
+against the oracle, so the published binding stays correct."""
 import re
 from pathlib import Path
 
