@@ -361,6 +361,32 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
         }
         del b
         torch.cuda.empty_cache()
+    # A mid-size prefill: 4 x 32 heads x 128 with 256-token chunks is one 128-row unit per CU, where
+    # the dispatch takes the wide kernel for bf16 KV; the 16-row kernel is timed beside it.
+    b = workloads.large_prefill(seed=0, device=device, batch=4, chunk=256, ctx_lo=512, ctx_hi=1536)
+    H, Hd = b.q.shape[1], b.q.shape[3]
+    flops = workloads.prefill_flops(b.extra["prev_lens"], b.cur_lens, H, Hd)
+    call = lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    ms = time_call(call, steps)
+    prev = os.environ.get("PAGED_HIP_PREFILL_KERNEL")
+    os.environ["PAGED_HIP_PREFILL_KERNEL"] = "tile"
+    try:
+        ms_tile = time_call(call, steps)
+    finally:
+        if prev is None:
+            del os.environ["PAGED_HIP_PREFILL_KERNEL"]
+        else:
+            os.environ["PAGED_HIP_PREFILL_KERNEL"] = prev
+    tfs = flops / (ms * 1e-3) / 1e12
+    res["mid_prefill_bf16kv"] = {
+        "workload": f"{b.batch} requests, {H} heads x {Hd}, context {b.extra['prev_lens']} + chunk 256 each, "
+                    "bf16 KV, fp32 q/out (default dispatch: wide-tile kernel, one unit per CU)",
+        "attention_us": round(1e3 * ms, 1), "attention_us_16row_kernel": round(1e3 * ms_tile, 1),
+        "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1), "mfma_peak_TFLOPs": 2500.0,
+        "mfma_frac": round(tfs / 2500.0, 4),
+    }
+    del b
+    torch.cuda.empty_cache()
     return res
 
 
@@ -546,7 +572,7 @@ def main() -> int:
     if args.calibrate_copy:
         calibration_copy(dev)
     if not args.no_secondary:
-        log("secondary workloads (single and ragged fp32 decode, chunked prefill, large prefill)")
+        log("secondary workloads (single and ragged fp32 decode, chunked, large and mid-size prefill)")
         result["secondary"] = secondary_workloads(dev, args.steps, with_cpu=not args.no_cpu_baseline)
     if not args.no_e2e:
         if args.e2e_model in ("fp32", "both"):
