@@ -15,9 +15,11 @@ Also reported on the same line:
                  accumulation) over the same batch on this host's cores, plus the rate of the
                  reference's own per-token torch loop on a small slice of it;
   secondary      the single fp32 decode (1 request, 128 tokens), the ragged fp32 decode (8 requests
-                 x 6 layers), the chunked prefill (4 requests, fp32 and bf16 KV) and the large
+                 x 6 layers), the chunked prefill (4 requests, fp32 and bf16 KV), the large
                  prefill (8 requests x 32 heads x 128, 512-token chunks over 1-4k contexts, bf16 and
-                 fp32 KV); MFMA utilisation against the fp32 / bf16 matrix peaks; for the first three
+                 fp32 KV) and a mid-size bf16 prefill (4 requests x 32 heads x 128, 256-token
+                 chunks, with the 16-row kernel timed beside the default dispatch); MFMA
+                 utilisation against the fp32 / bf16 matrix peaks; for the first three
                  also the same-run CPU times of one call (the oracle, and the reference's per-key
                  torch loop, whole or on a scaled sample);
   continuous_batching  the end-to-end run: decoder LM (vocab 5000, d_model 512, 8 heads,
