@@ -9,6 +9,8 @@
 // keeps its own online-softmax state (max m, sum l, acc) for the rows it sees, so the inner loop
 // needs no cross-row exchange. Groups merge with shuffles after the loop; wavefronts merge in LDS.
 // The next block's K and V are loaded into a second register set while the current one is used.
+#include <mutex>
+
 #include "pa_attention.h"
 
 // Tuning knobs (compile-time): wavefronts per workgroup, blocks loaded ahead of the one being
@@ -472,15 +474,18 @@ extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int
   return (size_t)batch * num_heads * s * (head_dim + 2) * sizeof(float);
 }
 
-extern "C" int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                         void* out, int64_t out_stride_b, int64_t out_stride_h, int io_dtype,
-                         const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
-                         const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
-                         const int32_t* seq_lens, const int32_t* cur_lens, const int32_t* order,
-                         int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
-                         float scale, int32_t split_blocks,
-                         void* workspace, size_t workspace_bytes, void* stream_) {
-  pa_host::clear_error();
+// Shared body of pa_decode and pa_decode_noalloc. `ws_limit_is_scratch` only changes the error
+// reported when the split records do not fit: the caller's workspace is too small (pa_decode) or
+// the request exceeds the fixed scratch array (pa_decode_noalloc).
+static int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                        void* out, int64_t out_stride_b, int64_t out_stride_h, int io_dtype,
+                        const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+                        const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+                        const int32_t* seq_lens, const int32_t* cur_lens, const int32_t* order,
+                        int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                        float scale, int32_t split_blocks,
+                        void* workspace, size_t workspace_bytes, bool ws_limit_is_scratch,
+                        void* stream_) {
   PA_CHECK_ARG(batch >= 0 && num_heads > 0 && head_dim > 0 && block_size > 0,
                "bad sizes: batch=%d heads=%d head_dim=%d block_size=%d", batch, num_heads, head_dim,
                block_size);
@@ -511,6 +516,11 @@ extern "C" int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   const int nsplit = num_splits_for(max_pages, split_blocks);
   if (nsplit > 1) {
     const size_t need = pa_decode_workspace_size(batch, num_heads, head_dim, max_pages, split_blocks);
+    if (ws_limit_is_scratch && need > workspace_bytes)
+      PA_FAIL(PA_ERR_INVALID_ARGUMENT,
+              "pa_decode_noalloc: %d x %d heads x %d splits of head_dim %d need %zu bytes of split "
+              "records, above the fixed scratch of %zu bytes (use pa_decode with a workspace, or a "
+              "larger split_blocks)", batch, num_heads, nsplit, head_dim, need, workspace_bytes);
     if (workspace == nullptr || workspace_bytes < need)
       PA_FAIL(PA_ERR_WORKSPACE, "decode workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
     a.num_splits = nsplit;
@@ -533,4 +543,77 @@ extern "C" int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
     PA_CHECK_LAUNCH("decode merge kernel");
   }
   return PA_OK;
+}
+
+extern "C" int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                         void* out, int64_t out_stride_b, int64_t out_stride_h, int io_dtype,
+                         const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+                         const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+                         const int32_t* seq_lens, const int32_t* cur_lens, const int32_t* order,
+                         int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                         float scale, int32_t split_blocks,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  pa_host::clear_error();
+  return decode_entry(q, q_stride_b, q_stride_h, out, out_stride_b, out_stride_h, io_dtype, k_pool, v_pool,
+                      kv_dtype, num_blocks, page_table, pt_stride, max_pages, seq_lens, cur_lens, order, batch,
+                      num_heads, head_dim, block_size, scale, split_blocks, workspace, workspace_bytes, false,
+                      stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free decode: the split-K records live in a fixed device array instead of a caller
+// workspace. Each device holds its own copy of `scratch` (in the library's code object, for the
+// life of the process); host code never passes the array's name to a kernel, only the device
+// address hipGetSymbolAddress returns for the current device, looked up once per device.
+// ---------------------------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = PA_DECODE_NOALLOC_SCRATCH_BYTES;  // 16 MiB per device
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {nullptr};
+
+// The current device's address of `scratch`, or nullptr (error set) when it cannot be resolved.
+float* scratch_for_current_device() {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    pa_host::set_error("pa_decode_noalloc: no usable current device (%s, device %d)", hipGetErrorString(ge), dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      pa_host::set_error("pa_decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                         hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                 void* out, int64_t out_stride_b, int64_t out_stride_h, int io_dtype,
+                                 const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+                                 const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+                                 const int32_t* seq_lens, const int32_t* cur_lens, const int32_t* order,
+                                 int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                                 float scale, int32_t split_blocks, void* stream) {
+  pa_host::clear_error();
+  // Only a split launch touches the scratch; resolve it (first call on a device) only then.
+  const bool fast = block_size == 16 && (head_dim == 64 || head_dim == 128);
+  float* ws = nullptr;
+  if (fast && batch > 0 && num_heads > 0 && head_dim > 0 && num_splits_for(max_pages, split_blocks) > 1) {
+    ws = scratch_for_current_device();
+    if (ws == nullptr) return PA_ERR_HIP;
+  }
+  return decode_entry(q, q_stride_b, q_stride_h, out, out_stride_b, out_stride_h, io_dtype, k_pool, v_pool,
+                      kv_dtype, num_blocks, page_table, pt_stride, max_pages, seq_lens, cur_lens, order, batch,
+                      num_heads, head_dim, block_size, scale, split_blocks, ws, kNoAllocScratchBytes, true,
+                      stream);
 }

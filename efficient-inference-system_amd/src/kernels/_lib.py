@@ -47,6 +47,16 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _size_t, _c_void_p],  # workspace, bytes, stream
     ),
     "pa_decode_workspace_size": (_size_t, [_i32, _i32, _i32, _i32, _i32]),
+    "pa_decode_noalloc": (
+        _int,
+        [_c_void_p, _i64, _i64,  # q, strides b, h
+         _c_void_p, _i64, _i64, _int,  # out, strides b, h, io dtype
+         _c_void_p, _c_void_p, _int, _i64,  # k pool, v pool, kv dtype, num_blocks
+         _c_void_p, _i64, _i32,  # page table, stride, max_pages
+         _c_void_p, _c_void_p, _c_void_p,  # seq_lens, cur_lens, order
+         _i32, _i32, _i32, _i32,  # batch, heads, head_dim, block_size
+         _f32, _i32, _c_void_p],  # scale, split_blocks, stream
+    ),
     "pa_prefill": (
         _int,
         [_c_void_p, _i64, _i64, _i64,

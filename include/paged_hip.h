@@ -88,6 +88,28 @@ int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                 int32_t max_pages, int32_t split_blocks);
 
+/* Size of the fixed per-device scratch array that pa_decode_noalloc keeps its split records in. */
+#define PA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/*
+ * pa_decode without a workspace argument and without any device allocation: the same kernels
+ * and results as pa_decode with the same arguments, but the split-K records (when split_blocks
+ * splits a request) go to a fixed device array of PA_DECODE_NOALLOC_SCRATCH_BYTES inside the
+ * library, one per device, resolved on the first call on that device. No counterpart in the
+ * reference: this is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). A call whose records
+ * (pa_decode_workspace_size) exceed the array fails with PA_ERR_INVALID_ARGUMENT before any
+ * launch. The records need no initialisation, but every call on a device shares that device's
+ * array: calls that overlap on one device (e.g. on two streams) race and must be serialised.
+ */
+int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                      void* out, int64_t out_stride_b, int64_t out_stride_h, int io_dtype,
+                      const void* k_pool, const void* v_pool, int kv_dtype, int64_t num_blocks,
+                      const int32_t* page_table, int64_t pt_stride, int32_t max_pages,
+                      const int32_t* seq_lens, const int32_t* cur_lens, const int32_t* order,
+                      int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                      float scale, int32_t split_blocks, void* stream);
+
 /*
  * Paged chunked-PREFILL attention (any query_len >= 1), causal over cached context plus the
  * in-chunk prefix. Replaces paged_attention_prefill_triton

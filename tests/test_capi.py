@@ -31,11 +31,16 @@ def lib():
 
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
-        "pa_decode", "pa_decode_workspace_size", "pa_embed_rows", "pa_kv_append", "pa_last_error_message",
+        "pa_decode", "pa_decode_noalloc", "pa_decode_workspace_size", "pa_embed_rows", "pa_kv_append", "pa_last_error_message",
         "pa_linear_rows",
         "pa_pack_metadata", "pa_prefill", "pa_prefill_workspace_size", "pa_qkv_append", "pa_version",
         "pa_zero_blocks",
     ])
+
+
+def test_noalloc_scratch_size_is_stated_in_the_header():
+    text = HEADER.read_text()
+    assert re.search(r"#define PA_DECODE_NOALLOC_SCRATCH_BYTES \(\(size_t\)16 << 20\)", text)
 
 
 def test_every_declared_symbol_is_exported(lib):
