@@ -105,6 +105,11 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _i64, _c_void_p, _i32,  # token table, vocab, position table, max_pos
          _i32, _c_void_p, _i64, _int, _c_void_p],  # d_model, out, out stride, dtype, stream
     ),
+    "pa_argmax_rows": (
+        _int,
+        [_c_void_p, _i64, _i32, _i32,  # logits, row stride, batch, rows per request
+         _c_void_p, _i32, _int, _c_void_p, _c_void_p],  # row index, vocab, dtype, tokens, stream
+    ),
     "pa_zero_blocks": (
         _int,
         [_c_void_p, _c_void_p, _int, _i64, _i32, _i32, _i32, _c_void_p, _i32, _c_void_p],

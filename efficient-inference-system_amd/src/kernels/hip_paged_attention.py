@@ -7,6 +7,7 @@ and add the device-side cache operations the reference does with per-request Pyt
   kv_append_hip      <- PagedKVCacheState.append slice copies   (src/cache/paged_kv.py:102-120)
   pack_metadata_hip  <- page_table_tensor / seq_lens_tensor      (src/cache/paged_kv.py:174-197)
   zero_blocks_hip    <- LayerBlockPool.release_block zero_()     (src/cache/paged_kv.py:80-85)
+  argmax_rows_hip    <- torch.argmax(logits[b, row]).item()      (src/serving/continuous_generate.py:145,238)
 
 All work is enqueued on torch's current stream; nothing here synchronises. Every tensor must live
 on a HIP device: there is no CPU path.
@@ -266,3 +267,30 @@ def zero_blocks_hip(k_pool: torch.Tensor, v_pool: torch.Tensor, block_ids: torch
         block_ids.data_ptr(), block_ids.numel(), _stream_ptr(k_pool.device),
     )
     _lib.check(status, "pa_zero_blocks")
+
+
+def argmax_rows_hip(logits: torch.Tensor, row_index: torch.Tensor | None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy tokens of a step: out[b] = argmax_v logits[b, row_index[b], v] (int64 [B]) for
+    logits [B, T, V] with unit stride along V and rows of one request adjacent (row_index int32
+    [B] on the device, negative values count from the end; None means row 0). torch.argmax's
+    rules: first index of the maximum, NaN above every number."""
+    _require_gpu("argmax_rows_hip", logits)
+    if logits.dim() != 3 or logits.stride(2) != 1 or logits.stride(0) != logits.shape[1] * logits.stride(1):
+        raise ValueError("argmax_rows_hip: logits must be [B, T, V] with unit stride along V and adjacent rows")
+    B, T, V = logits.shape
+    if row_index is not None:
+        _require_gpu("argmax_rows_hip", row_index)
+        _require_i32("row_index", row_index)
+        if row_index.numel() < B:
+            raise ValueError(f"row_index has {row_index.numel()} entries, expected {B}")
+    if out is None:
+        out = torch.empty((B,), dtype=torch.int64, device=logits.device)
+    elif out.dtype != torch.int64 or not out.is_contiguous() or out.numel() < B or not out.is_cuda:
+        raise ValueError("argmax_rows_hip: out must be a contiguous int64 device tensor of at least B entries")
+    status = _lib.load().pa_argmax_rows(
+        logits.data_ptr(), logits.stride(1), B, T,
+        row_index.data_ptr() if row_index is not None else None, V, _lib.dtype_code(logits.dtype),
+        out.data_ptr(), _stream_ptr(logits.device),
+    )
+    _lib.check(status, "pa_argmax_rows")
+    return out

@@ -1,13 +1,23 @@
-"""Causal self-attention over the paged KV cache (src/model/attention.py:9-78 of the reference).
+"""Self-attention of the decoder blocks, over the paged KV cache when caching.
 
-Cached branch: project q/k/v, split heads into [B, H, T, Hd] views, append the new keys/values to
-the paged cache, then attend with paged_attention() and merge heads (append before attend, as in
-the reference). The uncached branch is dense causal attention.
+Interface of the reference's CausalSelfAttention (src/model/attention.py:9-78): the same
+constructor, the four projections q_proj / k_proj / v_proj / out_proj and the dropout module (so
+state dicts load across the two), and forward(x, kv_cache, use_cache, current_lengths) returning
+(output, cache).
+
+Cached calls follow the paged contract: the step's keys and values enter the cache first
+(append_batch, which clamps each request's new-token count to [0, T]), and only then is the
+query attended over everything cached, through paged_attention() and the configured backend; a
+lone PagedKVCacheState is served as a one-request batch and handed back as the state itself.
+Uncached calls are dense causal attention over the call's own tokens.
+
+Head layout: [B, T, d_model] activations are viewed as [B, H, T, head_dim] without a copy
+(heads), which is the strided q layout the paged kernels take; attention outputs come back in that
+layout and merge_heads flattens them again for out_proj.
 """
-import math
-
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from src.cache.paged_kv import BatchedPagedKVCache, PagedKVCacheState
 from src.kernels.paged_attention import paged_attention
@@ -16,26 +26,40 @@ from src.kernels.paged_attention import paged_attention
 class CausalSelfAttention(nn.Module):
     def __init__(self, d_model: int, num_heads: int, dropout: float = 0.0, attention_backend: str = "hip_paged"):
         super().__init__()
-        assert d_model % num_heads == 0
+        if d_model % num_heads:
+            raise AssertionError(f"d_model {d_model} is not a multiple of num_heads {num_heads}")
         self.d_model = d_model
         self.num_heads = num_heads
         self.head_dim = d_model // num_heads
         self.attention_backend = attention_backend
-        self.q_proj = nn.Linear(d_model, d_model)
-        self.k_proj = nn.Linear(d_model, d_model)
-        self.v_proj = nn.Linear(d_model, d_model)
-        self.out_proj = nn.Linear(d_model, d_model)
+        for name in ("q_proj", "k_proj", "v_proj", "out_proj"):
+            setattr(self, name, nn.Linear(d_model, d_model))
         self.dropout = nn.Dropout(dropout)
 
-    def _split_heads(self, x: torch.Tensor) -> torch.Tensor:
-        # [B, T, D] -> [B, H, T, Hd] (a view: strides (T*D, Hd, D, 1))
-        bsz, seq_len, _ = x.shape
-        return x.view(bsz, seq_len, self.num_heads, self.head_dim).transpose(1, 2)
+    def heads(self, x: torch.Tensor) -> torch.Tensor:
+        """[B, T, d_model] -> [B, H, T, head_dim] view (strides T*d_model, head_dim, d_model, 1)."""
+        return x.unflatten(-1, (self.num_heads, self.head_dim)).transpose(1, 2)
 
-    def _merge_heads(self, x: torch.Tensor) -> torch.Tensor:
-        # [B, H, T, Hd] -> [B, T, D]
-        bsz, _, seq_len, _ = x.shape
-        return x.transpose(1, 2).contiguous().view(bsz, seq_len, self.d_model)
+    def merge_heads(self, x: torch.Tensor) -> torch.Tensor:
+        """[B, H, T, head_dim] -> contiguous [B, T, d_model]."""
+        return x.transpose(1, 2).flatten(2).contiguous()
+
+    def _paged(self, q, k, v, kv_cache, current_lengths):
+        if isinstance(kv_cache, PagedKVCacheState):
+            batch, single = BatchedPagedKVCache(states=[kv_cache], pool=kv_cache.pool), True
+        elif isinstance(kv_cache, BatchedPagedKVCache):
+            batch, single = kv_cache, len(kv_cache.states) == 1
+        else:
+            raise ValueError("Paged cached attention requires initialized paged cache state.")
+        batch.append_batch(k, v, current_lengths=current_lengths)
+        attended = paged_attention(backend=self.attention_backend, q=q, kv_cache=batch,
+                                   current_lengths=current_lengths)
+        return attended, (batch.states[0] if single else batch)
+
+    def _dense_causal(self, q, k, v):
+        # fp32 scores and softmax, one causal mask over the call's own T tokens
+        p = self.dropout.p if self.training else 0.0
+        return F.scaled_dot_product_attention(q, k, v, dropout_p=p, is_causal=True)
 
     def forward(
         self,
@@ -44,31 +68,9 @@ class CausalSelfAttention(nn.Module):
         use_cache: bool = False,
         current_lengths: int | torch.Tensor | None = None,
     ) -> tuple[torch.Tensor, PagedKVCacheState | BatchedPagedKVCache | None]:
-        _, seq_len, _ = x.shape
-        q = self._split_heads(self.q_proj(x))
-        k_new = self._split_heads(self.k_proj(x))
-        v_new = self._split_heads(self.v_proj(x))
-
+        q, k, v = (self.heads(proj(x)) for proj in (self.q_proj, self.k_proj, self.v_proj))
         if use_cache:
-            if isinstance(kv_cache, PagedKVCacheState):
-                kv_cache = BatchedPagedKVCache(states=[kv_cache], pool=kv_cache.pool)
-            elif kv_cache is None:
-                raise ValueError("Paged cached attention requires initialized paged cache state.")
-            kv_cache.append_batch(k_new, v_new, current_lengths=current_lengths)
-            out = paged_attention(
-                backend=self.attention_backend,
-                q=q,
-                kv_cache=kv_cache,
-                current_lengths=current_lengths,
-            )
-            out = self.out_proj(self._merge_heads(out))
-            if len(kv_cache.states) == 1:
-                return out, kv_cache.states[0]
-            return out, kv_cache
-
-        scores = torch.matmul(q, k_new.transpose(-2, -1).contiguous()) / math.sqrt(self.head_dim)
-        causal_mask = torch.tril(torch.ones(seq_len, seq_len, device=x.device, dtype=torch.bool))
-        scores = scores.masked_fill(~causal_mask.view(1, 1, seq_len, seq_len), float("-inf"))
-        attn = self.dropout(torch.softmax(scores, dim=-1))
-        out = torch.matmul(attn, v_new)
-        return self.out_proj(self._merge_heads(out)), None
+            attended, cache = self._paged(q, k, v, kv_cache, current_lengths)
+        else:
+            attended, cache = self._dense_causal(q, k, v), None
+        return self.out_proj(self.merge_heads(attended)), cache

@@ -44,7 +44,7 @@ import torch
 from src.cache.paged_kv import BatchedPagedKVCache
 from src.kernels import _lib, hip_linear
 from src.kernels.hip_paged_attention import (
-    _workspace, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
+    _workspace, argmax_rows_hip, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
     pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
 from src.kernels.staging import upload_into
 
@@ -146,9 +146,17 @@ class _Captured:
     def __init__(self, model, B: int, Tb: int, pages: int, device: torch.device, pools):
         H, Hd = model.num_heads, model.head_dim
         self.B, self.Tb, self.pages = B, Tb, pages
-        self.ids = torch.zeros((B, Tb), dtype=torch.long, device=device)
-        self.pos = torch.zeros((B,), dtype=torch.long, device=device)
-        self.cur = torch.ones((B,), dtype=torch.int32, device=device)
+        # [token ids padded to Tb | first positions], int64, one buffer so host data is one upload
+        self.io = torch.zeros((B * Tb + B,), dtype=torch.long, device=device)
+        self.ids = self.io[:B * Tb].view(B, Tb)
+        self.pos = self.io[B * Tb:]
+        # [current lengths | greedy rows]: the attention's cur_lens and, per request, the logits row
+        # whose argmax the step writes into self.tokens
+        self.sel = torch.zeros((2 * B,), dtype=torch.int32, device=device)
+        self.sel_host: tuple | None = None
+        self.cur = self.sel[:B]
+        self.rows = self.sel[B:]
+        self.tokens = torch.zeros((B,), dtype=torch.int64, device=device)
         self.csr = torch.zeros((3 * B + 1 + B * pages,), dtype=torch.int32, device=device)
         lib = _lib.load()
         if Tb == 1:
@@ -177,11 +185,14 @@ class GraphedStep:
         self.captures = 0
         self._attns = None
 
-    def usable(self, input_ids: torch.Tensor, kv_caches) -> bool:
+    def usable(self, input_ids, kv_caches) -> bool:
+        """Whether a step over input_ids ([B, T], device tensor or host data) and these per-layer
+        caches can replay a graph: a HIP model in eval mode on the hip_paged backend, batched
+        caches of every layer in lockstep, and T within the largest bucket."""
         m = self.model
         if self._attns is None or len(self._attns) != len(m.blocks):
             self._attns = [b.attn for b in m.blocks]  # plain attribute reads below, per call
-        if not (graphs_enabled() and input_ids.is_cuda and input_ids.dim() == 2 and not m.training
+        if not (graphs_enabled() and m.token_emb.weight.is_cuda and len(input_ids.shape) == 2 and not m.training
                 and m.attention_backend == "hip_paged"
                 and all(a.attention_backend == "hip_paged" for a in self._attns)
                 and isinstance(kv_caches, list) and len(kv_caches) == len(self._attns)
@@ -209,21 +220,29 @@ class GraphedStep:
             positions = torch.clamp(cap.pos.view(B, 1) + steps, max=m.max_seq_len - 1)
             x = m.token_emb(cap.ids) + m.pos_emb(positions)
         if cap.fused:
-            return self._fused_layers(cap, pools, x.view(B * Tb, -1), pt, seq32, slots)
+            logits = self._fused_layers(cap, pools, x.view(B * Tb, -1), pt, seq32, slots)
+        else:
+            logits = self._torch_layers(cap, pools, x, pt, seq32, slots)
+        argmax_rows_hip(logits, cap.rows, out=cap.tokens)
+        return logits
+
+    def _torch_layers(self, cap: _Captured, pools, x, pt, seq32, slots) -> torch.Tensor:
+        m = self.model
+        Tb = cap.Tb
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
             h = blk.ln1(x)
-            q = a._split_heads(a.q_proj(h))
-            k_new = a._split_heads(a.k_proj(h))
-            v_new = a._split_heads(a.v_proj(h))
+            q = a.heads(a.q_proj(h))
+            k_new = a.heads(a.k_proj(h))
+            v_new = a.heads(a.v_proj(h))
             kv_append_hip(k_new, v_new, k_pool, v_pool, slots)
             if Tb == 1:
                 o = paged_attention_decode_hip(q, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
             else:
                 o = paged_attention_prefill_hip(q, k_pool, v_pool, pt, seq32, cap.cur,
                                                 split_blocks=cap.split_blocks)
-            x = x + a.out_proj(a._merge_heads(o))
+            x = x + a.out_proj(a.merge_heads(o))
             x = x + blk.mlp(blk.ln2(x))
         return m.lm_head(m.ln_f(x))
 
@@ -277,13 +296,23 @@ class GraphedStep:
         self.captures += 1
 
     # ------------------------------------------------------------------------------------------
-    def __call__(self, input_ids: torch.Tensor, positions, current_lengths: list[int], kv_caches):
-        """One cached step. positions: int or [B] tensor of each request's first position;
-        current_lengths: host list (the reference's current_lengths, before clamping)."""
+    def __call__(self, input_ids, positions, current_lengths: list[int], kv_caches, rows: list[int] | None = None,
+                 want_logits: bool = True):
+        """One cached step, replayed from a captured graph that ends in a greedy argmax.
+
+        input_ids: [B, T] token ids, a device tensor or host data (tensor or numpy array);
+        positions: int, or each request's first position (device tensor or host data);
+        current_lengths: host list (the reference's current_lengths, before clamping);
+        rows: per request, the logits row whose argmax becomes its token (None keeps the last
+        rows uploaded: the tokens are then not meaningful).
+        Returns (logits [B, T, vocab] or None when want_logits is False, tokens): tokens is an
+        int64 [B] device tensor owned by the graph, overwritten by the next step of this batch
+        size and bucket. The caller checks ids and positions first (the model's
+        check_token_inputs), before any cache state changes."""
         m = self.model
         B, T = input_ids.shape
         Tb = bucket_for(T)
-        device = input_ids.device
+        device = m.token_emb.weight.device
         pools = [c.pool for c in kv_caches]
         app = [max(min(c, T), 0) for c in current_lengths]
         if _host is not None:
@@ -306,24 +335,35 @@ class GraphedStep:
             cap = _Captured(m, B, Tb, pages, device, pools)
             self.captured[key] = cap
         upload_into(buf, cap.csr)
-        if (Tb == T and not isinstance(positions, int) and positions.dtype == cap.pos.dtype
-                and input_ids.dtype == cap.ids.dtype and positions.device == device):
-            torch._foreach_copy_([cap.ids, cap.pos], [input_ids, positions.view(B)])  # one launch
+        if isinstance(input_ids, torch.Tensor) and input_ids.is_cuda:
+            if (Tb == T and isinstance(positions, torch.Tensor) and positions.is_cuda
+                    and positions.dtype == cap.pos.dtype and input_ids.dtype == cap.ids.dtype):
+                torch._foreach_copy_([cap.ids, cap.pos], [input_ids, positions.view(B)])  # one launch
+            else:
+                if Tb == T:
+                    cap.ids.copy_(input_ids)
+                else:
+                    cap.ids.zero_()
+                    cap.ids[:, :T].copy_(input_ids)
+                if isinstance(positions, int):
+                    cap.pos.fill_(positions)
+                else:
+                    cap.pos.copy_(torch.as_tensor(positions).view(B))
         else:
-            if Tb == T:
-                cap.ids.copy_(input_ids)
-            else:
-                cap.ids.zero_()
-                cap.ids[:, :T].copy_(input_ids)
-            if isinstance(positions, int):
-                cap.pos.fill_(positions)
-            else:
-                cap.pos.copy_(positions.view(B))
-        ones = all(c == 1 for c in current_lengths)
-        if not (ones and getattr(cap, "cur_ones", True)):
-            upload_into(np.asarray(current_lengths, dtype=np.int32), cap.cur)
-            cap.cur_ones = ones
+            # host token ids: one upload of [ids padded to the bucket | first positions]
+            io = np.zeros((B * Tb + B,), dtype=np.int64)
+            ids = input_ids.cpu().numpy() if isinstance(input_ids, torch.Tensor) else np.asarray(input_ids)
+            io[:B * Tb].reshape(B, Tb)[:, :T] = ids
+            if isinstance(positions, torch.Tensor):
+                positions = positions.cpu().numpy()
+            io[B * Tb:] = positions
+            upload_into(io, cap.io)
+        sel = tuple(current_lengths) + (tuple(rows) if rows is not None
+                                        else (cap.sel_host[B:] if cap.sel_host is not None else (0,) * B))
+        if sel != cap.sel_host:
+            upload_into(np.asarray(sel, dtype=np.int32), cap.sel)
+            cap.sel_host = sel
         if cap.graph is None:
             self._capture(cap, pools)
         cap.graph.replay()
-        return cap.logits[:, :T].clone()
+        return (cap.logits[:, :T].clone() if want_logits else None), cap.tokens

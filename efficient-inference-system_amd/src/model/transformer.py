@@ -7,6 +7,7 @@ names match the reference so state dicts load across the two. On the "hip_paged"
 steps over per-layer batched caches (decode steps and prefill chunks up to 256 tokens) replay
 captured HIP graphs (src/model/graph_decode.py); everything else runs eagerly.
 """
+import numpy as np
 import torch
 import torch.nn as nn
 
@@ -177,6 +178,89 @@ class TinyTransformerLM(nn.Module):
             "free_kv_pool_bytes": max(reserved - allocated, 0),
         }
 
+    def check_token_inputs(self, input_ids, positions, T: int) -> None:
+        """Raise IndexError where the embedding lookups of an eager forward would: a token id
+        outside [0, vocab_size) or a row position (first position + t, t < T) outside
+        [0, max_seq_len). Used before GPU steps, where the graph path clamps instead and an eager
+        lookup would fault the device rather than raise. Host data is checked on the host;
+        device tensors cost one device->host read."""
+        V, P = self.vocab_size, self.max_seq_len
+
+        def on_device(x):
+            return isinstance(x, torch.Tensor) and x.is_cuda
+
+        parts = []
+        if on_device(input_ids):
+            parts += [input_ids.min(), input_ids.max()]
+        if on_device(positions):
+            parts += [positions.min(), positions.max()]
+        vals = torch.stack([t.to(torch.int64) for t in parts]).tolist() if parts else []
+        if on_device(input_ids):
+            lo_id, hi_id = vals[0], vals[1]
+            vals = vals[2:]
+        else:
+            ids = np.asarray(input_ids.cpu() if isinstance(input_ids, torch.Tensor) else input_ids)
+            lo_id, hi_id = (int(ids.min()), int(ids.max())) if ids.size else (0, 0)
+        if isinstance(positions, int):
+            lo_pos = hi_pos = positions
+        elif on_device(positions):
+            lo_pos, hi_pos = vals[0], vals[1]
+        else:
+            p = np.asarray(positions.cpu() if isinstance(positions, torch.Tensor) else positions, dtype=np.int64)
+            lo_pos, hi_pos = (int(p.min()), int(p.max())) if p.size else (0, 0)
+        if lo_id < 0 or hi_id >= V:
+            raise IndexError(f"token id out of range [0, {V}): min {lo_id}, max {hi_id}")
+        if T > 0 and (lo_pos < 0 or hi_pos + T - 1 >= P):
+            raise IndexError(f"positions {lo_pos}..{hi_pos + T - 1} outside the position table [0, {P})")
+
+    @staticmethod
+    def _host_lengths(current_lengths, B: int, T: int) -> list[int]:
+        if current_lengths is None:
+            return [T] * B
+        if isinstance(current_lengths, int):
+            return [current_lengths] * B
+        if isinstance(current_lengths, torch.Tensor):
+            return [int(x) for x in current_lengths.reshape(-1).tolist()]
+        return [int(x) for x in current_lengths]
+
+    @torch.no_grad()
+    def greedy_step(self, input_ids, kv_caches, position_offset=0, current_lengths=None, select_rows=None,
+                    return_logits: bool = False):
+        """One cached step that also picks every request's next token greedily.
+
+        input_ids: [B, T] token ids, host data (tensor or numpy array) or a device tensor;
+        position_offset: int, or each request's first position (host data or tensor);
+        current_lengths: as forward() (None, int, tensor) or a host list;
+        select_rows: per request, the logits row whose argmax is its next token (default: its last
+        real row, current_lengths - 1; negative rows count from the end as torch indexing does).
+        Returns (tokens, logits, caches): tokens int64 [B] on the model's device (on the graph
+        path a buffer the next step of the same shape overwrites: read it before that), logits
+        [B, T, vocab] when return_logits else None, and the per-layer caches as forward() returns
+        them. On the hip_paged backend with batched caches the step replays a captured graph
+        whose last kernel is the argmax, so only the token ids need to leave the device."""
+        B, T = input_ids.shape
+        cur = self._host_lengths(current_lengths, B, T)
+        rows = list(select_rows) if select_rows is not None else [c - 1 for c in cur]
+        if len(rows) != B or any(not -T <= r < T for r in rows):
+            raise IndexError(f"select_rows {rows} out of range for {B} requests of {T} rows")
+        rows = [r % T for r in rows]
+        device = self.token_emb.weight.device
+        if device.type == "cuda":
+            self.check_token_inputs(input_ids, position_offset, T)
+        if kv_caches is not None and device.type == "cuda":
+            runner = self._graph_runner()
+            if runner.usable(input_ids, kv_caches):
+                logits, tokens = runner(input_ids, position_offset, cur, kv_caches, rows=rows,
+                                        want_logits=return_logits)
+                return tokens, logits, list(kv_caches)
+        ids = torch.as_tensor(input_ids, dtype=torch.long).to(device)
+        pos = position_offset if isinstance(position_offset, int) else \
+            torch.as_tensor(position_offset, dtype=torch.long).to(device)
+        logits, caches = self(ids, kv_caches=kv_caches, use_cache=True, position_offset=pos,
+                              current_lengths=torch.tensor(cur, dtype=torch.long))
+        picked = logits[torch.arange(B, device=device), torch.tensor(rows, device=device)]
+        return torch.argmax(picked, dim=-1), (logits if return_logits else None), caches
+
     def forward(
         self,
         input_ids: torch.Tensor,
@@ -187,16 +271,14 @@ class TinyTransformerLM(nn.Module):
     ):
         B, T = input_ids.shape
         device = input_ids.device
+        if input_ids.is_cuda:
+            self.check_token_inputs(input_ids, position_offset, T)
         if use_cache and kv_caches is not None and input_ids.is_cuda:
             runner = self._graph_runner()
             if runner.usable(input_ids, kv_caches):
-                if current_lengths is None:
-                    cur = [T] * B
-                elif isinstance(current_lengths, int):
-                    cur = [current_lengths] * B
-                else:
-                    cur = [int(x) for x in current_lengths.reshape(-1).tolist()]
-                return runner(input_ids, position_offset, cur, kv_caches), list(kv_caches)
+                cur = self._host_lengths(current_lengths, B, T)
+                logits, _ = runner(input_ids, position_offset, cur, kv_caches)
+                return logits, list(kv_caches)
         if isinstance(position_offset, int):
             positions = torch.arange(position_offset, position_offset + T, device=device).unsqueeze(0).expand(B, T)
         else:

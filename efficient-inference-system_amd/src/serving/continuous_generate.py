@@ -1,218 +1,221 @@
-"""Continuous-batching executors (src/serving/continuous_generate.py:82-276 of the reference).
+"""Continuous-batching executors: run one scheduler iteration's prefill chunk or decode step on a
+paged-KV model and pick each request's next token greedily.
 
-run_prefill_chunk: one forward over a group of requests with equal prompt progress, each taking
-min(chunk_size, remaining prompt) tokens (right-padded with id 0; current_lengths carries the real
-lengths); requests whose prompt completes emit their first token from the logits at their last
-real position. run_decode_step: one forward of one token per request at position
-prompt_len + generated - 1. The timed region is the model forward only, as in the reference; its
-elapsed time is the batch runtime that advances the scheduler's virtual clock.
+The two entry points keep the reference's names, positional arguments and event keys
+(src/serving/continuous_generate.py:82-276), since ContinuousBatchingScheduler and the benchmark
+harness call them that way and read those keys:
+
+    run_prefill_chunk(model, requests, chunk_size, device, start_time_ms, event_id) -> event
+    run_decode_step(model, requests, device, start_time_ms, event_id) -> event
+
+Each call goes through three stages of a StepExecutor:
+
+  plan     (host)  the step's token ids as a host array padded with id 0 to the group's longest
+                   chunk, each request's first position, its real token count (current_lengths)
+                   and the logits row its next token is read from (its last real row);
+  execute  (timed) one model.greedy_step(): on the hip_paged backend a captured HIP graph whose
+                   last kernel is the argmax, so no [B, T, vocab] logits leave the device; only
+                   the B token ids are read back, after the timed region;
+  commit   (host)  tokens appended, phase transitions (prefill -> decode -> finished), first-token
+                   and finish times on the scheduler's virtual clock, and the event record.
+
+As in the reference, the batch runtime that advances the virtual clock is the timed model step,
+which here includes the on-device argmax (part of the captured step). A StepExecutor can also
+keep each step's logits and report every step to an observer, which is what the end-to-end
+parity test uses to replay the same steps on another backend.
 """
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
 import torch
-from torch.nn.utils.rnn import pad_sequence
 
 from src.cache.paged_kv import BatchedPagedKVCache, PagedKVCacheState
 from src.utils.timing import timed_section
 
 
-def _cache_bytes_per_token(model) -> int:
-    param = next(model.parameters())
-    return len(model.blocks) * 2 * model.blocks[0].attn.d_model * param.element_size()
+@dataclass
+class StepPlan:
+    """Host-side description of one model step over a group of requests."""
+    phase: str                    # "prefill" or "decode"
+    requests: list
+    token_ids: np.ndarray         # int64 [B, T], right-padded with id 0
+    positions: int | list[int]    # first position: shared (prefill) or per request (decode)
+    lengths: list[int]            # real tokens per request (the model's current_lengths)
+    rows: list[int]               # logits row of each request's next token
+
+    @property
+    def padded_len(self) -> int:
+        return int(self.token_ids.shape[1])
 
 
-def _stack_layer_caches(requests: list):
-    """Per-layer BatchedPagedKVCache over the requests' per-layer states."""
-    if not requests or requests[0].kv_caches is None:
-        return None
-    batched = []
-    for layer_idx in range(len(requests[0].kv_caches)):
-        layer_caches = [req.kv_caches[layer_idx] for req in requests]
-        sample = next((c for c in layer_caches if c is not None), None)
-        if sample is None:
-            raise ValueError("Paged request caches must be initialized before batching.")
-        states = [c if isinstance(c, PagedKVCacheState) else PagedKVCacheState(pool=sample.pool) for c in layer_caches]
-        batched.append(BatchedPagedKVCache(states=states, pool=sample.pool))
-    return batched
-
-
-def _scatter_layer_caches(requests: list, batched_caches) -> None:
-    if batched_caches is None:
-        return
-    for request_idx, req in enumerate(requests):
-        req.kv_caches = []
-        for cache in batched_caches:
-            if cache is None:
-                req.kv_caches.append(None)
-            elif isinstance(cache, BatchedPagedKVCache):
-                req.kv_caches.append(cache.states[request_idx])
-            else:
-                req.kv_caches.append(cache)
-
-
-def _ensure_request_kv_caches(model, requests: list) -> None:
-    missing = [idx for idx, req in enumerate(requests) if req.kv_caches is None]
-    if not missing:
-        return
-    created = model.create_request_kv_caches(len(missing))
-    for local_idx, request_idx in enumerate(missing):
-        requests[request_idx].kv_caches = created[local_idx]
-
-
-def _cache_totals(model, requests: list) -> tuple[int, int, int]:
-    live = sum(
-        c.live_bytes() for req in requests if req.kv_caches is not None for c in req.kv_caches if isinstance(c, PagedKVCacheState)
-    )
-    pool_stats = model.paged_memory_stats() if hasattr(model, "paged_memory_stats") else {}
-    reserved = pool_stats.get("reserved_kv_bytes", live)
-    return live, reserved, max(reserved - live, 0)
-
-
-def _gpu_bytes(device: str) -> tuple[int, int]:
-    if str(device).startswith("cuda") and torch.cuda.is_available():
-        return int(torch.cuda.memory_allocated()), int(torch.cuda.max_memory_allocated())
-    return 0, 0
-
-
-@torch.no_grad()
-def run_prefill_chunk(model, requests: list, chunk_size: int, device: str, start_time_ms: float, event_id: int) -> dict:
-    if not requests:
-        return {"batch_runtime_ms": 0.0, "requests_completed": []}
-    chunk_start = requests[0].prompt_tokens_processed
-    if any(req.prompt_tokens_processed != chunk_start for req in requests):
+def plan_prefill(requests: list, chunk_size: int) -> StepPlan | None:
+    """The next chunk of a group with equal prompt progress: up to chunk_size prompt tokens per
+    request. None when no request has prompt tokens left."""
+    start = requests[0].prompt_tokens_processed
+    if any(r.prompt_tokens_processed != start for r in requests):
         raise ValueError("run_prefill_chunk expects requests with the same prompt progress.")
-    chunk_lengths = [max(min(chunk_size, req.prompt_len - chunk_start), 0) for req in requests]
-    max_chunk_len = max(chunk_lengths)
-    if max_chunk_len <= 0:
-        return {"batch_runtime_ms": 0.0, "requests_completed": []}
+    lengths = [max(min(chunk_size, r.prompt_len - start), 0) for r in requests]
+    width = max(lengths)
+    if width <= 0:
+        return None
+    ids = np.zeros((len(requests), width), dtype=np.int64)
+    for row, (r, n) in zip(ids, zip(requests, lengths)):
+        row[:n] = r.prompt_ids[start:start + n].cpu().numpy()
+    return StepPlan("prefill", requests, ids, start, lengths, [n - 1 for n in lengths])
 
-    prompt_batch = pad_sequence(
-        [req.prompt_ids[chunk_start:chunk_start + n].to(device) for req, n in zip(requests, chunk_lengths)],
-        batch_first=True,
-        padding_value=0,
-    )
-    current_lengths = torch.tensor(chunk_lengths, dtype=torch.long)
-    _ensure_request_kv_caches(model, requests)
-    batched_caches = _stack_layer_caches(requests)
 
-    with timed_section(device=device) as timer:
-        logits, new_caches = model(
-            prompt_batch,
-            kv_caches=batched_caches,
-            use_cache=True,
-            position_offset=chunk_start,
-            current_lengths=current_lengths,
-        )
+def plan_decode(requests: list) -> StepPlan:
+    """One token per request: its last generated token at position prompt_len + generated - 1."""
+    ids = np.asarray([[r.generated_token_ids[-1]] for r in requests], dtype=np.int64)
+    positions = [r.prompt_len + r.num_generated_tokens - 1 for r in requests]
+    return StepPlan("decode", requests, ids, positions, [1] * len(requests), [0] * len(requests))
 
-    finish_time_ms = start_time_ms + timer.elapsed_ms
-    last_idx = torch.tensor([n - 1 for n in chunk_lengths], device=logits.device)
-    next_tokens = torch.argmax(logits[torch.arange(len(requests), device=logits.device), last_idx, :], dim=-1).tolist()
-    completed_requests = []
-    first_tokens_emitted = 0
-    for req_idx, req in enumerate(requests):
-        if req.start_time_ms is None:
-            req.start_time_ms = start_time_ms
-            req.batch_id = event_id
-        req.scheduler_mode = "continuous"
-        req.prompt_tokens_processed = chunk_start + chunk_lengths[req_idx]
-        if req.prompt_tokens_processed >= req.prompt_len:
-            req.generated_token_ids.append(int(next_tokens[req_idx]))
-            first_tokens_emitted += 1
-            if req.first_token_time_ms is None:
-                req.first_token_time_ms = finish_time_ms
-            if req.num_generated_tokens >= req.max_new_tokens:
-                req.phase = "finished"
-                req.finish_time_ms = finish_time_ms
-                completed_requests.append(req)
+
+def _layer_batches(model, requests: list) -> list[BatchedPagedKVCache]:
+    """Per-layer batched caches over the requests' per-layer states, creating the states of
+    requests that have none yet (a request's states persist across its steps)."""
+    fresh = [r for r in requests if r.kv_caches is None]
+    for r, caches in zip(fresh, model.create_request_kv_caches(len(fresh)) if fresh else []):
+        r.kv_caches = caches
+    batches = []
+    for layer in zip(*(r.kv_caches for r in requests)):
+        pool = next((c.pool for c in layer if c is not None), None)
+        if pool is None:
+            raise ValueError("Paged request caches must be initialized before batching.")
+        states = [c if isinstance(c, PagedKVCacheState) else PagedKVCacheState(pool=pool) for c in layer]
+        batches.append(BatchedPagedKVCache(states=states, pool=pool))
+    return batches
+
+
+def _adopt(requests: list, layer_caches) -> None:
+    """Point each request at its per-layer state in the caches the model step returned."""
+    if layer_caches is None:
+        return
+    for i, r in enumerate(requests):
+        r.kv_caches = [c.states[i] if isinstance(c, BatchedPagedKVCache) else c for c in layer_caches]
+
+
+def _kv_accounting(model, requests: list) -> dict:
+    live = sum(c.live_bytes() for r in requests for c in (r.kv_caches or ()) if isinstance(c, PagedKVCacheState))
+    reserved = model.paged_memory_stats().get("reserved_kv_bytes", live) if hasattr(model, "paged_memory_stats") \
+        else live
+    return {"live_kv_bytes": live, "reserved_kv_bytes": reserved, "fragmentation_bytes": max(reserved - live, 0)}
+
+
+def _device_memory(device) -> dict:
+    on_gpu = str(device).startswith("cuda") and torch.cuda.is_available()
+    return {"gpu_allocated_bytes": int(torch.cuda.memory_allocated()) if on_gpu else 0,
+            "gpu_peak_allocated_bytes": int(torch.cuda.max_memory_allocated()) if on_gpu else 0}
+
+
+def _kv_bytes_per_token(model) -> int:
+    """KV bytes one token occupies over all layers (K and V rows of d_model elements)."""
+    elem = next(model.parameters()).element_size()
+    return 2 * len(model.blocks) * model.blocks[0].attn.d_model * elem
+
+
+class StepExecutor:
+    """Runs planned steps on `model`. keep_logits: also return each step's logits (for tests;
+    on the graph path this copies them out of the graph); observer(plan, tokens, logits, event):
+    called after every step."""
+
+    def __init__(self, model, device, keep_logits: bool = False, observer=None):
+        self.model = model
+        self.device = device
+        self.keep_logits = keep_logits
+        self.observer = observer
+
+    def _execute(self, plan: StepPlan) -> tuple[list[int], torch.Tensor | None, float]:
+        caches = _layer_batches(self.model, plan.requests)
+        with timed_section(device=self.device) as timer:
+            tokens, logits, caches = self.model.greedy_step(
+                plan.token_ids, caches, position_offset=plan.positions, current_lengths=plan.lengths,
+                select_rows=plan.rows, return_logits=self.keep_logits)
+        tokens = [int(t) for t in tokens.tolist()]  # the step's only device->host read
+        _adopt(plan.requests, caches)
+        return tokens, logits, timer.elapsed_ms
+
+    def run(self, plan: StepPlan, start_time_ms: float, event_id: int) -> dict:
+        tokens, logits, runtime = self._execute(plan)
+        finish = start_time_ms + runtime
+        completed, emitted = [], 0
+        for r, tok, n in zip(plan.requests, tokens, plan.lengths):
+            if r.start_time_ms is None:
+                r.start_time_ms, r.batch_id = start_time_ms, event_id
+            r.scheduler_mode = "continuous"
+            if plan.phase == "prefill":
+                r.prompt_tokens_processed += n
+                if r.prompt_tokens_processed < r.prompt_len:
+                    r.phase = "prefill"
+                    continue
+                if r.first_token_time_ms is None:
+                    r.first_token_time_ms = finish
+            r.generated_token_ids.append(tok)
+            emitted += 1
+            if r.num_generated_tokens >= r.max_new_tokens:
+                r.phase, r.finish_time_ms = "finished", finish
+                completed.append(r)
             else:
-                req.phase = "decode"
-        else:
-            req.phase = "prefill"
+                r.phase = "decode"
+        event = self._event(plan, runtime, completed, emitted)
+        if self.observer is not None:
+            self.observer(plan, tokens, logits, event)
+        return event
 
-    _scatter_layer_caches(requests, new_caches)
-    live_kv_bytes, reserved_kv_bytes, fragmentation_bytes = _cache_totals(model, requests)
-    gpu_allocated_bytes, gpu_peak_allocated_bytes = _gpu_bytes(device)
-    padding_waste_tokens = len(requests) * max_chunk_len - sum(chunk_lengths)
-    return {
-        "batch_runtime_ms": timer.elapsed_ms,
-        "requests_completed": completed_requests,
-        "batch_size": len(requests),
-        "tokens_scheduled": sum(chunk_lengths),
-        "phase": "prefill",
-        "prompt_len": max(req.prompt_len for req in requests),
-        "max_new_tokens": max(req.max_new_tokens for req in requests),
-        "prefill_tokens": sum(chunk_lengths),
-        "decode_tokens": first_tokens_emitted,
-        "decode_kernel_tokens": 0,
-        "prefill_runtime_ms": timer.elapsed_ms,
-        "decode_runtime_ms": 0.0,
-        "decode_ms_per_token": 0.0,
-        "live_kv_bytes": live_kv_bytes,
-        "reserved_kv_bytes": reserved_kv_bytes,
-        "fragmentation_bytes": fragmentation_bytes,
-        "workspace_bytes": 0,
-        "gpu_allocated_bytes": gpu_allocated_bytes,
-        "gpu_peak_allocated_bytes": gpu_peak_allocated_bytes,
-        "backend_name": getattr(model, "attention_backend", "hip_paged"),
-        "padding_waste_tokens": padding_waste_tokens,
-        "padding_waste_bytes_est": padding_waste_tokens * _cache_bytes_per_token(model),
-        "padding_waste_pct": 100.0 * padding_waste_tokens / (len(requests) * max_chunk_len) if max_chunk_len > 0 else 0.0,
-    }
+    def _event(self, plan: StepPlan, runtime: float, completed: list, emitted: int) -> dict:
+        reqs = plan.requests
+        n = len(reqs)
+        real = sum(plan.lengths)
+        prefill = plan.phase == "prefill"
+        waste = n * plan.padded_len - real if prefill else 0
+        event = {
+            "batch_runtime_ms": runtime,
+            "requests_completed": completed,
+            "batch_size": n,
+            "tokens_scheduled": real,
+            "phase": plan.phase,
+            "prompt_len": max(r.prompt_len for r in reqs),
+            "max_new_tokens": max(r.max_new_tokens for r in reqs),
+            "prefill_tokens": real if prefill else 0,
+            "decode_tokens": emitted,
+            "decode_kernel_tokens": 0 if prefill else n,
+            "prefill_runtime_ms": runtime if prefill else 0.0,
+            "decode_runtime_ms": 0.0 if prefill else runtime,
+            "decode_ms_per_token": 0.0 if prefill else runtime / max(n, 1),
+            # split-K workspaces of captured steps are allocated at capture, none per step
+            "workspace_bytes": 0,
+            "backend_name": getattr(self.model, "attention_backend", "hip_paged"),
+            "padding_waste_tokens": waste,
+            "padding_waste_bytes_est": waste * _kv_bytes_per_token(self.model),
+            "padding_waste_pct": 100.0 * waste / (n * plan.padded_len) if prefill else 0.0,
+        }
+        event.update(_kv_accounting(self.model, reqs))
+        event.update(_device_memory(self.device))
+        return event
+
+
+_IDLE = {"batch_runtime_ms": 0.0, "requests_completed": []}
 
 
 @torch.no_grad()
-def run_decode_step(model, requests: list, device: str, start_time_ms: float, event_id: int) -> dict:
+def run_prefill_chunk(model, requests: list, chunk_size: int, device: str, start_time_ms: float,
+                      event_id: int, executor: StepExecutor | None = None) -> dict:
+    """One prefill chunk for a group of requests with equal prompt progress; requests whose
+    prompt completes emit their first token."""
     if not requests:
-        return {"batch_runtime_ms": 0.0, "requests_completed": []}
-    decode_input = torch.tensor([[req.generated_token_ids[-1]] for req in requests], device=device, dtype=torch.long)
-    position_offset = torch.tensor(
-        [req.prompt_len + req.num_generated_tokens - 1 for req in requests], device=device, dtype=torch.long
-    )
-    _ensure_request_kv_caches(model, requests)
-    batched_caches = _stack_layer_caches(requests)
+        return dict(_IDLE)
+    plan = plan_prefill(requests, chunk_size)
+    if plan is None:
+        return dict(_IDLE)
+    return (executor or StepExecutor(model, device)).run(plan, start_time_ms, event_id)
 
-    with timed_section(device=device) as timer:
-        logits, new_caches = model(decode_input, kv_caches=batched_caches, use_cache=True, position_offset=position_offset)
 
-    finish_time_ms = start_time_ms + timer.elapsed_ms
-    next_tokens = torch.argmax(logits[:, -1, :], dim=-1).tolist()
-    completed_requests = []
-    for req_idx, req in enumerate(requests):
-        if req.start_time_ms is None:
-            req.start_time_ms = start_time_ms
-            req.batch_id = event_id
-        req.scheduler_mode = "continuous"
-        req.generated_token_ids.append(int(next_tokens[req_idx]))
-        if req.num_generated_tokens >= req.max_new_tokens:
-            req.phase = "finished"
-            req.finish_time_ms = finish_time_ms
-            completed_requests.append(req)
-        else:
-            req.phase = "decode"
-
-    _scatter_layer_caches(requests, new_caches)
-    live_kv_bytes, reserved_kv_bytes, fragmentation_bytes = _cache_totals(model, requests)
-    gpu_allocated_bytes, gpu_peak_allocated_bytes = _gpu_bytes(device)
-    return {
-        "batch_runtime_ms": timer.elapsed_ms,
-        "requests_completed": completed_requests,
-        "batch_size": len(requests),
-        "tokens_scheduled": len(requests),
-        "phase": "decode",
-        "prompt_len": max(req.prompt_len for req in requests),
-        "max_new_tokens": max(req.max_new_tokens for req in requests),
-        "prefill_tokens": 0,
-        "decode_tokens": len(requests),
-        "decode_kernel_tokens": len(requests),
-        "prefill_runtime_ms": 0.0,
-        "decode_runtime_ms": timer.elapsed_ms,
-        "decode_ms_per_token": timer.elapsed_ms / max(len(requests), 1),
-        "live_kv_bytes": live_kv_bytes,
-        "reserved_kv_bytes": reserved_kv_bytes,
-        "fragmentation_bytes": fragmentation_bytes,
-        "workspace_bytes": 0,
-        "gpu_allocated_bytes": gpu_allocated_bytes,
-        "gpu_peak_allocated_bytes": gpu_peak_allocated_bytes,
-        "backend_name": getattr(model, "attention_backend", "hip_paged"),
-        "padding_waste_tokens": 0,
-        "padding_waste_bytes_est": 0,
-        "padding_waste_pct": 0.0,
-    }
+@torch.no_grad()
+def run_decode_step(model, requests: list, device: str, start_time_ms: float, event_id: int,
+                    executor: StepExecutor | None = None) -> dict:
+    """One decode step: one new token for every request in the group."""
+    if not requests:
+        return dict(_IDLE)
+    return (executor or StepExecutor(model, device)).run(plan_decode(requests), start_time_ms, event_id)

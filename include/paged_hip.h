@@ -233,6 +233,20 @@ int pa_embed_rows(const int64_t* ids, const int64_t* pos_start, int32_t batch, i
                   const void* token_table, int64_t vocab, const void* pos_table, int32_t max_pos,
                   int32_t d_model, void* out, int64_t out_stride, int dtype, void* stream);
 
+/*
+ * pa_argmax_rows: greedy token selection for a step of `batch` requests whose logits are
+ * `rows_per_request` consecutive rows each (row m at logits + m * row_stride elements, `vocab`
+ * values of type dtype): tokens[b] = argmax_v logits[b * rows_per_request + r_b, v] with
+ * r_b = row_index[b] (NULL: 0; a negative value counts from the end of the request's rows, as a
+ * Python index does; then clamped into [0, rows_per_request)). Ties and NaN follow torch.argmax:
+ * the first index of the maximum, NaN above every number. Replaces the per-request
+ * `torch.argmax(logits[b, row, :]).item()` of the continuous-batching executors
+ * (src/serving/continuous_generate.py:145,238) and generate_with_cache
+ * (src/inference/generate_with_cache.py:151,204), so a captured step returns token ids.
+ */
+int pa_argmax_rows(const void* logits, int64_t row_stride, int32_t batch, int32_t rows_per_request,
+                   const int32_t* row_index, int32_t vocab, int dtype, int64_t* tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,7 +9,13 @@ Only functions that no closed form or invariant pins are recorded here:
                        summarize_run (src/serving/metrics.py:19-133) of that run;
   model_logits.json    src/model/transformer.py + src/model/attention.py through
                        src/inference/generate_with_cache.py on the CPU ("paged_reference"):
-                       logits and greedy tokens of a small model with formula-set weights.
+                       logits and greedy tokens of a small model with formula-set weights;
+  executor_run.json    the real continuous-batching executors (src/serving/continuous_generate.py:
+                       82-276) driven by ContinuousBatchingScheduler over a short trace on a small
+                       model on the CPU, with the executors' timer replaced by a fixed 1 ms per
+                       call so the event sequence does not depend on the machine: every event,
+                       every request's generated tokens and timings, the release order and the
+                       pools' final free lists.
 Run from any directory: python tests/golden/make_golden.py. The reference must not be on the
 path of anything else; this script imports it as the package `src`.
 """
@@ -138,10 +144,74 @@ def model_fixture() -> dict:
     }
 
 
+EXECUTOR_MIX = [  # small prompts and decodes so chunks, groups and pool growth all occur
+    ("short", 5, 20, 2, 6, 0.5),
+    ("mid", 21, 45, 3, 9, 0.35),
+    ("long", 46, 70, 4, 8, 0.15),
+]
+
+
+class _FixedTimer:
+    """Stand-in for timed_section: every timed call takes exactly 1 ms."""
+
+    def __init__(self, *args, **kwargs):
+        self.elapsed_ms = 1.0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.elapsed_ms = 1.0
+        return False
+
+
+def executor_fixture() -> dict:
+    import src.serving.continuous_generate as cg
+
+    cg.timed_section = _FixedTimer
+    model = TinyTransformerLM(vocab_size=128, d_model=64, num_heads=4, num_layers=2, d_ff=128, max_seq_len=128,
+                              attention_backend="paged_reference", kv_block_size=8, kv_pool_initial_blocks=8,
+                              kv_pool_growth_factor=2.0).eval()
+    set_weights(model)
+    mix = [RequestWorkloadProfile(*p) for p in EXECUTOR_MIX]
+    reqs = generate_requests(14, 400.0, 128, workload_profiles=mix, seed=11)
+    sched = ContinuousBatchingScheduler(max_batch_size=4, prefill_chunk_size=16, max_tokens_per_iteration=40)
+    released = []
+
+    def release(r):
+        released.append(r.request_id)
+        model.release_request_caches(r.kv_caches)
+
+    with torch.no_grad():
+        done, events = sched.run(
+            reqs,
+            prefill_executor=lambda b, c, t, e: cg.run_prefill_chunk(model, b, c, "cpu", t, e),
+            decode_executor=lambda b, t, e: cg.run_decode_step(model, b, "cpu", t, e),
+            release_request_cache=release)
+    fields = ["batch_id", "dispatch_time_ms", "finish_time_ms", "batch_size", "phase", "tokens_scheduled",
+              "prompt_len", "max_new_tokens", "prefill_tokens", "decode_tokens", "decode_kernel_tokens",
+              "live_kv_bytes", "reserved_kv_bytes", "fragmentation_bytes", "padding_waste_tokens",
+              "padding_waste_bytes_est", "padding_waste_pct", "prefill_runtime_ms", "decode_runtime_ms",
+              "decode_ms_per_token"]
+    return {
+        "config": {"vocab": 128, "d_model": 64, "heads": 4, "layers": 2, "d_ff": 128, "max_seq": 128, "block": 8,
+                   "initial_blocks": 8, "weight_seed": 1234, "weight_scale": 0.2, "mix": EXECUTOR_MIX,
+                   "requests": 14, "rate": 400.0, "seed": 11, "max_batch": 4, "chunk": 16, "budget": 40},
+        "event_fields": fields,
+        "events": [[e[k] for k in fields] for e in events],
+        "requests": [{"request_id": r.request_id, "generated_token_ids": list(r.generated_token_ids),
+                      "start_time_ms": r.start_time_ms, "first_token_time_ms": r.first_token_time_ms,
+                      "finish_time_ms": r.finish_time_ms, "batch_id": r.batch_id} for r in done],
+        "released_order": released,
+        "free_lists": [list(p.free_block_ids) for p in model.layer_block_pools],
+        "capacity_blocks": [p.capacity_blocks for p in model.layer_block_pools],
+    }
+
+
 def main() -> None:
     torch.set_num_threads(1)
     for name, fn in (("loadgen_trace.json", loadgen_fixture), ("scheduler_events.json", scheduler_fixture),
-                     ("model_logits.json", model_fixture)):
+                     ("model_logits.json", model_fixture), ("executor_run.json", executor_fixture)):
         data = fn()
         (HERE / name).write_text(json.dumps(data, indent=None, separators=(",", ":")) + "\n")
         print(f"wrote {name} ({(HERE / name).stat().st_size} bytes)")
