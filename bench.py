@@ -57,12 +57,37 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_threads() -> int:
+def affinity_cores() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baselines: every core this process may run on, capped by the host's
+    per-process thread allotment when one is set (OMP_NUM_THREADS; a shared GPU host allots each
+    one-GPU job a share of its cores and sets it)."""
+    n = affinity_cores()
+    allot = os.environ.get("OMP_NUM_THREADS", "")
+    if allot.isdigit() and int(allot) > 0:
+        n = min(n, int(allot))
+    return max(1, n)
+
+
+def cpu_info() -> dict:
+    """What the CPU baselines ran on: the CPU model, the cores this process may use, and the
+    threads the baselines used."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "affinity_cores": affinity_cores(), "threads": cpu_threads(),
+            "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS")}
 
 
 def pmc_traffic_bytes() -> float | None:
@@ -131,6 +156,7 @@ def cpu_baseline(batch, chunk: int = 32) -> dict:
         "value": batch.decode_bytes() / total_s / 1e9,
         "unit": "GB/s",
         "cores": nthreads,
+        "host": cpu_info(),
         "kind": "port",
         "sample": f"the whole batch ({batch.batch} requests, {sum(lens)} tokens x {H} heads x {Hd}, bf16 KV), "
                   f"copied to host {chunk} requests at a time; oracle C restatement of the reference's paged "
@@ -234,6 +260,66 @@ def time_call(fn, steps: int, warmup: int = 2) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+def time_cold_prefill(q, k_pool, v_pool, page_table, seq_lens, cur_lens, copies: int, replays: int = 3) -> float:
+    """Milliseconds per chunked-prefill call with its KV out of every cache: the call's blocks
+    are copied into `copies` disjoint block sets of a larger pool (random contents) and one HIP
+    graph runs the call once per set, each with its own page table, so that no set is read again
+    before all the others (copies x working set well beyond the 256 MB MALL and the L2s)."""
+    import torch
+
+    from src.kernels.hip_paged_attention import paged_attention_prefill_hip
+
+    dev = q.device
+    used = sorted(set(int(x) for x in page_table.flatten().tolist() if x >= 0))
+    n = len(used)
+    lut = torch.full((k_pool.shape[0],), -1, dtype=torch.int64, device=dev)
+    lut[torch.tensor(used, device=dev)] = torch.arange(n, device=dev)
+    local = torch.where(page_table >= 0, lut[page_table.long().clamp(min=0)], -1)
+    big_k = torch.empty((copies * n,) + tuple(k_pool.shape[1:]), dtype=k_pool.dtype, device=dev)
+    big_v = torch.empty_like(big_k)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    for t in (big_k, big_v):
+        t.copy_(torch.randn(t.shape, generator=gen, device=dev, dtype=torch.float32).to(t.dtype))
+    tables = [torch.where(local >= 0, local + c * n, -1).to(torch.int32).contiguous() for c in range(copies)]
+    out = torch.empty_like(q)
+    fns = [lambda pt=pt: paged_attention_prefill_hip(q, big_k, big_v, pt, seq_lens, cur_lens, out=out)
+           for pt in tables]
+    ms = time_graph_calls(fns, replays)
+    del big_k, big_v
+    torch.cuda.empty_cache()
+    return ms
+
+
+def time_graph_calls(fns, replays: int = 5) -> float:
+    """Milliseconds per call of one HIP graph that runs the callables in `fns` back to back."""
+    import torch
+
+    for fn in fns[:1]:
+        fn()  # eager first: workspaces are allocated outside the capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fns[0]()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in fns:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (replays * len(fns))
+
+
 def time_graph_call(fn, calls: int = 20, replays: int = 5) -> float:
     """Milliseconds per call of `fn` replayed from one HIP graph of `calls` back-to-back calls (the
     way the serving loop replays its decode steps): no Python or launch cost per call."""
@@ -331,6 +417,7 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
         cur = i32(w["chunk_lens"])
         append_ms = time_call(lambda: kv_append_hip(w["k_new"], w["v_new"], w["k_pool"], w["v_pool"], slots), steps)
         attn_ms = time_call(lambda: paged_attention_prefill_hip(w["q"], w["k_pool"], w["v_pool"], pt, s32, cur), steps)
+        cold_ms = time_cold_prefill(w["q"], w["k_pool"], w["v_pool"], pt, s32, cur, copies=64)
         flops = workloads.prefill_flops(w["prev_lens"], w["chunk_lens"], 8, 64)
         peak = 157.3 if tag == "fp32" else 2500.0
         tfs = flops / (attn_ms * 1e-3) / 1e12
@@ -338,7 +425,12 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
             "workload": f"4 requests, 8 heads x 64, context {w['prev_lens']} + chunk {w['chunk_lens']}, "
                         f"{'fp32' if tag == 'fp32' else 'bf16'} KV",
             "attention_us": round(1e3 * attn_ms, 2), "append_us": round(1e3 * append_ms, 2),
+            "attention_us_cold": round(1e3 * cold_ms, 2),
+            "timing": "attention_us: the same call repeated (its ~12 MB of KV stay in L2/MALL, as right after "
+                      "the chunk's append in a serving step); attention_us_cold: the call over 64 disjoint "
+                      "copies of its blocks in one graph (~0.4-0.75 GB, beyond the 256 MB MALL)",
             "useful_gflop": round(flops / 1e9, 4), "TFLOPs": round(tfs, 2),
+            "TFLOPs_cold": round(flops / (cold_ms * 1e-3) / 1e12, 2),
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
         }
         if with_cpu:  # the pools already hold the appended chunks
@@ -379,11 +471,15 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
             del os.environ["PAGED_HIP_PREFILL_KERNEL"]
         else:
             os.environ["PAGED_HIP_PREFILL_KERNEL"] = prev
+    cold_ms = time_cold_prefill(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t, copies=12)
     tfs = flops / (ms * 1e-3) / 1e12
     res["mid_prefill_bf16kv"] = {
         "workload": f"{b.batch} requests, {H} heads x {Hd}, context {b.extra['prev_lens']} + chunk 256 each, "
                     "bf16 KV, fp32 q/out (default dispatch: wide-tile kernel, one unit per CU)",
         "attention_us": round(1e3 * ms, 1), "attention_us_16row_kernel": round(1e3 * ms_tile, 1),
+        "attention_us_cold": round(1e3 * cold_ms, 1),
+        "timing": "attention_us: the same call repeated (~85 MB of KV, largely MALL-resident); attention_us_cold: "
+                  "the call over 12 disjoint copies of its blocks in one graph (~1 GB)",
         "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1), "mfma_peak_TFLOPs": 2500.0,
         "mfma_frac": round(tfs / 2500.0, 4),
     }
@@ -491,6 +587,7 @@ def continuous_batching_pair(device, with_cpu: bool = True) -> dict:
     log(f"continuous batching on the CPU ({torch.get_num_threads()} threads)")
     cpu = continuous_batching(torch.device("cpu"), "paged_reference", warmup=False)
     cpu["threads"] = torch.get_num_threads()
+    cpu["host"] = cpu_info()
     cpu["kind"] = "port: this package's paged_reference backend (vectorised torch) on the CPU, same trace and weights"
     gpu["clock"] = "scheduler virtual clock (sum of measured forward times), as the reference"
     gpu["cpu_baseline"] = cpu

@@ -84,6 +84,18 @@ def default_prefill_split_blocks(batch: int, num_heads: int, query_len: int, max
     return 0
 
 
+def _check_out(name: str, out: torch.Tensor, q: torch.Tensor) -> None:
+    """A caller-supplied output must look like q: the kernels write q's dtype through out's
+    b/h/t strides, with unit stride along head_dim."""
+    if not out.is_cuda or out.device != q.device:
+        raise ValueError(f"{name}: out must be on {q.device}, got {out.device}")
+    if out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError(f"{name}: out must match q's shape {tuple(q.shape)} and dtype {q.dtype}, "
+                         f"got {tuple(out.shape)} {out.dtype}")
+    if out.stride(3) != 1:
+        raise ValueError(f"{name}: out must have unit stride along head_dim")
+
+
 def _check_pool(name: str, k_pool: torch.Tensor, v_pool: torch.Tensor) -> None:
     if k_pool.dim() != 4 or k_pool.shape != v_pool.shape or k_pool.dtype != v_pool.dtype:
         raise ValueError(f"{name}: K/V pools must share shape [num_blocks, H, block_size, head_dim] and dtype")
@@ -121,8 +133,7 @@ def paged_attention_decode_hip(
         _require_i32("order", order)
     if out is None:
         out = torch.empty_like(q)
-    if out.stride(3) != 1:
-        raise ValueError("out must have unit stride along head_dim")
+    _check_out("paged_attention_decode_hip", out, q)
     max_pages = page_table.shape[1] if page_table.dim() == 2 else 0
     pt_stride = page_table.stride(0) if page_table.dim() == 2 and B > 0 else max_pages
     if split_blocks is None:
@@ -170,6 +181,7 @@ def paged_attention_prefill_hip(
     _require_i32("current_lengths", current_lengths)
     if out is None:
         out = torch.empty_like(q)
+    _check_out("paged_attention_prefill_hip", out, q)
     max_pages = page_table.shape[1] if page_table.dim() == 2 else 0
     pt_stride = page_table.stride(0) if page_table.dim() == 2 and B > 0 else max_pages
     if split_blocks is None:

@@ -184,34 +184,32 @@ class TinyTransformerLM(nn.Module):
         [0, max_seq_len). Used before GPU steps, where the graph path clamps instead and an eager
         lookup would fault the device rather than raise. Host data is checked on the host;
         device tensors cost one device->host read."""
-        V, P = self.vocab_size, self.max_seq_len
-
-        def on_device(x):
-            return isinstance(x, torch.Tensor) and x.is_cuda
-
-        parts = []
-        if on_device(input_ids):
-            parts += [input_ids.min(), input_ids.max()]
-        if on_device(positions):
-            parts += [positions.min(), positions.max()]
-        vals = torch.stack([t.to(torch.int64) for t in parts]).tolist() if parts else []
-        if on_device(input_ids):
-            lo_id, hi_id = vals[0], vals[1]
-            vals = vals[2:]
+        dev_ids = isinstance(input_ids, torch.Tensor) and input_ids.is_cuda
+        dev_pos = isinstance(positions, torch.Tensor) and positions.is_cuda
+        if dev_ids or dev_pos:
+            parts = ([input_ids.min(), input_ids.max()] if dev_ids and input_ids.numel() else []) + \
+                    ([positions.min(), positions.max()] if dev_pos and positions.numel() else [])
+            vals = torch.stack([t.to(torch.int64) for t in parts]).tolist() if parts else []
+        if dev_ids:
+            lo_id, hi_id = (vals[0], vals[1]) if input_ids.numel() else (0, 0)
+            vals = vals[2:] if input_ids.numel() else vals
         else:
-            ids = np.asarray(input_ids.cpu() if isinstance(input_ids, torch.Tensor) else input_ids)
+            ids = input_ids.numpy() if isinstance(input_ids, torch.Tensor) else input_ids
             lo_id, hi_id = (int(ids.min()), int(ids.max())) if ids.size else (0, 0)
         if isinstance(positions, int):
             lo_pos = hi_pos = positions
-        elif on_device(positions):
-            lo_pos, hi_pos = vals[0], vals[1]
+        elif dev_pos:
+            lo_pos, hi_pos = (vals[0], vals[1]) if positions.numel() else (0, 0)
+        elif isinstance(positions, list):
+            lo_pos, hi_pos = (min(positions), max(positions)) if positions else (0, 0)
         else:
-            p = np.asarray(positions.cpu() if isinstance(positions, torch.Tensor) else positions, dtype=np.int64)
+            p = positions.numpy() if isinstance(positions, torch.Tensor) else np.asarray(positions)
             lo_pos, hi_pos = (int(p.min()), int(p.max())) if p.size else (0, 0)
-        if lo_id < 0 or hi_id >= V:
-            raise IndexError(f"token id out of range [0, {V}): min {lo_id}, max {hi_id}")
-        if T > 0 and (lo_pos < 0 or hi_pos + T - 1 >= P):
-            raise IndexError(f"positions {lo_pos}..{hi_pos + T - 1} outside the position table [0, {P})")
+        if lo_id < 0 or hi_id >= self.vocab_size:
+            raise IndexError(f"token id out of range [0, {self.vocab_size}): min {lo_id}, max {hi_id}")
+        if T > 0 and (lo_pos < 0 or hi_pos + T - 1 >= self.max_seq_len):
+            raise IndexError(f"positions {lo_pos}..{hi_pos + T - 1} outside the position table "
+                             f"[0, {self.max_seq_len})")
 
     @staticmethod
     def _host_lengths(current_lengths, B: int, T: int) -> list[int]:

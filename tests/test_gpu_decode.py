@@ -2,7 +2,6 @@
 result on the unrounded values and within 1e-4 of the oracle on the same bf16 values)."""
 import math
 import os
-import random
 
 import numpy as np
 import pytest
@@ -168,25 +167,32 @@ def test_negative_page_entries_are_skipped(device):
     assert max_err(got[1:], oracle_out(b)[1:]) <= 1e-4
 
 
-def test_large_ragged_decode_sampled_parity(device):
-    """Full large ragged decode (B=256, 32x128, bf16 KV); a seeded sample of requests, plus the
-    longest and shortest, is checked against the oracle on the same bf16 values."""
+def test_large_ragged_decode_parity(device):
+    """Full large ragged decode (B=256, 32x128, bf16 KV): every request against the oracle on the
+    same bf16 values, 32 requests at a time (their blocks gathered to the host)."""
     b = workloads.large_decode(seed=0, device=device)
     print(f"large decode: B={b.batch} total tokens={sum(b.seq_lens)} pool={b.k_pool.shape[0]}", flush=True)
     got = run(b)
     torch.cuda.synchronize()
-    assert torch.isfinite(got).all()
-    rng = random.Random(0)
     lens = b.seq_lens
-    picks = sorted(set(rng.sample(range(b.batch), 10) + [lens.index(max(lens)), lens.index(min(lens))]))
-    for r in picks:
-        ids = torch.tensor(b.block_lists[r], device=device, dtype=torch.long)
-        k = b.k_pool.index_select(0, ids).cpu()
-        v = b.v_pool.index_select(0, ids).cpu()
-        want = oracle.paged_attention(b.q[r:r + 1].cpu(), k, v, [list(range(len(ids)))], [lens[r]], [1],
-                                      nthreads=NTHREADS)
-        err = max_err(got[r:r + 1], want)
-        print(f"  request {r} L={lens[r]} max err {err:.2e}", flush=True)
+    worst = 0.0
+    for c0 in range(0, b.batch, 32):
+        rows = list(range(c0, min(c0 + 32, b.batch)))
+        ids = torch.tensor([i for r in rows for i in b.block_lists[r]], device=device, dtype=torch.long)
+        k = oracle._np(b.k_pool.index_select(0, ids).cpu())
+        v = oracle._np(b.v_pool.index_select(0, ids).cpu())
+        lists, pos = [], 0
+        for r in rows:
+            lists.append(list(range(pos, pos + len(b.block_lists[r]))))
+            pos += len(b.block_lists[r])
+        want = oracle.paged_attention(b.q[c0:c0 + len(rows)].cpu(), k, v, lists, lens[c0:c0 + len(rows)],
+                                      [1] * len(rows), nthreads=NTHREADS)
+        err = max_err(got[c0:c0 + len(rows)], want)
+        worst = max(worst, err)
+        print(f"  requests {c0}..{rows[-1]} (L {min(lens[r] for r in rows)}..{max(lens[r] for r in rows)}): "
+              f"max err {err:.2e}", flush=True)
         assert err <= 1e-4
+        del k, v
+    print(f"  all {b.batch} requests: max err {worst:.2e}", flush=True)
     del b
     torch.cuda.empty_cache()

@@ -49,11 +49,15 @@ def oracle_out(b):
                                   b.cur_lens, nthreads=NTHREADS)
 
 
-def test_chunked_prefill_config(device):
-    w = workloads.chunked_prefill(seed=0, device=device)
+# seed 0 draws four 256-token chunks; seeds 2 and 4 mix 128- and 256-token chunks, so rows past a
+# 128-token chunk are padded rows inside the 256-row batch (the reference's padded-row semantics)
+@pytest.mark.parametrize("seed,kv_dtype,tol", [(0, torch.float32, 1e-4), (2, torch.float32, 1e-4),
+                                               (4, torch.float32, 1e-4), (2, torch.bfloat16, 2e-2)])
+def test_chunked_prefill_config(device, seed, kv_dtype, tol):
+    w = workloads.chunked_prefill(seed=seed, device=device, kv_dtype=kv_dtype)
     B = len(w["prev_lens"])
-    print(f"chunked prefill ctx={w['prev_lens']} chunk={w['chunk_lens']}", flush=True)
-    pool = LayerBlockPool(block_size=16, initial_blocks=w["k_pool"].shape[0], growth_factor=2.0)
+    print(f"chunked prefill seed={seed} kv={kv_dtype} ctx={w['prev_lens']} chunk={w['chunk_lens']}", flush=True)
+    pool = LayerBlockPool(block_size=16, initial_blocks=w["k_pool"].shape[0], growth_factor=2.0, dtype=kv_dtype)
     pool.ensure_initialized(8, 64, torch.float32, device)
     pool.k_blocks.copy_(w["k_pool"])
     pool.v_blocks.copy_(w["v_pool"])
@@ -80,7 +84,21 @@ def test_chunked_prefill_config(device):
                                   nthreads=NTHREADS)
     err = max_err(out, want)
     print(f"  max err {err:.2e}", flush=True)
-    assert err <= 1e-4
+    assert err <= tol
+
+
+def test_wrappers_reject_mismatched_out(device):
+    b = make_prefill(device, 23, [32, 0], [20, 5], T=20, H=2, Hd=64)
+    for bad in (torch.empty(2, 2, 19, 64, device=device), torch.empty(2, 2, 20, 64, device=device, dtype=torch.bfloat16),
+                torch.empty(2, 2, 64, 20, device=device).transpose(2, 3), torch.empty(2, 2, 20, 64)):
+        with pytest.raises(ValueError, match="out"):
+            run(b, out=bad)
+    d = make_prefill(device, 24, [40], [1], T=1, H=2, Hd=64)
+    with pytest.raises(ValueError, match="out"):
+        paged_attention_decode_hip(d.q, d.k_pool, d.v_pool, d.page_table, d.seq_lens_t, d.cur_lens_t,
+                                   out=torch.empty(1, 2, 1, 32, device=device))
+    ok = torch.empty_like(b.q)
+    assert run(b, out=ok) is ok
 
 
 @pytest.mark.parametrize("kv_dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
@@ -260,38 +278,35 @@ def test_wide_prefill_negative_pages_and_strided_views(device, monkeypatch):
     assert max_err(got[1:], want) <= 2e-2
 
 
-def test_large_prefill_fp32_sampled_parity(device):
-    """The large-prefill workload with fp32 KV (the wide fp32 kernel at this size): one request x
-    four heads against the oracle within 1e-4."""
+def _check_large_request(b, out, r, tol):
+    """Every head of request r of a large-prefill batch against the oracle."""
+    ids = torch.tensor(b.block_lists[r], device=b.q.device, dtype=torch.long)
+    k = b.k_pool.index_select(0, ids).cpu()
+    v = b.v_pool.index_select(0, ids).cpu()
+    want = oracle.paged_attention(b.q[r:r + 1].cpu(), k, v, [list(range(len(b.block_lists[r])))],
+                                  [b.seq_lens[r]], [b.cur_lens[r]], nthreads=NTHREADS)
+    err = max_err(out[r:r + 1], want)
+    print(f"  request {r} (L={b.seq_lens[r]}, all {b.q.shape[1]} heads): max err {err:.2e}", flush=True)
+    assert err <= tol
+
+
+def test_large_prefill_fp32_parity(device):
+    """The large-prefill workload with fp32 KV (the wide fp32 kernel at this size): one request,
+    all 32 heads x 512 rows, against the oracle within 1e-4."""
     b = workloads.large_prefill(seed=1, device=device, kv_dtype=torch.float32)
     out = paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
-    r = 3
-    ids = torch.tensor(b.block_lists[r], device=device, dtype=torch.long)
-    k = b.k_pool.index_select(0, ids)[:, :4].contiguous().cpu()
-    v = b.v_pool.index_select(0, ids)[:, :4].contiguous().cpu()
-    want = oracle.paged_attention(b.q[r:r + 1, :4].cpu(), k, v, [list(range(len(b.block_lists[r])))],
-                                  [b.seq_lens[r]], [b.cur_lens[r]], nthreads=NTHREADS)
-    err = max_err(out[r:r + 1, :4], want)
-    print(f"large fp32 prefill request {r}: max err {err:.2e}", flush=True)
-    assert err <= 1e-4
+    print(f"large fp32 prefill ctx={b.extra['prev_lens']}", flush=True)
+    _check_large_request(b, out, 3, 1e-4)
 
 
-def test_large_prefill_sampled_parity(device):
+def test_large_prefill_parity(device):
     """The MFMA-utilisation workload at full size (8 requests x 32 heads x 128, chunk 512 over
     1-4k contexts, bf16 KV) through the default dispatch (the wide kernel at this size); two
-    requests x four heads are checked against the oracle on the same bf16 values."""
+    requests, every head, against the oracle on the same bf16 values."""
     from src.kernels.hip_paged_attention import cu_count
     b = workloads.large_prefill(seed=0, device=device)
     print(f"large prefill ctx={b.extra['prev_lens']}", flush=True)
     out = paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
     assert 8 * 32 * 4 >= 2 * cu_count(device)  # the wide kernel's grid rule holds at this size
     for r in (0, 5):
-        ids = torch.tensor(b.block_lists[r], device=device, dtype=torch.long)
-        k = b.k_pool.index_select(0, ids)[:, :4].contiguous().cpu()
-        v = b.v_pool.index_select(0, ids)[:, :4].contiguous().cpu()
-        lists = [list(range(len(b.block_lists[r])))]
-        want = oracle.paged_attention(b.q[r:r + 1, :4].cpu(), k, v, lists, [b.seq_lens[r]], [b.cur_lens[r]],
-                                      nthreads=NTHREADS)
-        err = max_err(out[r:r + 1, :4], want)
-        print(f"  request {r}: max err {err:.2e}", flush=True)
-        assert err <= 2e-2
+        _check_large_request(b, out, r, 2e-2)
