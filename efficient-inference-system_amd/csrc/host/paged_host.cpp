@@ -13,6 +13,11 @@
 //                                                       before the append
 //   csr(states, prev, app) -> (bytearray, max_pages)    BatchedPagedKVCache.csr_buffer: int32
 //                                                       [offsets B+1 | prev B | app B | block ids]
+//   step_metadata(states, rows, prev, app, cur, sel, shadow, shadow_len, desc, layout)
+//                                              -> (updates, max_pages)
+//                                                       graph_decode._step_metadata_py: the int32
+//                                                       part of a step's descriptor for the device
+//                                                       block-table mirror (only what changed)
 //
 // Blocks are allocated through the pool's own allocate_block() (LIFO order, growth and its
 // mutation counter unchanged), which a step calls only when a request crosses a block boundary.
@@ -22,6 +27,7 @@
 #include <climits>
 #include <cstdint>
 #include <cstring>
+#include <initializer_list>
 
 namespace {
 
@@ -318,10 +324,129 @@ PyObject* csr(PyObject*, PyObject* args) {
   return Py_BuildValue("(On)", buf.get(), max_pages);
 }
 
+// Writable C-contiguous buffer of int32 words, released at scope exit.
+class Words {
+ public:
+  ~Words() {
+    if (ok_) PyBuffer_Release(&v_);
+  }
+  bool get(PyObject* o, const char* what) {
+    if (PyObject_GetBuffer(o, &v_, PyBUF_WRITABLE | PyBUF_C_CONTIGUOUS) < 0) return false;
+    ok_ = true;
+    if (v_.itemsize != 4) {
+      PyErr_Format(PyExc_TypeError, "%s must hold 4-byte words", what);
+      return false;
+    }
+    return true;
+  }
+  int32_t* data() const { return static_cast<int32_t*>(v_.buf); }
+  Py_ssize_t size() const { return v_.len / 4; }
+
+ private:
+  Py_buffer v_{};
+  bool ok_ = false;
+};
+
+bool seq_i32(PyObject* seq, Py_ssize_t i, int32_t* out) { return as_i32(PySequence_Fast_GET_ITEM(seq, i), out); }
+
+PyObject* step_metadata(PyObject*, PyObject* args) {
+  PyObject *states_in, *rows_in, *prev_in, *app_in, *cur_in, *sel_in, *shadow_in, *shadow_len_in, *desc_in;
+  Py_ssize_t o_cur, o_sel, o_mrow, o_first, o_npages, o_prev, o_app, o_upd, stride;
+  if (!PyArg_ParseTuple(args, "OOOOOOOOO(nnnnnnnnn)", &states_in, &rows_in, &prev_in, &app_in, &cur_in, &sel_in,
+                        &shadow_in, &shadow_len_in, &desc_in, &o_cur, &o_sel, &o_mrow, &o_first, &o_npages,
+                        &o_prev, &o_app, &o_upd, &stride))
+    return nullptr;
+  Ref states(PySequence_Fast(states_in, "states must be a sequence"));
+  Ref rows(PySequence_Fast(rows_in, "rows must be a sequence"));
+  Ref prev(PySequence_Fast(prev_in, "prev must be a sequence"));
+  Ref app(PySequence_Fast(app_in, "app must be a sequence"));
+  Ref cur(PySequence_Fast(cur_in, "cur must be a sequence"));
+  Ref sel(PySequence_Fast(sel_in, "sel must be a sequence"));
+  if (!states || !rows || !prev || !app || !cur || !sel) return nullptr;
+  const Py_ssize_t B = PySequence_Fast_GET_SIZE(states.get());
+  if (PySequence_Fast_GET_SIZE(rows.get()) != B || PySequence_Fast_GET_SIZE(prev.get()) != B ||
+      PySequence_Fast_GET_SIZE(app.get()) != B || PySequence_Fast_GET_SIZE(cur.get()) != B ||
+      PySequence_Fast_GET_SIZE(sel.get()) != B) {
+    PyErr_SetString(PyExc_ValueError, "rows, prev, app, cur and sel need one entry per state");
+    return nullptr;
+  }
+  Words shadow, shadow_len, desc;
+  if (!shadow.get(shadow_in, "shadow") || !shadow_len.get(shadow_len_in, "shadow_len") || !desc.get(desc_in, "desc"))
+    return nullptr;
+  const Py_ssize_t R = shadow_len.size();
+  if (R <= 0 || shadow.size() % R != 0) {
+    PyErr_SetString(PyExc_ValueError, "shadow must be [rows, width] with one length per row");
+    return nullptr;
+  }
+  const Py_ssize_t W = shadow.size() / R;
+  const Py_ssize_t n_desc = desc.size();
+  for (Py_ssize_t o : {o_cur, o_sel, o_mrow, o_first, o_npages, o_prev, o_app}) {
+    if (o < 0 || o + B > n_desc) {
+      PyErr_SetString(PyExc_ValueError, "descriptor layout outside the buffer");
+      return nullptr;
+    }
+  }
+  if (o_upd < 0 || stride < 0 || o_upd + B * stride > n_desc) {
+    PyErr_SetString(PyExc_ValueError, "descriptor layout outside the buffer");
+    return nullptr;
+  }
+  int32_t* d = desc.data();
+  int32_t* sh = shadow.data();
+  int32_t* shl = shadow_len.data();
+  Py_ssize_t n_upd = 0, max_pages = 0;
+  for (Py_ssize_t b = 0; b < B; ++b) {
+    int32_t row;
+    if (!seq_i32(rows.get(), b, &row)) return nullptr;
+    if (row < 0 || row >= R) {
+      PyErr_Format(PyExc_ValueError, "mirror row %d outside [0, %zd)", row, R);
+      return nullptr;
+    }
+    if (!seq_i32(prev.get(), b, &d[o_prev + b]) || !seq_i32(app.get(), b, &d[o_app + b]) ||
+        !seq_i32(cur.get(), b, &d[o_cur + b]) || !seq_i32(sel.get(), b, &d[o_sel + b]))
+      return nullptr;
+    d[o_mrow + b] = row;
+    Ref ids(list_attr(PySequence_Fast_GET_ITEM(states.get(), b), N.block_ids));
+    if (!ids) return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(ids.get());
+    if (n > W) {
+      PyErr_Format(PyExc_ValueError, "a request holds %zd blocks, more than the mirror width %zd", n, W);
+      return nullptr;
+    }
+    max_pages = n > max_pages ? n : max_pages;
+    int32_t* srow = sh + (Py_ssize_t)row * W;
+    const Py_ssize_t known = shl[row] < 0 ? 0 : (shl[row] < n ? shl[row] : n);
+    // first entry that differs from what the row holds; everything from there on is resent
+    Py_ssize_t f = 0;
+    for (; f < known; ++f) {
+      int32_t v;
+      if (!as_i32(PyList_GET_ITEM(ids.get(), f), &v)) return nullptr;
+      if (v != srow[f]) break;
+    }
+    if (n - f > stride) {
+      PyErr_SetString(PyExc_ValueError, "descriptor update area too small");
+      return nullptr;
+    }
+    int32_t* upd = d + o_upd + b * stride;
+    for (Py_ssize_t j = f; j < n; ++j) {
+      int32_t v;
+      if (!as_i32(PyList_GET_ITEM(ids.get(), j), &v)) return nullptr;
+      srow[j] = v;
+      upd[j - f] = v;
+    }
+    n_upd += n - f;
+    shl[row] = (int32_t)n;
+    d[o_first + b] = (int32_t)f;
+    d[o_npages + b] = (int32_t)n;
+  }
+  return Py_BuildValue("(nn)", n_upd, max_pages);
+}
+
 PyMethodDef methods[] = {
     {"lockstep", lockstep, METH_VARARGS, "Whether every layer's cache holds the same states and free-list tail."},
     {"host_append", host_append, METH_VARARGS, "Per-layer append bookkeeping; returns the first cache's lengths."},
     {"csr", csr, METH_VARARGS, "int32 CSR metadata buffer of a batch's block lists, and its max pages."},
+    {"step_metadata", step_metadata, METH_VARARGS,
+     "int32 part of a graph step's descriptor: block-list updates against the device mirror's shadow."},
     {nullptr, nullptr, 0, nullptr},
 };
 

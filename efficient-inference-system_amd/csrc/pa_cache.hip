@@ -99,6 +99,91 @@ __global__ __launch_bounds__(256) void pack_metadata_kernel(const PackArgs a) {
   }
 }
 
+struct MirrorPackArgs {
+  int32_t* mirror;
+  int64_t mirror_stride;
+  int32_t mirror_rows;
+  const int32_t* mirror_row;
+  const int32_t* first_page;
+  const int32_t* num_pages;
+  const int32_t* update_ids;
+  int64_t update_stride;
+  const int32_t* prev_lens;
+  const int32_t* append_lens;
+  int32_t B, T, BS, max_pages;
+  int32_t* page_table;
+  int64_t pt_stride;
+  int32_t* seq_lens;
+  int64_t* seq_lens64;
+  int32_t* slots;
+  const int32_t* stage_src;
+  int32_t* stage_dst;
+  int32_t stage_words;
+};
+
+constexpr int kMirrorSlice = 1024;  // update ids a workgroup stages in LDS (longer lists: read in place)
+
+// One workgroup per request. Request b's block list is its mirror row's first first_page[b] ids
+// followed by its update ids (update_ids + b * update_stride), which are also written into the row.
+// The row is read only below first_page and written only from it on, so no workgroup reads what
+// another writes (the host gives every request of a step its own row). The inputs may sit in host
+// memory, where every dependent read costs a bus round trip: the update slice is loaded into LDS
+// together with the request's header words and the staging copy, all independent of each other,
+// so only the mirror row (device memory) is read after the header arrives.
+__global__ __launch_bounds__(256) void pack_metadata_mirror_kernel(const MirrorPackArgs a) {
+  __shared__ int32_t upd[kMirrorSlice];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t slice = a.update_stride < kMirrorSlice ? a.update_stride : kMirrorSlice;
+  const int32_t* my_upd = a.update_ids ? a.update_ids + (int64_t)b * a.update_stride : nullptr;
+  if (my_upd)
+    for (int k = tid; k < slice; k += 256) upd[k] = my_upd[k];
+  for (int64_t i = (int64_t)b * 256 + tid; i < a.stage_words; i += (int64_t)a.B * 256) a.stage_dst[i] = a.stage_src[i];
+  const int row = a.mirror_row[b];
+  int first = a.first_page[b];
+  int npages = a.num_pages[b];
+  const int32_t prev = a.prev_lens[b];
+  const int32_t app = a.append_lens[b];
+  __syncthreads();
+
+  const bool row_ok = row >= 0 && row < a.mirror_rows;
+  int32_t* mrow = a.mirror + (int64_t)(row_ok ? row : 0) * a.mirror_stride;
+  first = first < 0 ? 0 : (first > a.mirror_stride ? (int)a.mirror_stride : first);
+  if (!row_ok) first = 0;
+  int n_upd = npages - first;
+  n_upd = n_upd < 0 ? 0 : (n_upd > a.update_stride ? (int)a.update_stride : n_upd);
+  if (!my_upd) n_upd = 0;
+  npages = first + n_upd;
+  auto block_at = [&](int p) -> int32_t {
+    if (p < first) return mrow[p];
+    if (p < npages) return p - first < slice ? upd[p - first] : my_upd[p - first];
+    return -1;
+  };
+
+  for (int p = tid; p < a.max_pages; p += 256) a.page_table[(int64_t)b * a.pt_stride + p] = block_at(p);
+  if (row_ok)
+    for (int k = tid; k < n_upd && first + k < a.mirror_stride; k += 256)
+      mrow[first + k] = k < slice ? upd[k] : my_upd[k];
+  if (tid == 0) {
+    a.seq_lens[b] = prev + app;
+    if (a.seq_lens64) a.seq_lens64[b] = prev + app;
+  }
+  if (a.slots) {
+    for (int j = tid; j < a.T; j += 256) {
+      int32_t slot = -1;
+      if (j < app) {
+        const int pos = prev + j;
+        const int pi = pos / a.BS;
+        if (pi < npages) {
+          const int32_t blk = block_at(pi);
+          if (blk >= 0) slot = blk * a.BS + (pos - pi * a.BS);
+        }
+      }
+      a.slots[(int64_t)b * a.T + j] = slot;
+    }
+  }
+}
+
 // Zero K and V tiles of the listed blocks: 16-byte stores, grid-stride over (id, vector).
 __global__ __launch_bounds__(256) void zero_blocks_kernel(uint4* k_pool, uint4* v_pool, int64_t num_blocks,
                                                           int64_t vecs_per_block, const int32_t* ids,
@@ -177,6 +262,40 @@ extern "C" int pa_pack_metadata(const int32_t* block_ids, const int32_t* row_off
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   pack_metadata_kernel<<<grid_for(total), 256, 0, stream>>>(a);
   PA_CHECK_LAUNCH("pack metadata kernel");
+  return PA_OK;
+}
+
+extern "C" int pa_pack_metadata_mirror(int32_t* mirror, int64_t mirror_stride, int32_t mirror_rows,
+                                       const int32_t* mirror_row, const int32_t* first_page,
+                                       const int32_t* num_pages, const int32_t* update_ids, int64_t update_stride,
+                                       const int32_t* prev_lens, const int32_t* append_lens,
+                                       int32_t batch, int32_t query_len, int32_t block_size, int32_t max_pages,
+                                       int32_t* page_table, int64_t pt_stride, int32_t* seq_lens,
+                                       int64_t* seq_lens64, int32_t* slot_mapping,
+                                       const int32_t* stage_src, int32_t* stage_dst, int32_t stage_words,
+                                       void* stream_) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(batch >= 0 && query_len >= 0 && block_size > 0 && max_pages >= 0 && stage_words >= 0 &&
+                   update_stride >= 0,
+               "bad sizes: batch=%d query_len=%d block_size=%d max_pages=%d stage_words=%d update_stride=%lld",
+               batch, query_len, block_size, max_pages, stage_words, (long long)update_stride);
+  PA_CHECK_ARG(mirror_rows > 0 && mirror_stride > 0, "bad mirror shape: rows=%d stride=%lld", mirror_rows,
+               (long long)mirror_stride);
+  if (batch == 0) {
+    PA_CHECK_ARG(stage_words == 0, "stage words need at least one request");
+    return PA_OK;
+  }
+  PA_CHECK_ARG(mirror && mirror_row && first_page && num_pages && prev_lens && append_lens && seq_lens,
+               "null metadata pointer");
+  PA_CHECK_ARG(update_stride == 0 || update_ids, "update_ids missing");
+  PA_CHECK_ARG(max_pages == 0 || (page_table && pt_stride >= max_pages), "page table missing or stride < max_pages");
+  PA_CHECK_ARG(stage_words == 0 || (stage_src && stage_dst), "null staging pointer");
+  MirrorPackArgs a{mirror, mirror_stride, mirror_rows, mirror_row, first_page, num_pages, update_ids, update_stride,
+                   prev_lens, append_lens, batch, query_len, block_size, max_pages, page_table, pt_stride,
+                   seq_lens, seq_lens64, slot_mapping, stage_src, stage_dst, stage_words};
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  pack_metadata_mirror_kernel<<<(unsigned)batch, 256, 0, stream>>>(a);
+  PA_CHECK_LAUNCH("pack metadata (mirror) kernel");
   return PA_OK;
 }
 

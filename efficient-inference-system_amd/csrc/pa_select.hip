@@ -6,15 +6,18 @@
 // decode/prefill step, so a step hands back B token ids instead of [B, T, vocab] logits.
 //
 // Semantics are torch.argmax's: the first index of the maximum; NaN compares above every number
-// (the first NaN wins); -0.0 and +0.0 are equal. One workgroup of kThreads per request: each thread
-// scans a strided slice of the row in increasing index order (so a later equal value never
-// replaces an earlier one), then the (value, index) pairs are reduced over the wavefront with
-// shuffles and over the workgroup's wavefronts in LDS, keeping the lower index on ties.
+// (the first NaN wins); -0.0 and +0.0 are equal. One workgroup of 1024 threads per request (a step
+// has only a few requests, so each row is spread over as many lanes as a workgroup holds and each
+// lane's loads are all in flight at once): each thread scans a strided slice of the row in
+// increasing index order (so a later equal value never replaces an earlier one), then the
+// (value, index) pairs are reduced over the wavefront with shuffles and over the workgroup's
+// wavefronts in LDS, keeping the lower index on ties.
 #include "pa_common.h"
 
 namespace pa {
 
-constexpr int kSelectThreads = 256;
+constexpr int kSelectThreads = 1024;
+constexpr int kSelectLoads = 8;  // loads each thread has in flight per pass (one pass up to 8192 values)
 
 struct Best {
   float v;
@@ -42,19 +45,20 @@ __global__ __launch_bounds__(kSelectThreads) void argmax_rows_kernel(const T* __
 
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  // Four independent loads per iteration; indices stay increasing within a thread.
-  int v = threadIdx.x;
-  for (; v + 3 * kSelectThreads < vocab; v += 4 * kSelectThreads) {
-    float x[4];
+  // All of a pass's loads are issued before any compare; a thread's indices increase within and
+  // across passes, so the first of equal values is kept.
+  for (int base = threadIdx.x; base < vocab; base += kSelectThreads * kSelectLoads) {
+    float x[kSelectLoads];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) x[k] = Elem<T>::load(row + v + k * kSelectThreads);
+    for (int k = 0; k < kSelectLoads; ++k) {
+      const int v = base + k * kSelectThreads;
+      x[k] = v < vocab ? Elem<T>::load(row + v) : -INFINITY;
+    }
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (better(x[k], v + k * kSelectThreads, bv, bi)) { bv = x[k]; bi = v + k * kSelectThreads; }
-  }
-  for (; v < vocab; v += kSelectThreads) {
-    const float x = Elem<T>::load(row + v);
-    if (better(x, v, bv, bi)) { bv = x; bi = v; }
+    for (int k = 0; k < kSelectLoads; ++k) {
+      const int v = base + k * kSelectThreads;
+      if (v < vocab && better(x[k], v, bv, bi)) { bv = x[k]; bi = v; }
+    }
   }
 
 #pragma unroll

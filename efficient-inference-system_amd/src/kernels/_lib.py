@@ -82,6 +82,16 @@ SIGNATURES: dict[str, tuple] = {
          _i32, _i32, _i32, _i32,
          _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     ),
+    "pa_pack_metadata_mirror": (
+        _int,
+        [_c_void_p, _i64, _i32,  # mirror, stride, rows
+         _c_void_p, _c_void_p,  # mirror row, first page
+         _c_void_p, _c_void_p, _i64,  # num pages, update ids, update stride
+         _c_void_p, _c_void_p,  # prev lens, append lens
+         _i32, _i32, _i32, _i32,  # batch, query_len, block_size, max_pages
+         _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,  # page table, stride, seq32, seq64, slots
+         _c_void_p, _c_void_p, _i32, _c_void_p],  # stage src, stage dst, stage words, stream
+    ),
     "pa_linear_rows": (
         _int,
         [_c_void_p, _i64, _i32, _i32,  # x, stride, rows, in_features

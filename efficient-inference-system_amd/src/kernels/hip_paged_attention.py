@@ -306,3 +306,48 @@ def argmax_rows_hip(logits: torch.Tensor, row_index: torch.Tensor | None, out: t
     )
     _lib.check(status, "pa_argmax_rows")
     return out
+
+
+def pack_metadata_mirror_hip(
+    mirror: torch.Tensor,
+    desc_addrs: dict,
+    *,
+    batch: int,
+    query_len: int,
+    block_size: int,
+    max_pages: int,
+    stage_dst: torch.Tensor | None = None,
+    stage_words: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """pa_pack_metadata_mirror: (page_table int32 [B, max_pages], seq_lens int32 [B], seq_lens int64
+    [B], slot_mapping int32 [B * query_len]) from the device block-table mirror (int32 [rows,
+    width], updated in place) and a step descriptor given as device addresses (pinned host memory
+    the device reads, or device memory) under the keys mirror_row, first_page, num_pages,
+    update_ids, prev_lens, append_lens and, with stage_words > 0, stage_src, plus the int
+    update_stride (words between two requests' update ids); stage_words int32 words are copied
+    from stage_src into stage_dst by the same launch."""
+    _require_gpu("pack_metadata_mirror_hip", mirror)
+    if mirror.dtype != torch.int32 or mirror.dim() != 2 or mirror.stride(1) != 1:
+        raise ValueError("mirror must be an int32 [rows, width] tensor with unit column stride")
+    if stage_words:
+        if stage_dst is None or stage_dst.dtype != torch.int32 or not stage_dst.is_contiguous() \
+                or stage_dst.numel() < stage_words or stage_dst.device != mirror.device:
+            raise ValueError("stage_dst must be a contiguous int32 device tensor of at least stage_words words")
+    dev = mirror.device
+    page_table = torch.empty((batch, max_pages), dtype=torch.int32, device=dev)
+    seq32 = torch.empty((batch,), dtype=torch.int32, device=dev)
+    seq64 = torch.empty((batch,), dtype=torch.int64, device=dev)
+    slots = torch.empty((batch * query_len,), dtype=torch.int32, device=dev)
+    d = desc_addrs
+    status = _lib.load().pa_pack_metadata_mirror(
+        mirror.data_ptr(), mirror.stride(0), mirror.shape[0],
+        d["mirror_row"], d["first_page"], d["num_pages"], d["update_ids"], d["update_stride"],
+        d["prev_lens"], d["append_lens"],
+        batch, query_len, block_size, max_pages,
+        page_table.data_ptr() if max_pages else None, max_pages, seq32.data_ptr(), seq64.data_ptr(),
+        slots.data_ptr() if slots.numel() else None,
+        d.get("stage_src") if stage_words else None, stage_dst.data_ptr() if stage_words else None, stage_words,
+        _stream_ptr(dev),
+    )
+    _lib.check(status, "pa_pack_metadata_mirror")
+    return page_table, seq32, seq64, slots

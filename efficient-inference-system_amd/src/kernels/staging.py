@@ -37,7 +37,9 @@ class _Hip:
         for name, args in (("hipMemcpyAsync", [vp, vp, ctypes.c_size_t, ctypes.c_int, vp]),
                            ("hipEventCreateWithFlags", [ctypes.POINTER(vp), ctypes.c_uint]),
                            ("hipEventRecord", [vp, vp]),
-                           ("hipEventSynchronize", [vp])):
+                           ("hipEventSynchronize", [vp]),
+                           ("hipHostMalloc", [ctypes.POINTER(vp), ctypes.c_size_t, ctypes.c_uint]),
+                           ("hipHostGetDevicePointer", [ctypes.POINTER(vp), vp, ctypes.c_uint])):
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
@@ -45,9 +47,18 @@ class _Hip:
         self.event_create = lib.hipEventCreateWithFlags
         self.event_record = lib.hipEventRecord
         self.event_sync = lib.hipEventSynchronize
+        self.host_malloc = lib.hipHostMalloc
+        self.host_device_pointer = lib.hipHostGetDevicePointer
 
 
 _hip: _Hip | None = None
+
+
+def _runtime() -> _Hip:
+    global _hip
+    if _hip is None:
+        _hip = _Hip()
+    return _hip
 
 
 def _check(status: int, what: str) -> None:
@@ -57,9 +68,7 @@ def _check(status: int, what: str) -> None:
 
 class _PinnedRing:
     def __init__(self, device: torch.device):
-        global _hip
-        if _hip is None:
-            _hip = _Hip()
+        _runtime()
         self.device = device
         self.host = torch.empty(_SLOTS * _SLOT_BYTES, dtype=torch.uint8, pin_memory=True)
         self.host_np = self.host.numpy()
@@ -124,3 +133,43 @@ def upload_into(arr: np.ndarray, dst: torch.Tensor) -> None:
         raise ValueError("upload_into: destination must be contiguous and large enough")
     if arr.nbytes:
         _ring(dst.device).upload_into(arr, dst)
+
+
+_HOST_MAPPED_COHERENT = 0x2 | 0x40000000  # hipHostMallocMapped | hipHostMallocCoherent
+
+
+class MappedHostWords:
+    """int32 words of pinned host memory that kernels read (and write) directly: allocated with
+    hipHostMalloc as mapped, coherent memory, so a kernel sees the host's latest stores without a
+    copy call and without stale cache lines. The host must not rewrite words a launch reads until
+    that launch has run: mark(stream) after enqueueing such a launch, wait() before the next
+    rewrite (an event; free when the launch has already finished). Kept until the process ends:
+    graphs captured with its device address may outlive any owner."""
+
+    def __init__(self, words: int, device: torch.device):
+        hip = _runtime()
+        with torch.cuda.device(device):
+            ptr = ctypes.c_void_p()
+            _check(hip.host_malloc(ctypes.byref(ptr), 4 * words, _HOST_MAPPED_COHERENT), "hipHostMalloc")
+            dptr = ctypes.c_void_p()
+            _check(hip.host_device_pointer(ctypes.byref(dptr), ptr, 0), "hipHostGetDevicePointer")
+            ev = ctypes.c_void_p()
+            _check(hip.event_create(ctypes.byref(ev), _EVENT_DISABLE_TIMING), "hipEventCreateWithFlags")
+        self.words = np.ctypeslib.as_array((ctypes.c_int32 * words).from_address(ptr.value))
+        self.words[:] = 0
+        self.host_ptr = ptr.value
+        self.device_ptr = dptr.value
+        self.event = ev
+        self.pending = False
+
+    def device_addr(self, word: int = 0) -> int:
+        return self.device_ptr + 4 * word
+
+    def wait(self) -> None:
+        if self.pending:
+            _check(_hip.event_sync(self.event), "hipEventSynchronize")
+            self.pending = False
+
+    def mark(self, stream: int) -> None:
+        _check(_hip.event_record(self.event, stream), "hipEventRecord")
+        self.pending = True

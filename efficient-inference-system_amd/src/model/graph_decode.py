@@ -5,14 +5,27 @@ mode the host (Python and the framework's dispatch) is the bottleneck. This runn
 whole step once per (batch size, query-length bucket) and replays it:
 
   outside the graph (host):  the cache bookkeeping of every layer (block allocation in the
-                             reference's LIFO order, seq_len advance), one upload of the batch's
-                             block lists in CSR form into a static device buffer, and copies of the
-                             token ids, start positions and current lengths into static buffers;
-  inside the graph (device): metadata packing (page table, lengths, slot of every new token),
-                             then per layer LayerNorm, q/k/v projections, KV scatter into the pool,
-                             paged attention (decode kernel for one-token steps, chunked-prefill
-                             kernel otherwise), output projection, MLP and residuals; final
-                             LayerNorm and lm_head.
+                             reference's LIFO order, seq_len advance), then the step descriptor:
+                             token ids, first positions, current lengths, greedy rows and, per
+                             request, only the part of its block list that its row of the device
+                             block-table mirror does not hold yet (normally the blocks this step
+                             opened). The descriptor is pinned host memory the device reads
+                             directly, so a step issues no copy call;
+  inside the graph (device): one launch reads the descriptor, updates the mirror rows and builds
+                             the page table, lengths and the slot of every new token, staging the
+                             ids, positions and lengths into device buffers; then per layer
+                             LayerNorm, q/k/v projections, KV scatter into the pool, paged
+                             attention (decode kernel for one-token steps, chunked-prefill kernel
+                             otherwise), output projection, MLP and residuals; final LayerNorm and
+                             lm_head; and the greedy argmax of each request's selected row.
+
+The mirror (int32 [rows, width] on the device) keeps every live request's block list between
+steps; the host keeps a shadow copy and, each step, sends a request's list from the first entry
+that differs from the shadow (the whole list for a request new to its row), so host-to-device
+traffic is O(blocks opened) per step and a block list edited by hand is still sent correctly.
+Requests own rows by the identity of their first layer's cache state; a row returns to the free
+list when that state is garbage collected, and the least recently used row is taken over when
+none is free.
 
 Steps of at most FUSED_STEP_ROWS rows (B * bucketed T: every decode step, and prefill chunks up
 to 384 rows) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
@@ -37,6 +50,7 @@ from __future__ import annotations
 
 import math
 import os
+import weakref
 
 import numpy as np
 import torch
@@ -44,9 +58,9 @@ import torch
 from src.cache.paged_kv import BatchedPagedKVCache
 from src.kernels import _lib, hip_linear
 from src.kernels.hip_paged_attention import (
-    _workspace, argmax_rows_hip, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
-    pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
-from src.kernels.staging import upload_into
+    _stream_ptr, _workspace, argmax_rows_hip, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
+    pack_metadata_mirror_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
+from src.kernels.staging import MappedHostWords
 
 try:  # native host bookkeeping (csrc/host/paged_host.cpp): same results as the Python below
     from src.cache import _paged_host as _host
@@ -142,22 +156,139 @@ def _lockstep_py(kv_caches: list[BatchedPagedKVCache], max_new_blocks: int) -> b
     return True
 
 
+def _step_metadata_py(states, rows, prev, app, cur, sel, shadow, shadow_len, desc, layout) -> tuple[int, int]:
+    """Python restatement of the native step_metadata: write the int32 part of a step's
+    descriptor (current lengths, greedy rows, mirror rows, first changed page, list lengths,
+    lengths before the append, appended counts, and each request's block-list update against its
+    mirror row's shadow at a fixed stride) and update the shadow. desc is a flat int32 array;
+    layout = (o_cur, o_sel, o_mrow, o_first, o_npages, o_prev, o_app, o_upd, stride) word offsets
+    and the update stride. Returns (update count, longest block list)."""
+    o_cur, o_sel, o_mrow, o_first, o_npages, o_prev, o_app, o_upd, stride = layout
+    R, W = shadow.shape
+    n_upd = max_pages = 0
+    for b, st in enumerate(states):
+        row = rows[b]
+        if not 0 <= row < R:
+            raise ValueError(f"mirror row {row} outside [0, {R})")
+        desc[o_cur + b], desc[o_sel + b], desc[o_mrow + b] = cur[b], sel[b], row
+        desc[o_prev + b], desc[o_app + b] = prev[b], app[b]
+        ids = st.block_ids
+        n = len(ids)
+        if n > W:
+            raise ValueError(f"a request holds {n} blocks, more than the mirror width {W}")
+        max_pages = max(max_pages, n)
+        known = min(max(int(shadow_len[row]), 0), n)
+        f = 0
+        while f < known and ids[f] == shadow[row, f]:
+            f += 1
+        if n - f > stride:
+            raise ValueError("descriptor update area too small")
+        shadow[row, f:n] = ids[f:n]
+        u = o_upd + b * stride
+        desc[u:u + n - f] = ids[f:n]
+        n_upd += n - f
+        shadow_len[row] = n
+        desc[o_first + b], desc[o_npages + b] = f, n
+    return n_upd, max_pages
+
+
+class _BlockTableMirror:
+    """The device block-table mirror (int32 [rows, width]), its host shadow and the assignment of
+    rows to requests (by the identity of the request's first-layer cache state)."""
+
+    def __init__(self, rows: int, width: int, device: torch.device):
+        self.rows, self.width = rows, width
+        self.dev = torch.full((rows, width), -1, dtype=torch.int32, device=device)
+        self.shadow = np.full((rows, width), -1, dtype=np.int32)
+        self.shadow_len = np.zeros((rows,), dtype=np.int32)
+        self._row_of: dict[int, int] = {}
+        self._owner: list = [None] * rows     # weakref to the state owning the row
+        self._used = [0] * rows              # step stamp of the row's last use
+        self._free = list(range(rows - 1, -1, -1))
+        self._stamp = 0
+
+    def _drop(self, row: int) -> None:
+        ref = self._owner[row]
+        if ref is not None:
+            for key, r in list(self._row_of.items()):
+                if r == row:
+                    del self._row_of[key]
+                    break
+        self._owner[row] = None
+        self.shadow_len[row] = 0
+
+    def _on_state_gone(self, row: int, ref) -> None:
+        if self._owner[row] is ref:
+            self._drop(row)
+            self._free.append(row)
+
+    def rows_for(self, states) -> list[int] | None:
+        """One row per state (distinct states), or None when there are more states than rows."""
+        if len(states) > self.rows:
+            return None
+        self._stamp += 1
+        stamp = self._stamp
+        out = []
+        for st in states:
+            r = self._row_of.get(id(st))
+            if r is None or self._owner[r] is None or self._owner[r]() is not st:
+                r = self._take(stamp)
+                self._owner[r] = weakref.ref(st, lambda ref, row=r, me=weakref.ref(self): (
+                    me() is not None and me()._on_state_gone(row, ref)))
+                self._row_of[id(st)] = r
+                self.shadow_len[r] = 0
+            self._used[r] = stamp
+            out.append(r)
+        return out
+
+    def _take(self, stamp: int) -> int:
+        if self._free:
+            return self._free.pop()
+        victim = min((r for r in range(self.rows) if self._used[r] != stamp), key=lambda r: self._used[r])
+        self._drop(victim)
+        return victim
+
+    def forget(self, rows: list[int]) -> None:
+        """The device copy of these rows is unknown (a step failed after its descriptor was
+        written): resend them whole next time."""
+        for r in rows:
+            self.shadow_len[r] = 0
+
+
 class _Captured:
-    def __init__(self, model, B: int, Tb: int, pages: int, device: torch.device, pools):
+    def __init__(self, model, B: int, Tb: int, pages: int, device: torch.device, pools, mirror_width: int):
         H, Hd = model.num_heads, model.head_dim
         self.B, self.Tb, self.pages = B, Tb, pages
-        # [token ids padded to Tb | first positions], int64, one buffer so host data is one upload
-        self.io = torch.zeros((B * Tb + B,), dtype=torch.long, device=device)
-        self.ids = self.io[:B * Tb].view(B, Tb)
-        self.pos = self.io[B * Tb:]
-        # [current lengths | greedy rows]: the attention's cur_lens and, per request, the logits row
-        # whose argmax the step writes into self.tokens
-        self.sel = torch.zeros((2 * B,), dtype=torch.int32, device=device)
-        self.sel_host: tuple | None = None
-        self.cur = self.sel[:B]
-        self.rows = self.sel[B:]
+        # Step descriptor (int32 words of pinned host memory the device reads):
+        #   [ids int64 B*Tb | first positions int64 B | current lengths B | greedy rows B]
+        #     staged into the device buffer `stage` by the metadata launch;
+        #   [mirror rows B | first changed page B | list lengths B | lengths before B | appended B |
+        #    update ids, mirror width words per request]  read by that launch in place.
+        o_pos = 2 * B * Tb
+        o_cur = o_pos + 2 * B
+        o_sel = o_cur + B
+        self.stage_words = o_sel + B
+        o_mrow = self.stage_words
+        o_first, o_npages = o_mrow + B, o_mrow + 2 * B
+        o_prev = o_npages + B
+        o_app = o_prev + B
+        o_upd = o_app + B
+        self.layout = (o_cur, o_sel, o_mrow, o_first, o_npages, o_prev, o_app, o_upd, mirror_width)
+        self.desc = MappedHostWords(o_upd + B * mirror_width, device)
+        w = self.desc.words
+        self.ids_host = w[0:o_pos].view(np.int64).reshape(B, Tb)
+        self.pos_host = w[o_pos:o_cur].view(np.int64)
+        addr = self.desc.device_addr
+        self.desc_addrs = {"mirror_row": addr(o_mrow), "first_page": addr(o_first), "num_pages": addr(o_npages),
+                           "update_ids": addr(o_upd), "update_stride": mirror_width, "prev_lens": addr(o_prev),
+                           "append_lens": addr(o_app), "stage_src": addr(0)}
+        self.stage = torch.zeros((self.stage_words,), dtype=torch.int32, device=device)
+        self.ids = self.stage[0:o_pos].view(torch.int64).view(B, Tb)
+        self.pos = self.stage[o_pos:o_cur].view(torch.int64)
+        self.cur = self.stage[o_cur:o_sel]
+        self.rows = self.stage[o_sel:o_sel + B]
         self.tokens = torch.zeros((B,), dtype=torch.int64, device=device)
-        self.csr = torch.zeros((3 * B + 1 + B * pages,), dtype=torch.int32, device=device)
+        self.last_sel: list[int] = [0] * B
         lib = _lib.load()
         if Tb == 1:
             self.split_blocks = default_split_blocks(B, H, pages, device)
@@ -184,6 +315,7 @@ class GraphedStep:
         self.captured: dict[tuple[int, int], _Captured] = {}
         self.captures = 0
         self._attns = None
+        self.mirror: _BlockTableMirror | None = None
 
     def usable(self, input_ids, kv_caches) -> bool:
         """Whether a step over input_ids ([B, T], device tensor or host data) and these per-layer
@@ -201,6 +333,9 @@ class GraphedStep:
         B, T = input_ids.shape
         if bucket_for(T) is None:
             return False
+        states0 = kv_caches[0].states
+        if len({id(st) for st in states0}) != len(states0):
+            return False  # a request twice in one batch: its mirror row would be written twice
         # a request appending up to T tokens opens at most ceil(T / block) + 1 new blocks
         return _lockstep(kv_caches, B * (-(-T // m.kv_block_size) + 1))
 
@@ -208,11 +343,9 @@ class GraphedStep:
     def _static_forward(self, cap: _Captured, pools) -> torch.Tensor:
         m = self.model
         B, Tb = cap.B, cap.Tb
-        csr = cap.csr
-        pt, seq32, _, slots = pack_metadata_hip(
-            csr[3 * B + 1:], csr[0:B + 1], csr[B + 1:2 * B + 1], csr[2 * B + 1:3 * B + 1],
-            query_len=Tb, block_size=m.kv_block_size, max_pages=cap.pages, with_slots=True,
-        )
+        pt, seq32, _, slots = pack_metadata_mirror_hip(
+            self.mirror.dev, cap.desc_addrs, batch=B, query_len=Tb, block_size=m.kv_block_size,
+            max_pages=cap.pages, stage_dst=cap.stage, stage_words=cap.stage_words)
         if cap.embed_fused:
             x = hip_linear.embed_rows_hip(cap.ids, cap.pos, m.token_emb, m.pos_emb).view(B, Tb, -1)
         else:
@@ -296,15 +429,25 @@ class GraphedStep:
         self.captures += 1
 
     # ------------------------------------------------------------------------------------------
+    def _mirror_for(self, B: int, pages: int, device: torch.device) -> _BlockTableMirror:
+        """The mirror, (re)allocated when a step needs more rows or a wider row than it has; a new
+        mirror has a new device address, so every graph is captured again."""
+        mir = self.mirror
+        if mir is None or B > mir.rows or pages > mir.width:
+            rows = max(64, 2 * B, mir.rows if mir is not None else 0)
+            width = max(pages, mir.width if mir is not None else 0)
+            self.mirror = mir = _BlockTableMirror(rows, width, device)
+            self.captured.clear()
+        return mir
+
     def __call__(self, input_ids, positions, current_lengths: list[int], kv_caches, rows: list[int] | None = None,
                  want_logits: bool = True):
         """One cached step, replayed from a captured graph that ends in a greedy argmax.
 
-        input_ids: [B, T] token ids, a device tensor or host data (tensor or numpy array);
-        positions: int, or each request's first position (device tensor or host data);
-        current_lengths: host list (the reference's current_lengths, before clamping);
-        rows: per request, the logits row whose argmax becomes its token (None keeps the last
-        rows uploaded: the tokens are then not meaningful).
+        input_ids: [B, T] token ids as host data (numpy array or CPU tensor); positions: int, or
+        each request's first position as host data; current_lengths: host list (the reference's
+        current_lengths, before clamping); rows: per request, the logits row whose argmax becomes
+        its token (None: row 0; the tokens then mean nothing).
         Returns (logits [B, T, vocab] or None when want_logits is False, tokens): tokens is an
         int64 [B] device tensor owned by the graph, overwritten by the next step of this batch
         size and bucket. The caller checks ids and positions first (the model's
@@ -317,53 +460,42 @@ class GraphedStep:
         app = [max(min(c, T), 0) for c in current_lengths]
         if _host is not None:
             prev = _host.host_append(kv_caches, app, m.num_heads, m.head_dim, pools[0].dtype, device)
-            raw, max_pages = _host.csr(kv_caches[0].states, prev, app)
-            buf = np.frombuffer(raw, dtype=np.int32)
         else:
             prev = None
             for cache in kv_caches:
                 p = cache.host_append(app, T, m.num_heads, m.head_dim, pools[0].dtype, device)
                 prev = p if prev is None else prev
-            buf, max_pages = kv_caches[0].csr_buffer(prev, app)
-        pages = max(math.ceil(m.max_seq_len / m.kv_block_size), max_pages)
+        states0 = kv_caches[0].states
+        max_pages = max((len(st.block_ids) for st in states0), default=0)
+        pages = max(-(-m.max_seq_len // m.kv_block_size), max_pages)
+        mirror = self._mirror_for(B, pages, device)
         sig = _signature(pools)
         key = (B, Tb)
         cap = self.captured.get(key)
         if cap is None or cap.signature != sig or cap.pages < max_pages:
             if cap is not None and cap.signature != sig:
                 self.captured.clear()  # every graph holds the old storage addresses
-            cap = _Captured(m, B, Tb, pages, device, pools)
+            cap = _Captured(m, B, Tb, pages, device, pools, mirror.width)
             self.captured[key] = cap
-        upload_into(buf, cap.csr)
-        if isinstance(input_ids, torch.Tensor) and input_ids.is_cuda:
-            if (Tb == T and isinstance(positions, torch.Tensor) and positions.is_cuda
-                    and positions.dtype == cap.pos.dtype and input_ids.dtype == cap.ids.dtype):
-                torch._foreach_copy_([cap.ids, cap.pos], [input_ids, positions.view(B)])  # one launch
+        mrows = mirror.rows_for(states0)
+        cap.desc.wait()  # the previous replay of this graph has read its descriptor
+        try:
+            sel = list(rows) if rows is not None else [0] * B
+            step = _host.step_metadata if _host is not None else _step_metadata_py
+            step(states0, mrows, prev, app, current_lengths, sel, mirror.shadow, mirror.shadow_len,
+                 cap.desc.words, cap.layout)
+            ids = input_ids.numpy() if isinstance(input_ids, torch.Tensor) else input_ids
+            if T == Tb:
+                cap.ids_host[:] = ids
             else:
-                if Tb == T:
-                    cap.ids.copy_(input_ids)
-                else:
-                    cap.ids.zero_()
-                    cap.ids[:, :T].copy_(input_ids)
-                if isinstance(positions, int):
-                    cap.pos.fill_(positions)
-                else:
-                    cap.pos.copy_(torch.as_tensor(positions).view(B))
-        else:
-            # host token ids: one upload of [ids padded to the bucket | first positions]
-            io = np.zeros((B * Tb + B,), dtype=np.int64)
-            ids = input_ids.cpu().numpy() if isinstance(input_ids, torch.Tensor) else np.asarray(input_ids)
-            io[:B * Tb].reshape(B, Tb)[:, :T] = ids
-            if isinstance(positions, torch.Tensor):
-                positions = positions.cpu().numpy()
-            io[B * Tb:] = positions
-            upload_into(io, cap.io)
-        sel = tuple(current_lengths) + (tuple(rows) if rows is not None
-                                        else (cap.sel_host[B:] if cap.sel_host is not None else (0,) * B))
-        if sel != cap.sel_host:
-            upload_into(np.asarray(sel, dtype=np.int32), cap.sel)
-            cap.sel_host = sel
-        if cap.graph is None:
-            self._capture(cap, pools)
-        cap.graph.replay()
+                cap.ids_host[:, :T] = ids
+                cap.ids_host[:, T:] = 0
+            cap.pos_host[:] = positions.numpy() if isinstance(positions, torch.Tensor) else positions
+            if cap.graph is None:
+                self._capture(cap, pools)
+            cap.graph.replay()
+            cap.desc.mark(_stream_ptr(device))
+        except BaseException:
+            mirror.forget(mrows)
+            raise
         return (cap.logits[:, :T].clone() if want_logits else None), cap.tokens

@@ -212,6 +212,23 @@ class TinyTransformerLM(nn.Module):
                              f"[0, {self.max_seq_len})")
 
     @staticmethod
+    def _host_step_inputs(input_ids, positions):
+        """Token ids and first positions of a graph step as host data (a graph step takes them
+        from pinned host memory): device tensors are read back in one copy."""
+        on_dev = [isinstance(x, torch.Tensor) and x.is_cuda for x in (input_ids, positions)]
+        if on_dev[0] and on_dev[1]:
+            n = input_ids.numel()
+            both = torch.cat([input_ids.reshape(-1).to(torch.int64), positions.reshape(-1).to(torch.int64)]).cpu()
+            return both[:n].view(input_ids.shape).numpy(), both[n:].numpy()
+        ids = input_ids.cpu() if on_dev[0] else input_ids
+        pos = positions.cpu() if on_dev[1] else positions
+        if isinstance(ids, torch.Tensor):
+            ids = ids.to(torch.int64).numpy()
+        if isinstance(pos, torch.Tensor):
+            pos = pos.reshape(-1).to(torch.int64).numpy()
+        return ids, pos
+
+    @staticmethod
     def _host_lengths(current_lengths, B: int, T: int) -> list[int]:
         if current_lengths is None:
             return [T] * B
@@ -243,14 +260,15 @@ class TinyTransformerLM(nn.Module):
             raise IndexError(f"select_rows {rows} out of range for {B} requests of {T} rows")
         rows = [r % T for r in rows]
         device = self.token_emb.weight.device
-        if device.type == "cuda":
-            self.check_token_inputs(input_ids, position_offset, T)
         if kv_caches is not None and device.type == "cuda":
             runner = self._graph_runner()
             if runner.usable(input_ids, kv_caches):
-                logits, tokens = runner(input_ids, position_offset, cur, kv_caches, rows=rows,
-                                        want_logits=return_logits)
+                ids_h, pos_h = self._host_step_inputs(input_ids, position_offset)
+                self.check_token_inputs(ids_h, pos_h, T)
+                logits, tokens = runner(ids_h, pos_h, cur, kv_caches, rows=rows, want_logits=return_logits)
                 return tokens, logits, list(kv_caches)
+        if device.type == "cuda":
+            self.check_token_inputs(input_ids, position_offset, T)
         ids = torch.as_tensor(input_ids, dtype=torch.long).to(device)
         pos = position_offset if isinstance(position_offset, int) else \
             torch.as_tensor(position_offset, dtype=torch.long).to(device)
@@ -269,14 +287,16 @@ class TinyTransformerLM(nn.Module):
     ):
         B, T = input_ids.shape
         device = input_ids.device
-        if input_ids.is_cuda:
-            self.check_token_inputs(input_ids, position_offset, T)
         if use_cache and kv_caches is not None and input_ids.is_cuda:
             runner = self._graph_runner()
             if runner.usable(input_ids, kv_caches):
+                ids_h, pos_h = self._host_step_inputs(input_ids, position_offset)
+                self.check_token_inputs(ids_h, pos_h, T)
                 cur = self._host_lengths(current_lengths, B, T)
-                logits, _ = runner(input_ids, position_offset, cur, kv_caches)
+                logits, _ = runner(ids_h, pos_h, cur, kv_caches)
                 return logits, list(kv_caches)
+        if input_ids.is_cuda:
+            self.check_token_inputs(input_ids, position_offset, T)
         if isinstance(position_offset, int):
             positions = torch.arange(position_offset, position_offset + T, device=device).unsqueeze(0).expand(B, T)
         else:

@@ -169,6 +169,32 @@ int pa_pack_metadata(const int32_t* block_ids, const int32_t* row_offsets,
                      int64_t* seq_lens64, int32_t* slot_mapping, void* stream);
 
 /*
+ * pa_pack_metadata with the block lists kept on the device between steps, so a step sends only
+ * what changed: mirror is int32 [mirror_rows, mirror_stride] device memory that persists across
+ * calls; request b of this step owns row mirror_row[b] (distinct rows within a call), and its
+ * block list (num_pages[b] ids) is the row's first first_page[b] ids followed by the
+ * num_pages[b] - first_page[b] ids at update_ids + b * update_stride, which the call also writes
+ * into the row from first_page[b] on. Outputs are those of pa_pack_metadata for that list
+ * (page_table, seq_lens, seq_lens64, slot_mapping; the last two may be NULL). The call also copies
+ * stage_words int32 words from stage_src to stage_dst (0: none), so a step's other small inputs
+ * (token ids, positions, lengths) reach device buffers in the same launch. The inputs may live in
+ * pinned host memory the device can read (hipHostMalloc), which lets a captured step take new
+ * inputs without a copy call; the host must then not rewrite them until the launch has run. No
+ * reference counterpart as one call: together with the host's diff of each request's block list
+ * against what its row holds, it replaces the per-call rebuild of page_table_tensor /
+ * seq_lens_tensor (src/cache/paged_kv.py:174-197) from every request's whole block list.
+ */
+int pa_pack_metadata_mirror(int32_t* mirror, int64_t mirror_stride, int32_t mirror_rows,
+                            const int32_t* mirror_row, const int32_t* first_page,
+                            const int32_t* num_pages, const int32_t* update_ids, int64_t update_stride,
+                            const int32_t* prev_lens, const int32_t* append_lens,
+                            int32_t batch, int32_t query_len, int32_t block_size, int32_t max_pages,
+                            int32_t* page_table, int64_t pt_stride, int32_t* seq_lens,
+                            int64_t* seq_lens64, int32_t* slot_mapping,
+                            const int32_t* stage_src, int32_t* stage_dst, int32_t stage_words,
+                            void* stream);
+
+/*
  * Zero the K and V tiles of n_ids pool blocks (block_ids on device), the batched form of
  * LayerBlockPool.release_block's per-block zero_() (src/cache/paged_kv.py:80-85).
  * Ids outside [0, num_blocks) are skipped.

@@ -33,7 +33,7 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
         "pa_argmax_rows", "pa_decode", "pa_decode_noalloc", "pa_decode_workspace_size", "pa_embed_rows", "pa_kv_append", "pa_last_error_message",
         "pa_linear_rows",
-        "pa_pack_metadata", "pa_prefill", "pa_prefill_workspace_size", "pa_qkv_append", "pa_version",
+        "pa_pack_metadata", "pa_pack_metadata_mirror", "pa_prefill", "pa_prefill_workspace_size", "pa_qkv_append", "pa_version",
         "pa_zero_blocks",
     ])
 

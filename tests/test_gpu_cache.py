@@ -1,6 +1,7 @@
 """HIP KV append / metadata packing / block zeroing: bit-exact against the oracle and against
 the CPU path of the same cache classes."""
 import math
+import random
 
 import numpy as np
 import pytest
@@ -97,6 +98,74 @@ def test_pack_metadata_bitwise(device):
             p = prev[b] + j
             want[b * T + j] = lists[b][p // bs] * bs + p % bs
     assert np.array_equal(slots.cpu().numpy(), want)
+
+
+def test_pack_metadata_mirror_matches_csr_pack(device):
+    """pa_pack_metadata_mirror over a random sequence of steps (appends, releases, hand edits, row
+    take-over), with the descriptor in pinned host memory the kernel reads directly, against
+    pa_pack_metadata from each step's full CSR lists: page tables, lengths and slots bit-exact, the
+    staged words copied exactly, and the device mirror equal to the host shadow after every step."""
+    from src.kernels.hip_paged_attention import pack_metadata_mirror_hip
+    from src.kernels.staging import MappedHostWords
+    from src.model.graph_decode import _step_metadata_py
+
+    rng = random.Random(17)
+    R, W, bs, T, Bmax = 6, 24, 16, 5, 4
+    mirror = torch.full((R, W), -1, dtype=torch.int32, device=device)
+    shadow, slen = np.full((R, W), -1, np.int32), np.zeros(R, np.int32)
+    stage_words = 3 * Bmax
+    # descriptor: [stage | mrow | first | num pages | prev | app | update ids, W per request]
+    o_cur, o_sel, o_mrow = 0, Bmax, 2 * Bmax
+    o_first, o_npages = 3 * Bmax, 4 * Bmax
+    o_prev, o_app, o_upd = 5 * Bmax, 6 * Bmax, 7 * Bmax
+    desc = MappedHostWords(o_upd + Bmax * W, device)
+    addrs = {"mirror_row": desc.device_addr(o_mrow), "first_page": desc.device_addr(o_first),
+             "num_pages": desc.device_addr(o_npages), "update_ids": desc.device_addr(o_upd), "update_stride": W,
+             "prev_lens": desc.device_addr(o_prev), "append_lens": desc.device_addr(o_app),
+             "stage_src": desc.device_addr(0)}
+    stage = torch.zeros(stage_words, dtype=torch.int32, device=device)
+    lists = {r: [] for r in range(R)}
+    dev = lambda a: torch.from_numpy(np.asarray(a, dtype=np.int32)).to(device)
+    for step in range(60):
+        B = rng.randint(1, Bmax)
+        rows = rng.sample(range(R), B)
+        for r in rows:
+            op = rng.random()
+            if op < 0.7:
+                lists[r] = (lists[r] + [rng.randrange(4000) for _ in range(rng.randint(0, 2))])[:W]
+            elif op < 0.8:
+                lists[r] = []
+            elif op < 0.9 and lists[r]:
+                lists[r][rng.randrange(len(lists[r]))] = rng.randrange(4000)
+            else:
+                slen[r] = 0  # taken over: resent whole
+        states = [PagedKVCacheState(pool=None, block_ids=list(lists[r])) for r in rows]
+        prev = [max(0, len(lists[r]) * bs - rng.randint(0, 20)) for r in rows]
+        app = [min(T, max(0, len(lists[r]) * bs - p)) for r, p in zip(rows, prev)]
+        cur = [rng.randint(0, 9) for _ in rows]
+        sel = [rng.randint(0, 4) for _ in rows]
+        desc.wait()
+        desc.words[:] = -99
+        lay = (o_cur, o_sel, o_mrow, o_first, o_npages, o_prev, o_app, o_upd, W)
+        _step_metadata_py(states, rows, prev, app, cur, sel, shadow, slen, desc.words, lay)
+        # stage region for this B: [cur B | sel B] packed at the front, as a graph step lays it out
+        desc.words[0:B] = cur
+        desc.words[B:2 * B] = sel
+        max_pages = max(len(lists[r]) for r in rows) + 1
+        print(f"mirror pack step {step}: B={B} rows={rows} max_pages={max_pages}", flush=True)
+        pt, s32, s64, slots = pack_metadata_mirror_hip(mirror, addrs, batch=B, query_len=T, block_size=bs,
+                                                       max_pages=max_pages, stage_dst=stage, stage_words=2 * B)
+        desc.mark(torch.cuda.current_stream(device).cuda_stream)
+        want_lists = [lists[r] for r in rows]
+        ids, offs = oracle.csr(want_lists)
+        wpt, w32, w64, wslots = pack_metadata_hip(dev(ids) if len(ids) else dev([0]), dev(offs), dev(prev),
+                                                  dev(app), query_len=T, block_size=bs, max_pages=max_pages)
+        assert torch.equal(pt, wpt) and torch.equal(s32, w32) and torch.equal(s64, w64)
+        assert torch.equal(slots, wslots), step
+        assert stage[:2 * B].cpu().tolist() == cur + sel
+        got = mirror.cpu().numpy()
+        for r in rows:
+            assert got[r, :len(lists[r])].tolist() == lists[r] == shadow[r, :slen[r]].tolist()
 
 
 def test_zero_blocks_and_release(device):
