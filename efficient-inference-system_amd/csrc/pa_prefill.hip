@@ -114,6 +114,18 @@ constexpr int prefill_waves() { return 4; }
 #ifndef PA_PREFILL_DEPTH_BF16_128
 #define PA_PREFILL_DEPTH_BF16_128 2
 #endif
+// KV blocks folded per softmax round. One: folding two blocks per round (interleaved QK^T chains,
+// one max/sum exchange and rescale test per 32 keys) measured slower at head_dim 64 in graph replay
+// on the chunked workload (fp32 KV 18.8 -> 22.1-22.6 us with 218 instead of 129 registers; bf16
+// 11.6 -> 12.0-12.2 us; 8 x 8 heads bf16 15.0 -> 20.2 us), and does not fit two wavefronts per SIMD
+// at head_dim 128. Starting each tile's walk at a tile-dependent rotation, so the tiles of one
+// pair do not request a block at the same moment, changed nothing (18.7-18.8 us).
+template <typename KV, int HD, bool OCC4>
+constexpr int prefill_round() { return 1; }
+
+// Lazy rescaling threshold (log2 units) of the 16-row kernel's running max.
+constexpr float kPrefillRescaleSlack = 8.f;
+
 template <typename KV, int HD>
 constexpr int prefill_depth() {
   return std::is_same<KV, float>::value ? (HD == 64 ? PA_PREFILL_DEPTH_F32_64 : PA_PREFILL_DEPTH_F32_128)
@@ -155,6 +167,17 @@ void prefill_mfma_kernel(const AttnArgs a) {
   const int i0 = qt * 16;
   const int i = i0 + c;
 
+  // The first chunk of this wave's page-table entries (blocks jb0 + w + lane * NW) does not depend
+  // on the request's lengths: load it now, clamped into the row, so it travels with the length
+  // loads instead of after them (one dependent memory round trip less before the first KV tile).
+  // Entries past the tile's blocks are never used.
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+  const int jb0 = a.num_splits > 1 ? split * a.split_blocks : 0;
+  int ids0 = -1;
+  if (a.max_pages > 0) {
+    const int idx = jb0 + w + lane * NW;
+    ids0 = pt[idx < a.max_pages ? idx : a.max_pages - 1];
+  }
   const int L = a.seq_lens[b];
   const int C = a.cur_lens[b];
   const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
@@ -200,7 +223,6 @@ void prefill_mfma_kernel(const AttnArgs a) {
 
   const KV* kpool = static_cast<const KV*>(a.k_pool);
   const KV* vpool = static_cast<const KV*>(a.v_pool);
-  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
 
   // Registers of one KV tile as this lane needs them: K row c, head_dim [G*QD, G*QD + QD), and
   // V rows 4G..4G+3, head_dim [c*DT, c*DT + DT).
@@ -217,44 +239,73 @@ void prefill_mfma_kernel(const AttnArgs a) {
     for (int r = 0; r < 4; ++r) load_words<VW>(vpool + base + (4 * G + r) * HD + c * DT, t.v[r]);
   };
 
-  // Fold one tile (KV block j) into the running state.
-  auto fold = [&](const Tile& tl, int j) {
+  // Fold NV tiles (this wave's blocks k0 .. k0 + NV - 1 of the current chunk) into the running
+  // state with one softmax round: the QK^T chains of the tiles interleave (independent
+  // accumulators), and the row max / sum exchanges and the rescale test are paid once per round.
+  // The running max moves lazily (only when a round's max exceeds it by more than
+  // kPrefillRescaleSlack in log2 units, tested for the whole wavefront), so the output
+  // accumulators are rescaled only in the rounds where it jumps; weights stay <= 2^slack.
+  auto fold_round = [&](const Tile* tr, auto nv_tag, int j0, int jstep) {
+    constexpr int NV = decltype(nv_tag)::value;
     // ---- S^T = K Q^T ------------------------------------------------------------------------
-    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 sacc[NV];
+#pragma unroll
+    for (int q = 0; q < NV; ++q) sacc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (!kBf16) {
 #pragma unroll
-      for (int s = 0; s < QD; ++s)
-        sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(tl.k[s]), qv[s], sacc, 0, 0, 0);
+      for (int s2 = 0; s2 < QD; ++s2)
+#pragma unroll
+        for (int q = 0; q < NV; ++q)
+          sacc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(tr[q].k[s2]), qv[s2], sacc[q], 0, 0, 0);
     } else {
 #pragma unroll
-      for (int s = 0; s < QD / 8; ++s) {
-        const u32x4 x = {tl.k[4 * s], tl.k[4 * s + 1], tl.k[4 * s + 2], tl.k[4 * s + 3]};
-        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x), qb[s], sacc, 0, 0, 0);
-      }
+      for (int s2 = 0; s2 < QD / 8; ++s2)
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+          const u32x4 x = {tr[q].k[4 * s2], tr[q].k[4 * s2 + 1], tr[q].k[4 * s2 + 2], tr[q].k[4 * s2 + 3]};
+          sacc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x), qb[s2], sacc[q], 0, 0, 0);
+        }
     }
-    // ---- online softmax over this block's keys, per query column c ----------------------------
-    float p[4];
+    // ---- online softmax over the round's keys, per query column c ---------------------------
+    // Interior rounds (every block valid, every key below every column's limit) need no mask.
+    bool all_ok = true;
+#pragma unroll
+    for (int q = 0; q < NV; ++q) all_ok = all_ok && tr[q].ok;
+    const int j_last = j0 + (NV - 1) * jstep;
+    const bool full = all_ok && __builtin_amdgcn_ballot_w64(n_c < (j_last + 1) * BS) == 0;
+    if (!full) {
+#pragma unroll
+      for (int q = 0; q < NV; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = (j0 + q * jstep) * BS + 4 * G + r;
+          sacc[q][r] = (tr[q].ok && t < n_c) ? sacc[q][r] : -INFINITY;
+        }
+    }
     float mloc = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = j * BS + 4 * G + r;
-      p[r] = (tl.ok && t < n_c) ? sacc[r] : -INFINITY;
-      mloc = fmaxf(mloc, p[r]);
-    }
+    for (int q = 0; q < NV; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sacc[q][r]);
     mloc = max_xor32(max_xor16(mloc));
-    const float mnew = fmaxf(m, mloc);
-    const float alpha = fast_exp2(m - mnew);
+    const bool grow = mloc > m + kPrefillRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float mnew = grow ? mloc : m;
+      const float alpha = fast_exp2(m - mnew);
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+      m = mnew;
+    }
     float ps = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = fast_exp2(p[r] - mnew);
-      ps += p[r];
-    }
-    ps = sum_xor32(sum_xor16(ps));
-    l = l * alpha + ps;
-    m = mnew;
+    for (int q = 0; q < NV; ++q)
 #pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+      for (int r = 0; r < 4; ++r) {
+        sacc[q][r] = fast_exp2(sacc[q][r] - m);
+        ps += sacc[q][r];
+      }
+    l += sum_xor32(sum_xor16(ps));
     // ---- O^T += V^T P^T -----------------------------------------------------------------------
     // fp32 KV at head_dim 128: the PV MFMAs run at raised wavefront priority, so a wavefront that
     // reaches them issues ahead of co-resident ones still in their softmax (4 requests x 32
@@ -264,56 +315,78 @@ void prefill_mfma_kernel(const AttnArgs a) {
     if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
     if constexpr (!kBf16) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int q = 0; q < NV; ++q)
 #pragma unroll
-        for (int t = 0; t < DT; ++t)
-          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(tl.v[r][t]), p[r], oacc[t], 0, 0, 0);
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int t = 0; t < DT; ++t)
+            oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(tr[q].v[r][t]), sacc[q][r], oacc[t], 0, 0,
+                                                           0);
     } else {
-      const s16x4 pb = {(short)f32_to_bf16(p[0]), (short)f32_to_bf16(p[1]), (short)f32_to_bf16(p[2]),
-                        (short)f32_to_bf16(p[3])};
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const int sh = (t & 1) * 16;
-        const s16x4 av = {(short)(tl.v[0][t >> 1] >> sh), (short)(tl.v[1][t >> 1] >> sh),
-                          (short)(tl.v[2][t >> 1] >> sh), (short)(tl.v[3][t >> 1] >> sh)};
-        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb, oacc[t], 0, 0, 0);
+      for (int q = 0; q < NV; ++q) {
+        const uint32_t p01 = pack_bf16x2(sacc[q][0], sacc[q][1]);
+        const uint32_t p23 = pack_bf16x2(sacc[q][2], sacc[q][3]);
+        const s16x4 pb = {(short)(p01 & 0xffff), (short)(p01 >> 16), (short)(p23 & 0xffff), (short)(p23 >> 16)};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const int sh = (t & 1) * 16;
+          const s16x4 av = {(short)(tr[q].v[0][t >> 1] >> sh), (short)(tr[q].v[1][t >> 1] >> sh),
+                            (short)(tr[q].v[2][t >> 1] >> sh), (short)(tr[q].v[3][t >> 1] >> sh)};
+          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb, oacc[t], 0, 0, 0);
+        }
       }
     }
     if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
   };
 
-  // This wave's blocks j = jb + w + k*NW, k < mine, in chunks of one page-table entry per lane.
-  // D tiles load into a ring of D + 1 register sets while the oldest one is folded; the
-  // steady-state loop issues its loads unconditionally so the compiler's wait counts stay exact,
-  // and the tail is peeled (the prologue's guarded loads also cover walks of at most D tiles).
+  // This wave's blocks j = jb + w + k*NW, k < mine, in chunks of one page-table entry per lane,
+  // folded R blocks per round (the last round of the walk may hold fewer). D rounds load into a
+  // ring of D + 1 register sets while the oldest one is folded; the steady-state loop issues its
+  // loads unconditionally so the compiler's wait counts stay exact, and the tail is peeled.
   const int span = je - jb;
   const int mine = span > w ? (span - w + NW - 1) / NW : 0;
-  constexpr int D = prefill_depth<KV, HD>();  // tiles in flight ahead of the one being folded
-  constexpr int S = D + 1;                // register slots
+  constexpr int R = prefill_round<KV, HD, OCC4>();  // KV blocks per softmax round
+  constexpr int D = prefill_depth<KV, HD>();  // rounds in flight ahead of the one being folded
+  constexpr int S = D + 1;                    // register sets of R tiles
+  static_assert(kWave % R == 0, "a page-table chunk holds whole rounds");
+  using Full = std::integral_constant<int, R>;
+  using One = std::integral_constant<int, 1>;
   for (int c0 = 0; c0 < mine; c0 += kWave) {
     const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
+    const int nr = (cnt + R - 1) / R;
     int ids = -1;
-    if (lane < cnt) ids = pt[jb + w + (c0 + lane) * NW];
-    auto jidx = [&](int k) { return jb + w + (c0 + k) * NW; };
-    auto put = [&](Tile& t, int k) { issue(t, __builtin_amdgcn_readlane(ids, k)); };
-    Tile t[S];
+    if (lane < cnt) ids = c0 == 0 ? ids0 : pt[jb + w + (c0 + lane) * NW];
+    auto put = [&](Tile* tr, int rr) {
 #pragma unroll
-    for (int k = 0; k < D; ++k)
-      if (k < cnt) put(t[k], k);
-    int k = 0;
-    for (; k + D + S - 1 < cnt; k += S) {
+      for (int q = 0; q < R; ++q) {
+        const int k = rr * R + q;
+        issue(tr[q], k < cnt ? __builtin_amdgcn_readlane(ids, k) : -1);
+      }
+    };
+    auto fold = [&](const Tile* tr, int rr) {
+      const int j0 = jb + w + (c0 + rr * R) * NW;
+      if (R == 1 || rr * R + R <= cnt) fold_round(tr, Full{}, j0, NW);
+      else fold_round(tr, One{}, j0, NW);  // the walk's last round holds a single block
+    };
+    Tile t[S][R];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < nr) put(t[d], d);
+    int rr = 0;
+    for (; rr + D + S - 1 < nr; rr += S) {
 #pragma unroll
       for (int u = 0; u < S; ++u) {
-        put(t[(u + D) % S], k + u + D);
-        fold(t[u], jidx(k + u));
+        put(t[(u + D) % S], rr + u + D);
+        fold(t[u], rr + u);
       }
     }
-    // Drain: at most S + D - 1 tiles remain; k % S == 0 here, so tile k + u sits in slot u % S.
+    // Drain: at most S + D - 1 rounds remain; rr % S == 0 here, so round rr + u sits in slot u % S.
 #pragma unroll
     for (int u = 0; u < S + D - 1; ++u) {
-      if (k + u < cnt) {
-        if (k + u + D < cnt) put(t[(u + D) % S], k + u + D);
-        fold(t[u % S], jidx(k + u));
+      if (rr + u < nr) {
+        if (rr + u + D < nr) put(t[(u + D) % S], rr + u + D);
+        fold(t[u % S], rr + u);
       }
     }
   }

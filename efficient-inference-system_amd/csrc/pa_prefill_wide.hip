@@ -35,12 +35,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// Two fp32 values to packed bf16 (round to nearest even) with gfx950's v_cvt_pk_bf16_f32.
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
 // Lazy rescaling threshold (log2 units): the running max only moves when a step's max exceeds it
 // by more than this, so softmax weights stay <= 2^8 and the accumulators are rescaled only in
 // the few steps where the max jumps.
