@@ -13,6 +13,10 @@
 //                                                       before the append
 //   csr(states, prev, app) -> (bytearray, max_pages)    BatchedPagedKVCache.csr_buffer: int32
 //                                                       [offsets B+1 | prev B | app B | block ids]
+//   check_tokens(ids, positions, T, vocab, max_pos)     TinyTransformerLM.check_token_inputs for
+//                                                       host data: IndexError where the eager
+//                                                       embedding lookups would raise
+//   max_blocks(states) -> int                           the longest block list of a batch
 //   step_metadata(states, rows, prev, app, cur, sel, shadow, shadow_len, desc, layout)
 //                                              -> (updates, max_pages)
 //                                                       graph_decode._step_metadata_py: the int32
@@ -441,10 +445,83 @@ PyObject* step_metadata(PyObject*, PyObject* args) {
   return Py_BuildValue("(nn)", n_upd, max_pages);
 }
 
+// Smallest and largest value of an int64 host array (buffer of 8-byte items) or of a (nested)
+// sequence of ints; count 0 leaves lo/hi untouched.
+bool int_range(PyObject* o, long long* lo, long long* hi, Py_ssize_t* count) {
+  if (PyLong_Check(o)) {
+    const long long v = PyLong_AsLongLong(o);
+    if (v == -1 && PyErr_Occurred()) return false;
+    *lo = *count ? (v < *lo ? v : *lo) : v;
+    *hi = *count ? (v > *hi ? v : *hi) : v;
+    ++*count;
+    return true;
+  }
+  if (PyObject_CheckBuffer(o)) {
+    Py_buffer v;
+    if (PyObject_GetBuffer(o, &v, PyBUF_C_CONTIGUOUS | PyBUF_FORMAT) < 0) return false;
+    const bool i64 = v.itemsize == 8 && v.format != nullptr && (v.format[0] == 'q' || v.format[0] == 'l' ||
+                                                                 ((v.format[0] == '<' || v.format[0] == '=') &&
+                                                                  (v.format[1] == 'q' || v.format[1] == 'l')));
+    if (!i64) {
+      PyBuffer_Release(&v);
+      PyErr_SetString(PyExc_TypeError, "token ids and positions must be int64 arrays or ints");
+      return false;
+    }
+    const long long* d = static_cast<const long long*>(v.buf);
+    const Py_ssize_t n = v.len / 8;
+    for (Py_ssize_t i = 0; i < n; ++i) {
+      *lo = *count ? (d[i] < *lo ? d[i] : *lo) : d[i];
+      *hi = *count ? (d[i] > *hi ? d[i] : *hi) : d[i];
+      ++*count;
+    }
+    PyBuffer_Release(&v);
+    return true;
+  }
+  Ref seq(PySequence_Fast(o, "token ids and positions must be int64 arrays, sequences or ints"));
+  if (!seq) return false;
+  const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq.get());
+  for (Py_ssize_t i = 0; i < n; ++i)
+    if (!int_range(PySequence_Fast_GET_ITEM(seq.get(), i), lo, hi, count)) return false;
+  return true;
+}
+
+PyObject* check_tokens(PyObject*, PyObject* args) {
+  PyObject *ids, *pos;
+  long long T, V, P;
+  if (!PyArg_ParseTuple(args, "OOLLL", &ids, &pos, &T, &V, &P)) return nullptr;
+  long long lo = 0, hi = 0, plo = 0, phi = 0;
+  Py_ssize_t n = 0, np_ = 0;
+  if (!int_range(ids, &lo, &hi, &n) || !int_range(pos, &plo, &phi, &np_)) return nullptr;
+  if (n && (lo < 0 || hi >= V)) {
+    PyErr_Format(PyExc_IndexError, "token id out of range [0, %lld): min %lld, max %lld", V, lo, hi);
+    return nullptr;
+  }
+  if (np_ && T > 0 && (plo < 0 || phi + T - 1 >= P)) {
+    PyErr_Format(PyExc_IndexError, "positions %lld..%lld outside the position table [0, %lld)", plo, phi + T - 1, P);
+    return nullptr;
+  }
+  Py_RETURN_NONE;
+}
+
+PyObject* max_blocks(PyObject*, PyObject* states_in) {
+  Ref states(PySequence_Fast(states_in, "states must be a sequence"));
+  if (!states) return nullptr;
+  Py_ssize_t best = 0;
+  const Py_ssize_t B = PySequence_Fast_GET_SIZE(states.get());
+  for (Py_ssize_t b = 0; b < B; ++b) {
+    Ref ids(list_attr(PySequence_Fast_GET_ITEM(states.get(), b), N.block_ids));
+    if (!ids) return nullptr;
+    best = PyList_GET_SIZE(ids.get()) > best ? PyList_GET_SIZE(ids.get()) : best;
+  }
+  return PyLong_FromSsize_t(best);
+}
+
 PyMethodDef methods[] = {
     {"lockstep", lockstep, METH_VARARGS, "Whether every layer's cache holds the same states and free-list tail."},
     {"host_append", host_append, METH_VARARGS, "Per-layer append bookkeeping; returns the first cache's lengths."},
     {"csr", csr, METH_VARARGS, "int32 CSR metadata buffer of a batch's block lists, and its max pages."},
+    {"check_tokens", check_tokens, METH_VARARGS, "IndexError for token ids or positions the embeddings do not hold."},
+    {"max_blocks", max_blocks, METH_O, "Length of the longest block list of a batch's states."},
     {"step_metadata", step_metadata, METH_VARARGS,
      "int32 part of a graph step's descriptor: block-list updates against the device mirror's shadow."},
     {nullptr, nullptr, 0, nullptr},

@@ -40,6 +40,10 @@ class KVStorage:
     fixed while the pool grows and across pools that reuse it (a model keeps one per layer).
     Holds `blocks` physical blocks; replaced by a larger allocation only when a pool outgrows it."""
 
+    # Bumped by every (re)allocation of any storage: a step captured against storages whose
+    # addresses it recorded stays valid while this count is unchanged.
+    allocations = 0
+
     def __init__(self, reserve_blocks: int):
         self.reserve_blocks = reserve_blocks
         self.k: torch.Tensor | None = None
@@ -67,6 +71,7 @@ class KVStorage:
             new_k[:keep].copy_(self.k[:keep])
             new_v[:keep].copy_(self.v[:keep])
         self.k, self.v = new_k, new_v
+        KVStorage.allocations += 1
 
 
 class LayerBlockPool:

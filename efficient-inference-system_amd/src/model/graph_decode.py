@@ -55,7 +55,7 @@ import weakref
 import numpy as np
 import torch
 
-from src.cache.paged_kv import BatchedPagedKVCache
+from src.cache.paged_kv import BatchedPagedKVCache, KVStorage
 from src.kernels import _lib, hip_linear
 from src.kernels.hip_paged_attention import (
     _stream_ptr, _workspace, argmax_rows_hip, default_prefill_split_blocks, default_split_blocks, kv_append_hip,
@@ -112,6 +112,11 @@ def _pool_tensors(pool):
 
 
 def _signature(pools) -> tuple:
+    """What a captured step's recorded pool addresses depend on: for storage-backed pools, the
+    storages and their allocation count (a view that grows inside its storage keeps its address);
+    otherwise every pool tensor's address, length and dtype."""
+    if all(p.storage is not None and p.storage.k is not None for p in pools):
+        return ("storage", KVStorage.allocations) + tuple(id(p.storage) for p in pools)
     sig = []
     for p in pools:
         k, v = _pool_tensors(p)
@@ -316,6 +321,9 @@ class GraphedStep:
         self.captures = 0
         self._attns = None
         self.mirror: _BlockTableMirror | None = None
+        # the embedding weight, read per call only for its device (a Parameter keeps its identity
+        # across .to() and load_state_dict)
+        self._weight = model.token_emb.weight
 
     def usable(self, input_ids, kv_caches) -> bool:
         """Whether a step over input_ids ([B, T], device tensor or host data) and these per-layer
@@ -324,7 +332,7 @@ class GraphedStep:
         m = self.model
         if self._attns is None or len(self._attns) != len(m.blocks):
             self._attns = [b.attn for b in m.blocks]  # plain attribute reads below, per call
-        if not (graphs_enabled() and m.token_emb.weight.is_cuda and len(input_ids.shape) == 2 and not m.training
+        if not (self._weight.is_cuda and graphs_enabled() and len(input_ids.shape) == 2 and not m.training
                 and m.attention_backend == "hip_paged"
                 and all(a.attention_backend == "hip_paged" for a in self._attns)
                 and isinstance(kv_caches, list) and len(kv_caches) == len(self._attns)
@@ -455,7 +463,7 @@ class GraphedStep:
         m = self.model
         B, T = input_ids.shape
         Tb = bucket_for(T)
-        device = m.token_emb.weight.device
+        device = self._weight.device
         pools = [c.pool for c in kv_caches]
         app = [max(min(c, T), 0) for c in current_lengths]
         if _host is not None:
@@ -466,7 +474,8 @@ class GraphedStep:
                 p = cache.host_append(app, T, m.num_heads, m.head_dim, pools[0].dtype, device)
                 prev = p if prev is None else prev
         states0 = kv_caches[0].states
-        max_pages = max((len(st.block_ids) for st in states0), default=0)
+        max_pages = _host.max_blocks(states0) if _host is not None else \
+            max((len(st.block_ids) for st in states0), default=0)
         pages = max(-(-m.max_seq_len // m.kv_block_size), max_pages)
         mirror = self._mirror_for(B, pages, device)
         sig = _signature(pools)

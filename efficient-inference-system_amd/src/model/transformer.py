@@ -12,6 +12,11 @@ import torch
 import torch.nn as nn
 
 from src.cache.paged_kv import BatchedPagedKVCache, KVStorage, LayerBlockPool, PagedKVCacheState
+
+try:  # native host checks (csrc/host/paged_host.cpp); the Python versions below run without it
+    from src.cache import _paged_host as _host
+except ImportError:
+    _host = None
 from src.config import ATTENTION_BACKENDS
 from src.model.attention import CausalSelfAttention
 
@@ -186,6 +191,12 @@ class TinyTransformerLM(nn.Module):
         device tensors cost one device->host read."""
         dev_ids = isinstance(input_ids, torch.Tensor) and input_ids.is_cuda
         dev_pos = isinstance(positions, torch.Tensor) and positions.is_cuda
+        if _host is not None and not isinstance(input_ids, torch.Tensor) and not isinstance(positions, torch.Tensor):
+            try:  # int64 arrays, sequences and ints: one native pass
+                _host.check_tokens(input_ids, positions, T, self.vocab_size, self.max_seq_len)
+                return
+            except TypeError:
+                pass  # other element types: the general path below
         if dev_ids or dev_pos:
             parts = ([input_ids.min(), input_ids.max()] if dev_ids and input_ids.numel() else []) + \
                     ([positions.min(), positions.max()] if dev_pos and positions.numel() else [])
@@ -194,7 +205,7 @@ class TinyTransformerLM(nn.Module):
             lo_id, hi_id = (vals[0], vals[1]) if input_ids.numel() else (0, 0)
             vals = vals[2:] if input_ids.numel() else vals
         else:
-            ids = input_ids.numpy() if isinstance(input_ids, torch.Tensor) else input_ids
+            ids = input_ids.numpy() if isinstance(input_ids, torch.Tensor) else np.asarray(input_ids)
             lo_id, hi_id = (int(ids.min()), int(ids.max())) if ids.size else (0, 0)
         if isinstance(positions, int):
             lo_pos = hi_pos = positions
@@ -259,14 +270,13 @@ class TinyTransformerLM(nn.Module):
         if len(rows) != B or any(not -T <= r < T for r in rows):
             raise IndexError(f"select_rows {rows} out of range for {B} requests of {T} rows")
         rows = [r % T for r in rows]
+        runner = self._graph_runner()
+        if kv_caches is not None and runner.usable(input_ids, kv_caches):
+            ids_h, pos_h = self._host_step_inputs(input_ids, position_offset)
+            self.check_token_inputs(ids_h, pos_h, T)
+            logits, tokens = runner(ids_h, pos_h, cur, kv_caches, rows=rows, want_logits=return_logits)
+            return tokens, logits, list(kv_caches)
         device = self.token_emb.weight.device
-        if kv_caches is not None and device.type == "cuda":
-            runner = self._graph_runner()
-            if runner.usable(input_ids, kv_caches):
-                ids_h, pos_h = self._host_step_inputs(input_ids, position_offset)
-                self.check_token_inputs(ids_h, pos_h, T)
-                logits, tokens = runner(ids_h, pos_h, cur, kv_caches, rows=rows, want_logits=return_logits)
-                return tokens, logits, list(kv_caches)
         if device.type == "cuda":
             self.check_token_inputs(input_ids, position_offset, T)
         ids = torch.as_tensor(input_ids, dtype=torch.long).to(device)

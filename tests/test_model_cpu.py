@@ -88,3 +88,31 @@ def test_state_dict_names_match_reference_layout():
                  "lm_head.weight"):
         assert name in keys
     assert "lm_head.bias" not in keys
+
+
+@pytest.mark.parametrize("native", [True, False])
+def test_token_and_position_checks(native, monkeypatch):
+    """check_token_inputs raises IndexError exactly where the eager embedding lookups would, for
+    the native host check and the Python one."""
+    import numpy as np
+
+    import src.model.transformer as tr
+
+    if not native:
+        monkeypatch.setattr(tr, "_host", None)
+    elif tr._host is None:
+        pytest.skip("native host module not built")
+    model = build_tiny_model("paged_reference", "cpu")  # vocab 128, max_seq_len 128
+    ok_ids = np.array([[0, 127], [5, 6]], dtype=np.int64)
+    model.check_token_inputs(ok_ids, 0, 2)
+    model.check_token_inputs(ok_ids, [0, 126], 2)
+    model.check_token_inputs([[1], [2]], [10, 127], 1)
+    model.check_token_inputs(np.array([[3]], dtype=np.int32), np.array([5], dtype=np.int32), 1)
+    for ids, pos, T in ((np.array([[128]]), 0, 1), ([[-1]], 0, 1), (ok_ids, [0, 127], 2), (ok_ids, -1, 2),
+                        ([[1]], np.array([128], dtype=np.int64), 1)):
+        with pytest.raises(IndexError):
+            model.check_token_inputs(ids, pos, T)
+        with pytest.raises(IndexError):  # eager lookups agree
+            ids_t = torch.as_tensor(np.asarray(ids), dtype=torch.long)
+            p = torch.as_tensor(np.asarray(pos), dtype=torch.long).view(-1, 1) + torch.arange(T).view(1, T)
+            model.token_emb(ids_t) + model.pos_emb(p.expand(ids_t.shape[0], T))
