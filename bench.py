@@ -32,7 +32,9 @@ Also reported on the same line:
                  arriving at once (the serving path's capacity at max batch 8), GPU only.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-e2e]
                        [--no-secondary] [--no-decode] [--calibrate-copy] [--e2e-model fp32|bf16|both]
-(--no-decode skips the headline decode measurement; it is for profiling the other workloads alone.)
+                       [--only GROUP[,GROUP...]]
+(--no-decode skips the headline decode measurement and --only restricts the secondary workloads to
+the named groups; both are for profiling one workload alone.)
 """
 from __future__ import annotations
 
@@ -349,16 +351,31 @@ def time_graph_call(fn, calls: int = 20, replays: int = 5) -> float:
     return e0.elapsed_time(e1) / (replays * calls)
 
 
-def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
+SECONDARY = ("single_decode", "ragged_decode", "chunked_prefill", "large_prefill", "mid_prefill")
+
+
+def secondary_workloads(device, steps: int, with_cpu: bool = True, only=SECONDARY) -> dict:
     """Single decode, ragged fp32 decode (8 requests x 6 layers), chunked prefill (fp32 and bf16
-    KV) and large prefill; with `with_cpu`, the same-run CPU timings of the first three."""
-    import torch
-
-    from src import workloads
-    from src.kernels.hip_paged_attention import (
-        kv_append_hip, pack_metadata_hip, paged_attention_decode_hip, paged_attention_prefill_hip)
-
+    KV), large and mid-size prefill (the groups named in `only`); with `with_cpu`, the same-run CPU
+    timings of the first three."""
     res = {}
+    if "single_decode" in only:
+        _single_decode(res, device, steps, with_cpu)
+    if "ragged_decode" in only:
+        _ragged_decode(res, device, steps, with_cpu)
+    if "chunked_prefill" in only:
+        _chunked_prefill(res, device, steps, with_cpu)
+    if "large_prefill" in only:
+        _large_prefill(res, device, steps)
+    if "mid_prefill" in only:
+        _mid_prefill(res, device, steps)
+    return res
+
+
+def _single_decode(res, device, steps, with_cpu):
+    from src import workloads
+    from src.kernels.hip_paged_attention import paged_attention_decode_hip
+
     b = workloads.single_decode(seed=0, device=device)
     call = lambda: paged_attention_decode_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
     ms = time_call(call, steps)
@@ -374,6 +391,12 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
         log("CPU timings: single decode")
         res["single_decode_fp32"]["cpu"] = cpu_call_times(b.q, b.k_pool, b.v_pool, b.block_lists, b.seq_lens,
                                                           b.cur_lens)
+
+
+def _ragged_decode(res, device, steps, with_cpu):
+    from src import workloads
+    from src.kernels.hip_paged_attention import paged_attention_decode_hip
+
     per_layer, cpu_layers = [], []
     for layer in range(6):
         b = workloads.ragged_decode(seed=0, layer=layer, device=device)
@@ -401,6 +424,14 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
             "reference_loop_sample": "every layer's whole call",
             "threads": cpu_layers[0]["threads"],
         }
+
+
+def _chunked_prefill(res, device, steps, with_cpu):
+    import torch
+
+    from src import workloads
+    from src.kernels.hip_paged_attention import kv_append_hip, pack_metadata_hip, paged_attention_prefill_hip
+
     for kv_dtype, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16kv")):
         w = workloads.chunked_prefill(seed=0, device=device, kv_dtype=kv_dtype)
         B = len(w["prev_lens"])
@@ -416,7 +447,9 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
                                               query_len=T, block_size=16, max_pages=max_pages)
         cur = i32(w["chunk_lens"])
         append_ms = time_call(lambda: kv_append_hip(w["k_new"], w["v_new"], w["k_pool"], w["v_pool"], slots), steps)
-        attn_ms = time_call(lambda: paged_attention_prefill_hip(w["q"], w["k_pool"], w["v_pool"], pt, s32, cur), steps)
+        attn = lambda: paged_attention_prefill_hip(w["q"], w["k_pool"], w["v_pool"], pt, s32, cur)
+        attn_ms = time_call(attn, steps)
+        graph_ms = time_graph_call(attn)
         cold_ms = time_cold_prefill(w["q"], w["k_pool"], w["v_pool"], pt, s32, cur, copies=64)
         flops = workloads.prefill_flops(w["prev_lens"], w["chunk_lens"], 8, 64)
         peak = 157.3 if tag == "fp32" else 2500.0
@@ -425,19 +458,31 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
             "workload": f"4 requests, 8 heads x 64, context {w['prev_lens']} + chunk {w['chunk_lens']}, "
                         f"{'fp32' if tag == 'fp32' else 'bf16'} KV",
             "attention_us": round(1e3 * attn_ms, 2), "append_us": round(1e3 * append_ms, 2),
-            "attention_us_cold": round(1e3 * cold_ms, 2),
-            "timing": "attention_us: the same call repeated (its ~12 MB of KV stay in L2/MALL, as right after "
-                      "the chunk's append in a serving step); attention_us_cold: the call over 64 disjoint "
-                      "copies of its blocks in one graph (~0.4-0.75 GB, beyond the 256 MB MALL)",
+            "attention_us_graph": round(1e3 * graph_ms, 2), "attention_us_cold": round(1e3 * cold_ms, 2),
+            "timing": "attention_us: the same call repeated eagerly through the Python wrapper (its ~12 MB of KV "
+                      "stay in L2/MALL, as right after the chunk's append in a serving step); attention_us_graph: "
+                      "the same call replayed 20 times from a HIP graph (no launch cost between calls, the way "
+                      "serving steps run it); attention_us_cold: the call over 64 disjoint copies of its blocks "
+                      "in one graph (~0.4-0.75 GB, beyond the 256 MB MALL)",
             "useful_gflop": round(flops / 1e9, 4), "TFLOPs": round(tfs, 2),
+            "TFLOPs_graph": round(flops / (graph_ms * 1e-3) / 1e12, 2),
             "TFLOPs_cold": round(flops / (cold_ms * 1e-3) / 1e12, 2),
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
+            "mfma_frac_graph": round(flops / (graph_ms * 1e-3) / 1e12 / peak, 4),
         }
         if with_cpu:  # the pools already hold the appended chunks
             log(f"CPU timings: chunked prefill ({tag})")
             res[f"chunked_prefill_{tag}"]["cpu"] = cpu_call_times(
                 w["q"], w["k_pool"], w["v_pool"], lists, w["seq_lens"], w["chunk_lens"], loop_request=0)
         del w
+
+
+def _large_prefill(res, device, steps):
+    import torch
+
+    from src import workloads
+    from src.kernels.hip_paged_attention import paged_attention_prefill_hip
+
     for kv_dtype, tag in ((torch.bfloat16, "bf16kv"), (torch.float32, "fp32")):
         b = workloads.large_prefill(seed=0, device=device, kv_dtype=kv_dtype)
         H, Hd = b.q.shape[1], b.q.shape[3]
@@ -455,6 +500,14 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
         }
         del b
         torch.cuda.empty_cache()
+
+
+def _mid_prefill(res, device, steps):
+    import torch
+
+    from src import workloads
+    from src.kernels.hip_paged_attention import paged_attention_prefill_hip
+
     # A mid-size prefill: 4 x 32 heads x 128 with 256-token chunks is one 128-row unit per CU, where
     # the dispatch takes the wide kernel for bf16 KV; the 16-row kernel is timed beside it.
     b = workloads.large_prefill(seed=0, device=device, batch=4, chunk=256, ctx_lo=512, ctx_hi=1536)
@@ -485,7 +538,6 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True) -> dict:
     }
     del b
     torch.cuda.empty_cache()
-    return res
 
 
 def calibration_copy(device, nbytes: int = 1 << 32) -> None:
@@ -603,10 +655,17 @@ def main() -> int:
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the headline decode (profiling runs)")
+    ap.add_argument("--only", default=",".join(SECONDARY),
+                    help="comma-separated secondary workload groups to run: " + ", ".join(SECONDARY))
     ap.add_argument("--calibrate-copy", action="store_true", help="also run a copy kernel of known size")
     ap.add_argument("--e2e-model", choices=("fp32", "bf16", "both"), default="both",
                     help="end-to-end runs: the fp32 model (with its CPU baseline), the bf16 model, or both")
     args = ap.parse_args()
+    only = tuple(x for x in args.only.split(",") if x)
+    unknown = sorted(set(only) - set(SECONDARY))
+    if unknown:
+        print(f"bench.py: unknown --only groups {unknown}; choose from {', '.join(SECONDARY)}", file=sys.stderr)
+        return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -672,7 +731,7 @@ def main() -> int:
         calibration_copy(dev)
     if not args.no_secondary:
         log("secondary workloads (single and ragged fp32 decode, chunked, large and mid-size prefill)")
-        result["secondary"] = secondary_workloads(dev, args.steps, with_cpu=not args.no_cpu_baseline)
+        result["secondary"] = secondary_workloads(dev, args.steps, with_cpu=not args.no_cpu_baseline, only=only)
     if not args.no_e2e:
         if args.e2e_model in ("fp32", "both"):
             log("end-to-end continuous batching (200 requests, 32 req/s)")
