@@ -57,7 +57,18 @@ struct LinArgs {
   int32_t H, Hd, bs;
   int32_t bf16;       // T = bf16 (else fp32)
   int32_t cw_log2;    // output columns per workgroup: 1 << cw_log2 (4, 8 or 16)
+  const int32_t* row_sel;  // when set: row m of the product is x row m * sel_group + row_sel[m]
+  int32_t sel_group;       // (a negative entry counts from the group's end; clamped into the group)
 };
+
+// The x row that product row m reads.
+__device__ __forceinline__ int64_t lin_x_row(const LinArgs& a, int m) {
+  if (a.row_sel == nullptr) return m;
+  int r = a.row_sel[m];
+  if (r < 0) r += a.sel_group;
+  r = r < 0 ? 0 : (r >= a.sel_group ? a.sel_group - 1 : r);
+  return (int64_t)m * a.sel_group + r;
+}
 
 // Wavefronts per workgroup (they split K): 16 at K = 2048 keeps more of the 128 KB weight tile in
 // flight per compute unit (fc2 of the benchmark model, 8 rows: 9.3 -> 8.2 us inside a graph).
@@ -135,7 +146,7 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   {
     const int n = n0 + c < a.seg_n ? n0 + c : a.seg_n - 1;  // clamp: the column is discarded
     load_words(wv, W + (int64_t)n * a.K + kb, c < cw);
-    load_words(xv, static_cast<const T*>(a.x) + (int64_t)(row_ok ? r0 + c : 0) * a.x_stride + kb, row_ok);
+    load_words(xv, static_cast<const T*>(a.x) + (row_ok ? lin_x_row(a, r0 + c) : 0) * a.x_stride + kb, row_ok);
     if constexpr (PRE) {
       load_words(lgv, static_cast<const T*>(a.ln_w) + kb, true);
       load_words(lbv, static_cast<const T*>(a.ln_b) + kb, true);
@@ -374,6 +385,34 @@ extern "C" int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int
   a.w[0] = weight; a.b[0] = bias; a.seg_n = out_features; a.nseg = 1;
   a.act = activation; a.res = residual; a.res_stride = residual_stride;
   a.out = out; a.out_stride = out_stride; a.bf16 = dtype == PA_DTYPE_BF16;
+  return launch_small_linear(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t groups, int32_t group_rows,
+                                     const int32_t* row_index, int32_t in_features, const void* weight,
+                                     const void* bias, int32_t out_features, const void* ln_weight,
+                                     const void* ln_bias, float ln_eps, int32_t activation, void* out,
+                                     int64_t out_stride, int dtype, void* stream) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(groups >= 0 && groups <= kLinMaxRows, "groups must be in [0, %d], got %d", kLinMaxRows, groups);
+  PA_CHECK_ARG(group_rows > 0, "group_rows must be positive, got %d", group_rows);
+  PA_CHECK_ARG(out_features > 0 && in_features > 0, "bad sizes: in=%d out=%d", in_features, out_features);
+  PA_CHECK_ARG(activation == 0 || activation == 1, "bad activation %d", activation);
+  PA_CHECK_ARG(lin_dtype_ok(dtype), "bad dtype %d", dtype);
+  if (groups == 0) return PA_OK;
+  PA_CHECK_ARG(x && weight && out && row_index, "null x/weight/out/row_index");
+  PA_CHECK_ARG((ln_weight == nullptr) == (ln_bias == nullptr), "LayerNorm needs both weight and bias");
+  const int vec = elems_per_16b(dtype);
+  PA_CHECK_ARG(aligned16(x) && aligned16(weight) && x_stride % vec == 0 && (!ln_weight || (aligned16(ln_weight) &&
+               aligned16(ln_bias))), "x, weight and LayerNorm parameters must be 16-byte aligned, x_stride a multiple of %d", vec);
+  PA_CHECK_ARG(x_stride >= in_features && out_stride >= out_features, "row strides smaller than the rows");
+  LinArgs a{};
+  a.x = x; a.x_stride = x_stride; a.M = groups; a.K = in_features;
+  a.ln_w = ln_weight; a.ln_b = ln_bias; a.ln_eps = ln_eps;
+  a.w[0] = weight; a.b[0] = bias; a.seg_n = out_features; a.nseg = 1;
+  a.act = activation; a.res = nullptr; a.res_stride = 0;
+  a.out = out; a.out_stride = out_stride; a.bf16 = dtype == PA_DTYPE_BF16;
+  a.row_sel = row_index; a.sel_group = group_rows;
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
 }
 

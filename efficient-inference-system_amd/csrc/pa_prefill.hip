@@ -120,6 +120,17 @@ constexpr int prefill_waves() { return 4; }
 // 11.6 -> 12.0-12.2 us; 8 x 8 heads bf16 15.0 -> 20.2 us), and does not fit two wavefronts per SIMD
 // at head_dim 128. Starting each tile's walk at a tile-dependent rotation, so the tiles of one
 // pair do not request a block at the same moment, changed nothing (18.7-18.8 us).
+// Also measured on the chunked workload (graph replay, three interleaved runs, one box) and not
+// kept: software-pipelining the walk so that block k+1's QK^T MFMAs overlap block k's softmax
+// (three-tile ring, with or without branch-free masking and rescaling): fp32 KV 18.5 -> 19.4-20.5
+// us, bf16 11.5 -> 11.9-12.2 us; two or four independent QK^T accumulators instead of one chain:
+// fp32 18.4 -> 19.0-19.3 us; 8-wavefront workgroups that own a heavy and a light tile and deal the
+// union of their blocks to all 8 wavefronts (every wavefront within one block of the mean, no
+// wavefront alone on its SIMD): fp32 18.4 -> 21.4 us, bf16 11.5 -> 13.4 us. A per-wavefront trace
+// of the last one showed why: a SIMD finishes the same number of blocks at the same time either
+// way (a heavy tile's wavefront left alone on its SIMD runs about a third faster per block), while
+// loading both units' queries and merging 8 partial states per unit lengthen the prologue (1.1 ->
+// 1.9 us) and the epilogue.
 template <typename KV, int HD, bool OCC4>
 constexpr int prefill_round() { return 1; }
 

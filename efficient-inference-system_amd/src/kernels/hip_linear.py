@@ -1,6 +1,8 @@
 """torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32 or bf16, <= 1024 rows).
 
   linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
+  linear_select_rows_hip  the same without residual for one selected row per group of rows
+                   (a step's greedy rows)                                    (pa_linear_select_rows)
   qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
                    one launch; returns q                                     (pa_qkv_append)
   embed_rows_hip   token + clamped position embedding of a [B, T] step       (pa_embed_rows)
@@ -79,6 +81,42 @@ def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | No
         out.data_ptr(), out.stride(0), _lib.dtype_code(dt), _stream(x.device),
     )
     _lib.check(status, "pa_linear_rows")
+    return out
+
+
+def linear_select_rows_hip(x: torch.Tensor, group_rows: int, row_index: torch.Tensor, linear: nn.Linear, *,
+                           ln: nn.LayerNorm | None = None, gelu: bool = False,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[g] = act(LN(x[g * group_rows + r_g]) W^T + b) with r_g = row_index[g] (negative values
+    count from the group's end; clamped into the group), for the len(row_index) groups of rows of
+    x; x, the layer's parameters and out share one dtype (float32 or bfloat16)."""
+    _rows(x, "x")
+    dt = x.dtype
+    M, K = x.shape
+    if K != linear.in_features:
+        raise ValueError(f"x has {K} features, the layer takes {linear.in_features}")
+    if (row_index.dtype != torch.int32 or row_index.dim() != 1 or not row_index.is_contiguous()
+            or row_index.device != x.device):
+        raise ValueError("row_index must be a contiguous 1-d int32 tensor on x's device")
+    groups = row_index.numel()
+    if group_rows <= 0 or groups * group_rows > M:
+        raise ValueError(f"{groups} groups of {group_rows} rows do not fit in x's {M} rows")
+    _same_dtype(dt, linear.weight, linear.bias, ln.weight if ln is not None else None,
+                ln.bias if ln is not None else None)
+    N = linear.out_features
+    if out is None:
+        out = torch.empty((groups, N), dtype=dt, device=x.device)
+    _rows(out, "out", dt)
+    if out.shape[0] < groups or out.shape[1] != N:
+        raise ValueError(f"out must hold {groups} rows of {N} features")
+    status = _lib.load().pa_linear_select_rows(
+        x.data_ptr(), x.stride(0), groups, group_rows, row_index.data_ptr(), K,
+        linear.weight.data_ptr(), _ptr(linear.bias), N,
+        _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
+        float(ln.eps) if ln is not None else 0.0,
+        1 if gelu else 0, out.data_ptr(), out.stride(0), _lib.dtype_code(dt), _stream(x.device),
+    )
+    _lib.check(status, "pa_linear_select_rows")
     return out
 
 

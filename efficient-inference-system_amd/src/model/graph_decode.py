@@ -261,7 +261,8 @@ class _BlockTableMirror:
 
 
 class _Captured:
-    def __init__(self, model, B: int, Tb: int, pages: int, device: torch.device, pools, mirror_width: int):
+    def __init__(self, model, B: int, Tb: int, pages: int, device: torch.device, pools, mirror_width: int,
+                 tokens_only: bool = False):
         H, Hd = model.num_heads, model.head_dim
         self.B, self.Tb, self.pages = B, Tb, pages
         # Step descriptor (int32 words of pinned host memory the device reads):
@@ -309,6 +310,9 @@ class _Captured:
         self.embed_fused = (fused_decode_enabled() and emb_dt in hip_linear.DTYPES
                             and model.pos_emb.weight.dtype == emb_dt
                             and model.token_emb.embedding_dim % (4 if emb_dt == torch.float32 else 8) == 0)
+        # A graph whose callers take only the tokens computes ln_f + lm_head for each request's
+        # greedy row alone (the other rows' logits are never read).
+        self.select_head = tokens_only and hip_linear.model_supported(model)
         self.signature = _signature(pools)
         self.graph = None
         self.logits = None
@@ -317,7 +321,7 @@ class _Captured:
 class GraphedStep:
     def __init__(self, model):
         self.model = model
-        self.captured: dict[tuple[int, int], _Captured] = {}
+        self.captured: dict[tuple[int, int, bool], _Captured] = {}
         self.captures = 0
         self._attns = None
         self.mirror: _BlockTableMirror | None = None
@@ -361,9 +365,18 @@ class GraphedStep:
             positions = torch.clamp(cap.pos.view(B, 1) + steps, max=m.max_seq_len - 1)
             x = m.token_emb(cap.ids) + m.pos_emb(positions)
         if cap.fused:
-            logits = self._fused_layers(cap, pools, x.view(B * Tb, -1), pt, seq32, slots)
+            x = self._fused_layers(cap, pools, x.view(B * Tb, -1), pt, seq32, slots)
         else:
-            logits = self._torch_layers(cap, pools, x, pt, seq32, slots)
+            x = self._torch_layers(cap, pools, x, pt, seq32, slots).reshape(B * Tb, -1)
+        if cap.select_head:
+            logits = hip_linear.linear_select_rows_hip(x, Tb, cap.rows, m.lm_head, ln=m.ln_f)
+            argmax_rows_hip(logits.view(B, 1, -1), None, out=cap.tokens)
+            return logits
+        if cap.fused and B * Tb <= FUSED_ROWS[x.dtype]["lm_head"]:
+            logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
+        else:
+            logits = m.lm_head(m.ln_f(x))
+        logits = logits.view(B, Tb, -1)
         argmax_rows_hip(logits, cap.rows, out=cap.tokens)
         return logits
 
@@ -385,7 +398,7 @@ class GraphedStep:
                                                 split_blocks=cap.split_blocks)
             x = x + a.out_proj(a.merge_heads(o))
             x = x + blk.mlp(blk.ln2(x))
-        return m.lm_head(m.ln_f(x))
+        return x
 
     def _fused_layers(self, cap: _Captured, pools, x, pt, seq32, slots) -> torch.Tensor:
         """The layers of a step through the fused kernels; x is [B * Tb, d_model] with at most
@@ -394,7 +407,7 @@ class GraphedStep:
         B, Tb = cap.B, cap.Tb
         lim = FUSED_ROWS[x.dtype]
         rows = B * Tb
-        fc1_fused, fc2_fused, head_fused = rows <= lim["fc1"], rows <= lim["fc2"], rows <= lim["lm_head"]
+        fc1_fused, fc2_fused = rows <= lim["fc1"], rows <= lim["fc2"]
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
@@ -413,11 +426,7 @@ class GraphedStep:
                 x = hip_linear.linear_rows_hip(h, blk.mlp[2], residual=x1)
             else:
                 x = blk.mlp[2](h) + x1
-        if head_fused:
-            logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
-        else:
-            logits = m.lm_head(m.ln_f(x))
-        return logits.view(B, Tb, -1)
+        return x
 
     def _capture(self, cap: _Captured, pools) -> None:
         # Warm-up on a side stream (initialises library handles); it performs the same step the
@@ -479,12 +488,12 @@ class GraphedStep:
         pages = max(-(-m.max_seq_len // m.kv_block_size), max_pages)
         mirror = self._mirror_for(B, pages, device)
         sig = _signature(pools)
-        key = (B, Tb)
+        key = (B, Tb, bool(want_logits))
         cap = self.captured.get(key)
         if cap is None or cap.signature != sig or cap.pages < max_pages:
             if cap is not None and cap.signature != sig:
                 self.captured.clear()  # every graph holds the old storage addresses
-            cap = _Captured(m, B, Tb, pages, device, pools, mirror.width)
+            cap = _Captured(m, B, Tb, pages, device, pools, mirror.width, tokens_only=not want_logits)
             self.captured[key] = cap
         mrows = mirror.rows_for(states0)
         cap.desc.wait()  # the previous replay of this graph has read its descriptor

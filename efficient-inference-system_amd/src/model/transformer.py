@@ -113,10 +113,12 @@ class TinyTransformerLM(nn.Module):
         return self._graph_step
 
     @torch.no_grad()
-    def prepare_graphs(self, max_batch: int, device) -> int:
+    def prepare_graphs(self, max_batch: int, device, want_logits: bool = False) -> int:
         """Capture the HIP graphs of cached steps ahead of time: for every batch size up to
         max_batch, one prefill chunk per length bucket and one decode step, on throwaway
-        requests that are released afterwards. Leaves fresh pools; returns the captures made."""
+        requests that are released afterwards. want_logits selects the graphs of steps that return
+        logits (forward, greedy_step(return_logits=True)) instead of those that return only the
+        greedy tokens. Leaves fresh pools; returns the captures made."""
         from src.model.graph_decode import T_BUCKETS
 
         device = torch.device(device)
@@ -137,7 +139,10 @@ class TinyTransformerLM(nn.Module):
                 if pos + T > self.max_seq_len:
                     continue
                 ids = torch.zeros((B, T), dtype=torch.long, device=device)
-                self(ids, kv_caches=stacked(), use_cache=True, position_offset=pos, current_lengths=T)
+                if want_logits:
+                    self(ids, kv_caches=stacked(), use_cache=True, position_offset=pos, current_lengths=T)
+                else:
+                    self.greedy_step(ids, stacked(), position_offset=pos, current_lengths=[T] * B)
                 pos += T
             for r in range(B):
                 self.release_request_caches(per_request[r])

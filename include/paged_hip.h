@@ -229,6 +229,22 @@ int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int32_t in_fea
                    void* out, int64_t out_stride, int dtype, void* stream);
 
 /*
+ * pa_linear_select_rows: pa_linear_rows over one selected row per group of x, without a residual:
+ * out[g, :] = act(LN(x[g * group_rows + r_g, :]) W^T + bias) for g < groups, where r_g =
+ * row_index[g] (device int32; a negative value counts from the group's end, as Python indexing
+ * does, and the result is clamped into [0, group_rows)). Same dtypes, shapes and alignment as
+ * pa_linear_rows; groups is at most 1024. No reference counterpart as an entry point: it computes
+ * ln_f + lm_head (src/model/transformer.py:176-177) only for the row of each request whose greedy
+ * token the executors take (src/serving/continuous_generate.py:145,238), instead of every row
+ * of a prefill chunk.
+ */
+int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t groups, int32_t group_rows,
+                          const int32_t* row_index, int32_t in_features, const void* weight,
+                          const void* bias, int32_t out_features, const void* ln_weight,
+                          const void* ln_bias, float ln_eps, int32_t activation, void* out,
+                          int64_t out_stride, int dtype, void* stream);
+
+/*
  * pa_qkv_append: the three projections of a cached attention layer in one launch, with the
  * LayerNorm before them and the KV append after them: q_out[m, :] = LN(x[m, :]) wq^T + bq, and
  * the rows LN(x[m, :]) wk^T + bk and LN(x[m, :]) wv^T + bv are written, split into num_heads

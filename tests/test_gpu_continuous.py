@@ -102,7 +102,7 @@ def test_continuous_batching_benchmark_model_lockstep(device, monkeypatch):
     hip = benchmark_model("hip_paged", device)
     ref = benchmark_model("paged_reference", device)
     ref.load_state_dict(copy.deepcopy(hip.state_dict()))
-    captured = hip.prepare_graphs(8, device)
+    captured = hip.prepare_graphs(8, device, want_logits=True)
     print(f"C4 lockstep: {N_REQUESTS} requests, {captured} graphs captured ahead", flush=True)
 
     ref_states: dict[int, list] = {}

@@ -117,3 +117,44 @@ def test_graph_decode_bf16_kv_cache_matches_eager(device, monkeypatch):
             tok = torch.randint(0, 300, (B, 1), device=device)
     assert graphed._graph_step is not None and graphed._graph_step.captures >= 1
     assert any(c.fused for c in graphed._graph_step.captured.values()), "the fused decode kernels were not used"
+
+
+def test_tokens_only_graphs_select_the_greedy_rows(device):
+    """greedy_step without logits replays graphs that compute ln_f + lm_head only for each request's
+    greedy row (pa_linear_select_rows): the same tokens as the argmax of the full logits of a
+    twin model's logits graphs (unless a row's top two logits are within 1e-4), and the same block
+    lists, over prefill chunks in several buckets and decode steps."""
+    full, sel = make(device, seed=3), make(device, seed=3)
+    sel.load_state_dict(full.state_dict())
+    B = 3
+    per = {}
+    for name, m in (("full", full), ("sel", sel)):
+        per[name] = m.create_request_kv_caches(B)
+    pos = [0, 0, 0]
+    steps = [(40, [40, 17, 40]), (100, [100, 64, 3]), (16, [16, 16, 0])] + [(1, [1, 1, 1])] * 20
+    ties = 0
+    g = torch.Generator().manual_seed(9)
+    for T, cur in steps:
+        ids = torch.randint(0, 300, (B, T), generator=g)
+        with torch.no_grad():
+            tf, logits, _ = full.greedy_step(ids, stack(per["full"], [0, 1, 2]), position_offset=list(pos),
+                                             current_lengths=cur, return_logits=True)
+            ts, none, _ = sel.greedy_step(ids, stack(per["sel"], [0, 1, 2]), position_offset=list(pos),
+                                          current_lengths=cur)
+        assert none is None
+        tf, ts = tf.tolist(), ts.tolist()
+        for b in range(B):
+            row = logits[b, (cur[b] - 1) % T]
+            top2 = torch.topk(row, 2).values
+            assert tf[b] == int(torch.argmax(row))
+            if (top2[0] - top2[1]).item() < 1e-4:
+                ties += 1
+            else:
+                assert ts[b] == tf[b], (T, b)
+        pos = [p + c for p, c in zip(pos, cur)]
+    assert ties <= 2
+    caps = sel._graph_step.captured
+    assert any(not k[2] and c.select_head for k, c in caps.items()), "the row-selecting graphs were not used"
+    for rf, rs in zip(per["full"], per["sel"]):
+        for a, b in zip(rf, rs):
+            assert a.block_ids == b.block_ids and a.seq_len == b.seq_len

@@ -263,3 +263,45 @@ def test_embed_rows_bf16(device):
             row = tok.weight[i].float().cpu() if 0 <= i < 300 else torch.zeros(128)
             want[b * 9 + t] = (row + pos.weight[min(int(p0[b]) + t, 63)].float().cpu()).to(torch.bfloat16)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("groups,group_rows", [(1, 1), (3, 7), (8, 1), (8, 256), (5, 33)])
+def test_linear_select_rows(device, dtype, groups, group_rows):
+    """pa_linear_select_rows computes each group's selected row, bit-identical to pa_linear_rows on
+    that row alone (same kernel, same per-row arithmetic), and within 2e-5 of float64 torch for fp32;
+    negative rows count from the group's end, out-of-range rows are clamped into the group."""
+    torch.manual_seed(groups * 100 + group_rows)
+    K, N = 512, 5000
+    lin = nn.Linear(K, N).to(device=device, dtype=dtype)
+    ln = nn.LayerNorm(K).to(device=device, dtype=dtype)
+    with torch.no_grad():
+        ln.weight.normal_(1.0, 0.1)
+        ln.bias.normal_(0.0, 0.1)
+    x = torch.randn(groups * group_rows, K, device=device).to(dtype)
+    g = torch.Generator().manual_seed(groups + group_rows)
+    rows = torch.randint(-group_rows, group_rows, (groups,), generator=g, dtype=torch.int32)
+    if groups >= 3:
+        rows[0], rows[1] = group_rows + 5, -group_rows - 3  # clamped to the group's last / first row
+    eff = [min(max(r + group_rows if r < 0 else r, 0), group_rows - 1) for r in rows.tolist()]
+    picked = torch.stack([x[gi * group_rows + r] for gi, r in enumerate(eff)])
+    got = hip_linear.linear_select_rows_hip(x, group_rows, rows.to(device), lin, ln=ln)
+    assert got.shape == (groups, N)
+    same = hip_linear.linear_rows_hip(picked.contiguous(), lin, ln=ln)
+    assert torch.equal(got, same)
+    if dtype == torch.float32:
+        assert (got.double().cpu() - ref_linear(picked, lin, ln)).abs().max().item() <= 2e-5
+
+
+def test_linear_select_rows_rejects_bad_arguments(device):
+    lin = nn.Linear(256, 64).to(device)
+    x = torch.randn(12, 256, device=device)
+    rows = torch.zeros(3, dtype=torch.int32, device=device)
+    with pytest.raises(ValueError):
+        hip_linear.linear_select_rows_hip(x, 5, rows, lin)  # 3 groups of 5 rows > 12 rows
+    with pytest.raises(ValueError):
+        hip_linear.linear_select_rows_hip(x, 4, rows.long(), lin)
+    with pytest.raises(ValueError):
+        hip_linear.linear_select_rows_hip(x, 4, rows.cpu(), lin)
+    with pytest.raises(ValueError):
+        hip_linear.linear_select_rows_hip(x, 4, rows, lin, out=torch.empty(3, 32, device=device))
