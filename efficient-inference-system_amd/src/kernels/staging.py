@@ -38,7 +38,9 @@ class _Hip:
                            ("hipEventCreateWithFlags", [ctypes.POINTER(vp), ctypes.c_uint]),
                            ("hipEventRecord", [vp, vp]),
                            ("hipEventSynchronize", [vp]),
+                           ("hipEventDestroy", [vp]),
                            ("hipHostMalloc", [ctypes.POINTER(vp), ctypes.c_size_t, ctypes.c_uint]),
+                           ("hipHostFree", [vp]),
                            ("hipHostGetDevicePointer", [ctypes.POINTER(vp), vp, ctypes.c_uint])):
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -47,7 +49,9 @@ class _Hip:
         self.event_create = lib.hipEventCreateWithFlags
         self.event_record = lib.hipEventRecord
         self.event_sync = lib.hipEventSynchronize
+        self.event_destroy = lib.hipEventDestroy
         self.host_malloc = lib.hipHostMalloc
+        self.host_free = lib.hipHostFree
         self.host_device_pointer = lib.hipHostGetDevicePointer
 
 
@@ -143,8 +147,8 @@ class MappedHostWords:
     hipHostMalloc as mapped, coherent memory, so a kernel sees the host's latest stores without a
     copy call and without stale cache lines. The host must not rewrite words a launch reads until
     that launch has run: mark(stream) after enqueueing such a launch, wait() before the next
-    rewrite (an event; free when the launch has already finished). Kept until the process ends:
-    graphs captured with its device address may outlive any owner."""
+    rewrite (an event; free when the launch has already finished). close() frees it, once no
+    launch that reads it can run again (the graphs captured with its device address are gone)."""
 
     def __init__(self, words: int, device: torch.device):
         hip = _runtime()
@@ -173,3 +177,13 @@ class MappedHostWords:
     def mark(self, stream: int) -> None:
         _check(_hip.event_record(self.event, stream), "hipEventRecord")
         self.pending = True
+
+    def close(self) -> None:
+        """Wait for the last marked launch, then free the memory and the event (idempotent)."""
+        if self.host_ptr is None:
+            return
+        self.wait()
+        self.words = None
+        _check(_hip.host_free(ctypes.c_void_p(self.host_ptr)), "hipHostFree")
+        _check(_hip.event_destroy(self.event), "hipEventDestroy")
+        self.host_ptr = self.device_ptr = self.event = None

@@ -317,6 +317,12 @@ class _Captured:
         self.graph = None
         self.logits = None
 
+    def release(self) -> None:
+        """Drop the graph, then free the step descriptor it reads (after its last replay)."""
+        self.desc.wait()
+        self.graph = None
+        self.desc.close()
+
 
 class GraphedStep:
     def __init__(self, model):
@@ -445,6 +451,11 @@ class GraphedStep:
         cap.graph = g
         self.captures += 1
 
+    def _drop_captures(self) -> None:
+        for cap in self.captured.values():
+            cap.release()
+        self.captured.clear()
+
     # ------------------------------------------------------------------------------------------
     def _mirror_for(self, B: int, pages: int, device: torch.device) -> _BlockTableMirror:
         """The mirror, (re)allocated when a step needs more rows or a wider row than it has; a new
@@ -453,8 +464,8 @@ class GraphedStep:
         if mir is None or B > mir.rows or pages > mir.width:
             rows = max(64, 2 * B, mir.rows if mir is not None else 0)
             width = max(pages, mir.width if mir is not None else 0)
+            self._drop_captures()
             self.mirror = mir = _BlockTableMirror(rows, width, device)
-            self.captured.clear()
         return mir
 
     def __call__(self, input_ids, positions, current_lengths: list[int], kv_caches, rows: list[int] | None = None,
@@ -492,7 +503,9 @@ class GraphedStep:
         cap = self.captured.get(key)
         if cap is None or cap.signature != sig or cap.pages < max_pages:
             if cap is not None and cap.signature != sig:
-                self.captured.clear()  # every graph holds the old storage addresses
+                self._drop_captures()  # every graph holds the old storage addresses
+            elif cap is not None:
+                cap.release()  # replaced by one with more pages
             cap = _Captured(m, B, Tb, pages, device, pools, mirror.width, tokens_only=not want_logits)
             self.captured[key] = cap
         mrows = mirror.rows_for(states0)

@@ -166,6 +166,9 @@ def test_pack_metadata_mirror_matches_csr_pack(device):
         got = mirror.cpu().numpy()
         for r in rows:
             assert got[r, :len(lists[r])].tolist() == lists[r] == shadow[r, :slen[r]].tolist()
+    desc.close()
+    assert desc.host_ptr is None
+    desc.close()  # idempotent
 
 
 def test_zero_blocks_and_release(device):

@@ -158,3 +158,33 @@ def test_tokens_only_graphs_select_the_greedy_rows(device):
     for rf, rs in zip(per["full"], per["sel"]):
         for a, b in zip(rf, rs):
             assert a.block_ids == b.block_ids and a.seq_len == b.seq_len
+
+
+def test_dropped_graphs_free_their_descriptors(device, monkeypatch):
+    """Graphs dropped for a new storage or mirror release their pinned step descriptors (after
+    their last replay); the steps that follow capture again and still match the eager forward."""
+    graphed, eager = make(device, seed=5), make(device, seed=5)
+    eager.load_state_dict(graphed.state_dict())
+    B = 2
+    caches = {"graph": graphed.create_request_kv_caches(B), "eager": eager.create_request_kv_caches(B)}
+    g = torch.Generator().manual_seed(4)
+    pos = torch.zeros(B, dtype=torch.long)
+    old = []
+    for step, T in enumerate((20, 1, 1, 16, 1, 1)):
+        if step == 3:
+            runner = graphed._graph_step
+            old = list(runner.captured.values())
+            assert old and all(c.desc.host_ptr is not None for c in old)
+            runner._drop_captures()
+            assert not runner.captured and all(c.desc.host_ptr is None and c.graph is None for c in old)
+        ids = torch.randint(0, 300, (B, T), generator=g).to(device)
+        outs = {}
+        with torch.no_grad():
+            for name, m in (("eager", eager), ("graph", graphed)):
+                monkeypatch.setenv("PAGED_HIP_GRAPHS", "0" if name == "eager" else "1")
+                outs[name], _ = m(ids, kv_caches=stack(caches[name], [0, 1]), use_cache=True,
+                                  position_offset=pos.to(device), current_lengths=torch.tensor([T] * B))
+        assert (outs["eager"] - outs["graph"]).abs().max().item() <= 1e-5, step
+        pos += T
+    runner = graphed._graph_step
+    assert runner.captured and all(c.desc.host_ptr is not None for c in runner.captured.values())
