@@ -101,7 +101,9 @@ constexpr int prefill_waves() { return 4; }
 // at 1, 14.5 at 2, 15.0 at 3; fp32 22.8 us at 1, 29.5 at 2, where the registers cost a
 // wavefront per SIMD; with 4 wavefronts per workgroup and the die-aware order, 20.0 at 1 and 20.9
 // at 2); at head_dim 128, 4 requests x 32 heads, 256-token chunks over ~1k contexts, bf16 KV
-// 109.6 us at 1, 102-105 at 2 or 3; fp32 KV spills beyond 1.
+// 109.6 us at 1, 102-105 at 2 or 3; fp32 KV spills beyond 1. Measured again on the current kernel
+// (chunked workload, three interleaved runs): bf16 KV 11.5-11.7 us at 1, 11.9-12.0 at 2, 12.1-12.7
+// at 3; fp32 KV 18.4-18.8 at 1, 19.8-20.0 at 2 (and 8 x 8 heads fp32 25 -> 54 us).
 #ifndef PA_PREFILL_DEPTH_F32_64
 #define PA_PREFILL_DEPTH_F32_64 1
 #endif
