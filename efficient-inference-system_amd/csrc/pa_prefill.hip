@@ -132,7 +132,9 @@ constexpr int prefill_waves() { return 4; }
 // of the last one showed why: a SIMD finishes the same number of blocks at the same time either
 // way (a heavy tile's wavefront left alone on its SIMD runs about a third faster per block), while
 // loading both units' queries and merging 8 partial states per unit lengthen the prologue (1.1 ->
-// 1.9 us) and the epilogue.
+// 1.9 us) and the epilogue. Dealing the 16-byte chunks of each K (and q) row round-robin to the
+// four lane groups, so that one load instruction reads one 64-byte line per key row instead of
+// 16 bytes from each of four lines: no change (fp32 18.2-18.4 us, bf16 11.4-11.6 us).
 template <typename KV, int HD, bool OCC4>
 constexpr int prefill_round() { return 1; }
 
