@@ -92,7 +92,9 @@ struct PrefillShape {
 // 8 and two tiles in flight, 29.2 us with 16 on the chunked-prefill workload (4 x 8 heads x 64);
 // 217 against 252 us with 8 on 4 x 32 heads x 128, 256-token chunks over 0.6-1.2k contexts; within
 // 0.4 us either way on single requests. bf16 KV: 12.3-12.7 us with 4, 13.4-13.8 with 8, 19.0 with
-// 16 (chunked workload), 99 against 128 us with 8 (4 x 32 heads x 128).
+// 16 (chunked workload), 99 against 128 us with 8 (4 x 32 heads x 128). Measured again on the current
+// kernel (three wavefronts per SIMD fit its registers at 6 per workgroup): 5 and 6 wavefronts, fp32
+// KV 21.5-21.6 and 22.1-22.4 us against 18.3; bf16 12.2 and 12.5-12.7 against 11.4-11.5.
 template <typename KV>
 constexpr int prefill_waves() { return 4; }
 
