@@ -136,7 +136,13 @@ constexpr int prefill_waves() { return 4; }
 // loading both units' queries and merging 8 partial states per unit lengthen the prologue (1.1 ->
 // 1.9 us) and the epilogue. Dealing the 16-byte chunks of each K (and q) row round-robin to the
 // four lane groups, so that one load instruction reads one 64-byte line per key row instead of
-// 16 bytes from each of four lines: no change (fp32 18.2-18.4 us, bf16 11.4-11.6 us).
+// 16 bytes from each of four lines: no change (fp32 18.2-18.4 us, bf16 11.4-11.6 us). fp32 KV
+// through the bf16 matrix cores (every fp32 operand split into bf16 hi + lo, products hi*hi +
+// hi*lo + lo*hi accumulated in fp32: 3.5x less matrix-pipe time, ~1e-5 error): 18.5 -> 17.6 us.
+// So the kernel is not matrix-bound: with bf16 KV (1/16 of the fp32 MFMA time, half the bytes)
+// it still takes 11.5 us. What bounds it is each wavefront's per-block chain (loads, QK^T, the
+// softmax exchanges, PV) at two wavefronts per SIMD and the L2 traffic of reading every KV block
+// once per 16-row tile (16 times per (request, head): ~155 MB per launch with fp32 KV).
 template <typename KV, int HD, bool OCC4>
 constexpr int prefill_round() { return 1; }
 
