@@ -140,9 +140,19 @@ constexpr int prefill_waves() { return 4; }
 // through the bf16 matrix cores (every fp32 operand split into bf16 hi + lo, products hi*hi +
 // hi*lo + lo*hi accumulated in fp32: 3.5x less matrix-pipe time, ~1e-5 error): 18.5 -> 17.6 us.
 // So the kernel is not matrix-bound: with bf16 KV (1/16 of the fp32 MFMA time, half the bytes)
-// it still takes 11.5 us. What bounds it is each wavefront's per-block chain (loads, QK^T, the
-// softmax exchanges, PV) at two wavefronts per SIMD and the L2 traffic of reading every KV block
-// once per 16-row tile (16 times per (request, head): ~155 MB per launch with fp32 KV).
+// it still takes 11.5 us. Timing copies without the KV loads in the walk take 7.7-8.1 us (bf16)
+// and 15.6-17.4 us (fp32): the loads cost about a third of the bf16 time. Counters
+// (TCP_TCP_LATENCY / TA_TCP_STATE_READ, TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ,
+// TA_ADDR_STALLED_BY_TC_CYCLES) place that cost in the compute unit's L1: a load instruction spends
+// ~1,170 cycles there, an L2 request ~160, L2 hits 88%, and the address path waits on L1 a quarter
+// of the time. Not kept, each measured in graph replay against the kernel here: two query tiles per
+// workgroup folding every KV tile into both (half the loads per item; one wavefront per SIMD at
+// 256 workgroups): fp32 18.3 -> 23.1 us, bf16 11.4 -> 12.2 (a 128/256 chunk mix 13.4 -> 12.4);
+// non-temporal KV loads: fp32 18.2 -> 19.2, bf16 unchanged; a tile-dependent rotation of each
+// tile's walk: bf16 11.4 -> 11.6; KV pools of 200 to 32768 blocks, ids scattered or sorted: within
+// 0.4 us (not translation-bound); the wavefronts' states rescaled before the LDS merge so the final
+// pass is plain sums: unchanged. The lazy rescale test per lane and one lane read per block for
+// the block address (about 60 instead of 100 instructions per bf16 block): bf16 11.5 -> 11.3 us.
 template <typename KV, int HD, bool OCC4>
 constexpr int prefill_round() { return 1; }
 
@@ -254,9 +264,8 @@ void prefill_mfma_kernel(const AttnArgs a) {
     uint32_t v[4][VW];
     bool ok;
   };
-  auto issue = [&](Tile& t, int blk) {
-    t.ok = blk >= 0 && blk < a.num_blocks;
-    const int64_t base = ((int64_t)(t.ok ? blk : 0) * a.H + h) * (BS * HD);
+  auto issue = [&](Tile& t, int64_t base, bool ok) {
+    t.ok = ok;
     load_words<KW>(kpool + base + c * HD + G * QD, t.k);
 #pragma unroll
     for (int r = 0; r < 4; ++r) load_words<VW>(vpool + base + (4 * G + r) * HD + c * DT, t.v[r]);
@@ -305,30 +314,32 @@ void prefill_mfma_kernel(const AttnArgs a) {
           sacc[q][r] = (tr[q].ok && t < n_c) ? sacc[q][r] : -INFINITY;
         }
     }
+    // A column's max over the round can pass m + slack only where one of its four lanes' partial
+    // maxima does, so the cross-lane reduction and the rescale run only in the rounds where some
+    // lane's partial max passes (same results as reducing every round).
     float mloc = -INFINITY;
 #pragma unroll
     for (int q = 0; q < NV; ++q)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sacc[q][r]);
-    mloc = max_xor32(max_xor16(mloc));
-    const bool grow = mloc > m + kPrefillRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float mnew = grow ? mloc : m;
+    if (__builtin_amdgcn_ballot_w64(mloc > m + kPrefillRescaleSlack) != 0) {
+      const float mcol = max_xor32(max_xor16(mloc));
+      const float mnew = mcol > m + kPrefillRescaleSlack ? mcol : m;
       const float alpha = fast_exp2(m - mnew);
       l *= alpha;
 #pragma unroll
       for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
       m = mnew;
     }
-    float ps = 0.f;
+    // l is this lane's part of the row sum (its four keys of every round); the four lanes of a
+    // column are summed once, after the walk.
 #pragma unroll
     for (int q = 0; q < NV; ++q)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         sacc[q][r] = fast_exp2(sacc[q][r] - m);
-        ps += sacc[q][r];
+        l += sacc[q][r];
       }
-    l += sum_xor32(sum_xor16(ps));
     // ---- O^T += V^T P^T -----------------------------------------------------------------------
     // fp32 KV at head_dim 128: the PV MFMAs run at raised wavefront priority, so a wavefront that
     // reaches them issues ahead of co-resident ones still in their softmax (4 requests x 32
@@ -380,11 +391,19 @@ void prefill_mfma_kernel(const AttnArgs a) {
     const int nr = (cnt + R - 1) / R;
     int ids = -1;
     if (lane < cnt) ids = c0 == 0 ? ids0 : pt[jb + w + (c0 + lane) * NW];
+    // Each lane turns its entry into the element offset of its (block, head) slab and a validity
+    // bit once per chunk; a block then costs two lane reads. Entries outside the pool (and lanes
+    // past the chunk) read slab (0, h) and are masked.
+    const bool okl = ids >= 0 && ids < a.num_blocks;
+    const uint64_t okmask = __builtin_amdgcn_ballot_w64(okl);
+    const int64_t offl = ((int64_t)(okl ? ids : 0) * a.H + h) * (BS * HD);
     auto put = [&](Tile* tr, int rr) {
 #pragma unroll
       for (int q = 0; q < R; ++q) {
-        const int k = rr * R + q;
-        issue(tr[q], k < cnt ? __builtin_amdgcn_readlane(ids, k) : -1);
+        const int k = rr * R + q;  // < nr * R <= kWave; lanes past cnt hold -1
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)offl, k);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)offl >> 32), k);
+        issue(tr[q], (int64_t)(((uint64_t)hi << 32) | lo), ((okmask >> k) & 1) != 0);
       }
     };
     auto fold = [&](const Tile* tr, int rr) {
@@ -415,6 +434,7 @@ void prefill_mfma_kernel(const AttnArgs a) {
   }
 
   // ---- merge the wavefronts' states ---------------------------------------------------------
+  l = sum_xor32(sum_xor16(l));
 #pragma unroll
   for (int t = 0; t < DT; ++t)
 #pragma unroll
