@@ -18,6 +18,14 @@
 // v_mfma_f32_16x16x32_bf16 for QK^T (q rounded to bf16) and v_mfma_f32_16x16x16_bf16 for PV
 // (softmax weights rounded to bf16), accumulating in fp32.
 //
+// KV staging. The K operand puts key row c on lane c, so a load straight into the operand
+// registers has every 4-lane group of an instruction touching 4 cache lines; the compute unit's L1
+// serves one line per lane group per access, and on the chunked workload with bf16 KV that made
+// the walk L1-bound (11.3 us against 7.7-8.1 us for a copy without the walk's KV loads). At
+// head_dim 64 each wavefront instead copies its blocks' K and V slabs into its own two-stage LDS
+// ring with LDS-direct loads, which read the contiguous slab 16 bytes per lane (one line per lane
+// group), and reads the operands from LDS (prefill_stage_in_lds picks the staging per launch).
+//
 // Split-K: when num_splits > 1 each unit's KV blocks are cut into ranges of split_blocks blocks,
 // one workgroup per range. Work items are ordered split-major, so the grid holds many
 // equal-sized items instead of a few long ones. A unit with one active split writes its output
@@ -141,11 +149,13 @@ constexpr int prefill_waves() { return 4; }
 // hi*lo + lo*hi accumulated in fp32: 3.5x less matrix-pipe time, ~1e-5 error): 18.5 -> 17.6 us.
 // So the kernel is not matrix-bound: with bf16 KV (1/16 of the fp32 MFMA time, half the bytes)
 // it still takes 11.5 us. Timing copies without the KV loads in the walk take 7.7-8.1 us (bf16)
-// and 15.6-17.4 us (fp32): the loads cost about a third of the bf16 time. Counters
-// (TCP_TCP_LATENCY / TA_TCP_STATE_READ, TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ,
-// TA_ADDR_STALLED_BY_TC_CYCLES) place that cost in the compute unit's L1: a load instruction spends
-// ~1,170 cycles there, an L2 request ~160, L2 hits 88%, and the address path waits on L1 a quarter
-// of the time. Not kept, each measured in graph replay against the kernel here: two query tiles per
+// and 15.6-17.4 us (fp32): with register staging the loads cost about a third of the bf16 time.
+// Counters (TCP_TCP_LATENCY / TA_TCP_STATE_READ, TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ,
+// TA_ADDR_STALLED_BY_TC_CYCLES, TCP_TOTAL_CACHE_ACCESSES) place that cost in the compute unit's L1:
+// a load instruction spends ~1,170 cycles there, an L2 request ~160, L2 hits 88%, the address path
+// waits on L1 a quarter of the time, and ~210 L1 accesses per (tile, bf16 block) item match one
+// access per lane for the K rows: what the LDS staging removes. Not kept, each measured in graph
+// replay against the register-staged kernel: two query tiles per
 // workgroup folding every KV tile into both (half the loads per item; one wavefront per SIMD at
 // 256 workgroups): fp32 18.3 -> 23.1 us, bf16 11.4 -> 12.2 (a 128/256 chunk mix 13.4 -> 12.4);
 // non-temporal KV loads: fp32 18.2 -> 19.2, bf16 unchanged; a tile-dependent rotation of each
@@ -165,12 +175,26 @@ constexpr int prefill_depth() {
                                         : (HD == 64 ? PA_PREFILL_DEPTH_BF16_64 : PA_PREFILL_DEPTH_BF16_128);
 }
 
+// One LDS-direct load (global_load_lds_dwordx4): lane L reads the 16 bytes at base + voff
+// (bytes) and writes them to LDS at lds + 16L; base and lds are wavefront-uniform. Inline
+// assembly, so the compiler neither tracks it (the caller waits with vm_wait) nor moves memory
+// accesses across it.
+__device__ __forceinline__ void stage_load16(const void* base, uint32_t voff, const void* lds) {
+  const uint32_t m0 = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m0) : "memory");
+}
+// Wait until at most N vector memory loads of this wavefront are outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // OCC4: registers capped at 128 so that 4 wavefronts share a SIMD (4 workgroups per CU instead of
 // 3). Only fp32 KV at head_dim 64 is near the cap (129 registers unconstrained, 128 and two
 // spilled values capped); the launch takes the capped build when the grid would not fit on the
 // GPU at 3 workgroups per CU (8 x 8 heads x 256 rows, 1024 workgroups: 39.3 -> 33.3 us), and the
 // unconstrained one otherwise (chunked workload, 512 workgroups: 20.4 us against 21.3 capped).
-template <typename KV, typename IO, int HD, bool OCC4 = false>
+template <typename KV, typename IO, int HD, bool OCC4 = false, bool LDSK = false>
 __global__ __launch_bounds__(prefill_waves<KV>() * kWave) __attribute__((amdgpu_waves_per_eu(OCC4 ? 4 : 1)))
 void prefill_mfma_kernel(const AttnArgs a) {
   constexpr int BS = 16;
@@ -179,9 +203,16 @@ void prefill_mfma_kernel(const AttnArgs a) {
   constexpr int QD = Sh::QD, DT = Sh::DT, KW = Sh::KW, VW = Sh::VW;
   constexpr bool kBf16 = Sh::kBf16;
 
-  __shared__ float sm_o[NW][16][HD + 1];
+  // Per wavefront: its merge rows (16 x (HD + 1) floats) and, with LDSK, a two-stage ring of
+  // (K slab, V slab) the merge rows reuse after the walk.
+  constexpr int kRowB = HD * (int)sizeof(KV);  // bytes of one key row
+  constexpr int kSlab = BS * kRowB;            // bytes of one (block, head) K or V slab
+  constexpr int kOB = 16 * (HD + 1) * 4;
+  constexpr int kWaveB = LDSK ? (4 * kSlab > kOB ? 4 * kSlab : kOB) : kOB;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[NW * kWaveB];
   __shared__ float sm_m[NW][16];
   __shared__ float sm_l[NW][16];
+  auto sm_o = [&](int ww, int cc) -> float* { return reinterpret_cast<float*>(smem + ww * kWaveB) + cc * (HD + 1); };
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -386,6 +417,91 @@ void prefill_mfma_kernel(const AttnArgs a) {
   static_assert(kWave % R == 0, "a page-table chunk holds whole rounds");
   using Full = std::integral_constant<int, R>;
   using One = std::integral_constant<int, 1>;
+  if constexpr (LDSK) {
+    // KV through LDS: each block's K and V slabs are copied into the wavefront's ring with
+    // LDS-direct loads (each instruction copies 1 KB of the contiguous slab, so every 4 lanes read
+    // one cache line), then read in the operand layouts. K rows are stored with their 16-byte
+    // chunks XOR-swizzled by row so that the 16 rows of an operand read hit every bank once; bf16
+    // V rows r and r ^ 1 trade places in every other group of four, so that the two lane groups of
+    // a 64-bit read pass land in different bank halves. The loads are untracked by the compiler:
+    // the walk waits for them itself (vmcnt), one block ahead.
+    static_assert(HD == 64 && R == 1 && D == 1, "LDS staging: head_dim 64, one block per round and one ahead");
+    constexpr int CPR = kRowB / 16;        // 16-byte chunks per row
+    constexpr int RPB = 256 / kRowB;       // rows per 256 bytes (one pass over the banks)
+    constexpr int NI = kSlab / (16 * kWave);  // LDS-direct instructions per slab
+    auto ksw = [](int r) { return (r / RPB) & (CPR - 1); };
+    auto vpos = [](int r) { return kBf16 ? (r ^ ((r >> 2) & 1)) : r; };  // an involution
+    uint32_t kso[NI], vso[NI];
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+      const int sl = n * kWave + lane;  // the LDS chunk this lane fills
+      const int r = sl / CPR, p = sl % CPR;
+      kso[n] = (uint32_t)(r * kRowB + 16 * (p ^ ksw(r)));
+      vso[n] = (uint32_t)(vpos(r) * kRowB + 16 * p);
+    }
+    unsigned char* ring = smem + w * kWaveB;
+    for (int c0 = 0; c0 < mine; c0 += kWave) {
+      const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
+      int ids = -1;
+      if (lane < cnt) ids = c0 == 0 ? ids0 : pt[jb + w + (c0 + lane) * NW];
+      const bool okl = ids >= 0 && ids < a.num_blocks;
+      const uint64_t okmask = __builtin_amdgcn_ballot_w64(okl);
+      const int64_t offl = ((int64_t)(okl ? ids : 0) * a.H + h) * (BS * HD);
+      auto stage_issue = [&](int st, int k) {
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)offl, k);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)offl >> 32), k);
+        const int64_t off = (int64_t)(((uint64_t)hi << 32) | lo);
+        unsigned char* dst = ring + st * 2 * kSlab;
+#pragma unroll
+        for (int n = 0; n < NI; ++n) stage_load16(kpool + off, kso[n], dst + n * 16 * kWave);
+#pragma unroll
+        for (int n = 0; n < NI; ++n) stage_load16(vpool + off, vso[n], dst + kSlab + n * 16 * kWave);
+      };
+      stage_issue(0, 0);
+      for (int k = 0; k < cnt; ++k) {
+        const int st = k & 1;
+        if (k + 1 < cnt) {
+          stage_issue(st ^ 1, k + 1);
+          vm_wait<2 * NI>();
+        } else {
+          vm_wait<0>();
+        }
+        const unsigned char* sb = ring + st * 2 * kSlab;
+        Tile tt;
+        tt.ok = ((okmask >> k) & 1) != 0;
+        if constexpr (kBf16) {
+#pragma unroll
+          for (int s2 = 0; s2 < QD / 8; ++s2) {
+            const int q = G * (QD / 8) + s2;
+            const u32x4 x = *reinterpret_cast<const u32x4*>(sb + c * kRowB + 16 * (q ^ ksw(c)));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tt.k[4 * s2 + e] = x[e];
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const u32x2 x = *reinterpret_cast<const u32x2*>(sb + kSlab + vpos(4 * G + r) * kRowB + 8 * c);
+            tt.v[r][0] = x[0];
+            tt.v[r][1] = x[1];
+          }
+        } else {
+#pragma unroll
+          for (int kk = 0; kk < QD / 4; ++kk) {
+            const int q = G * (QD / 4) + kk;
+            const u32x4 x = *reinterpret_cast<const u32x4*>(sb + c * kRowB + 16 * (q ^ ksw(c)));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tt.k[4 * kk + e] = x[e];
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(sb + kSlab + (4 * G + r) * kRowB + 16 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tt.v[r][e] = x[e];
+          }
+        }
+        fold_round(&tt, One{}, jb + w + (c0 + k) * NW, NW);
+      }
+    }
+  } else
   for (int c0 = 0; c0 < mine; c0 += kWave) {
     const int cnt = (mine - c0) < kWave ? (mine - c0) : kWave;
     const int nr = (cnt + R - 1) / R;
@@ -438,7 +554,7 @@ void prefill_mfma_kernel(const AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < DT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sm_o[w][c][(4 * G + r) * DT + t] = oacc[t][r];
+    for (int r = 0; r < 4; ++r) sm_o(w, c)[(4 * G + r) * DT + t] = oacc[t][r];
   if (G == 0) {
     sm_m[w][c] = m;
     sm_l[w][c] = l;
@@ -459,7 +575,7 @@ void prefill_mfma_kernel(const AttnArgs a) {
     for (int ww = 0; ww < NW; ++ww) {
       const float f = fast_exp2(sm_m[ww][cc] - M);
       lsum = fmaf(sm_l[ww][cc], f, lsum);
-      A = fmaf(sm_o[ww][cc][d], f, A);
+      A = fmaf(sm_o(ww, cc)[d], f, A);
     }
     if (nact == 1) {
       IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(i0 + cc) * a.o_st;
@@ -510,10 +626,28 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
   }
 }
 
+// KV staging of the 16-row kernel at head_dim 64 (graph replay, MI355X):
+//   through LDS: bf16 KV chunked workload 11.3 -> 9.7 us (4 x 8 heads, four 256-token chunks),
+//   13.3 -> 9.6 us (a 128/256 chunk mix), 8 x 8 heads 14.7 -> 12.0 us; fp32 KV 18.3 -> 18.3 us and
+//   21.6 -> 21.2 us on the same two, but 25.6 -> 29.9 us on 8 x 8 heads (1024 workgroups: its 64 KB
+//   of LDS per workgroup allow 2 per CU where the register-staged build fits 4).
+// So: LDS for bf16 KV always, for fp32 KV while the grid fits 2 workgroups per CU.
+// PAGED_HIP_PREFILL_STAGING=lds / regs forces one of them (tests cover both).
+static bool prefill_stage_in_lds(bool fp32_kv, unsigned grid) {
+  const char* env = getenv("PAGED_HIP_PREFILL_STAGING");
+  if (env != nullptr && strcmp(env, "lds") == 0) return true;
+  if (env != nullptr && strcmp(env, "regs") == 0) return false;
+  return !fp32_kv || (int64_t)grid <= 2 * (int64_t)pa_host::device_cu_count();
+}
+
 template <typename KV, typename IO>
 static bool dispatch_prefill_io(const AttnArgs& a, dim3 grid, hipStream_t stream) {
   constexpr int threads = prefill_waves<KV>() * kWave;
   if (a.head_dim == 64) {
+    if (prefill_stage_in_lds(std::is_same<KV, float>::value, grid.x)) {
+      prefill_mfma_kernel<KV, IO, 64, false, true><<<grid, threads, 0, stream>>>(a);
+      return true;
+    }
     if constexpr (std::is_same<KV, float>::value) {
       if ((int64_t)grid.x > 3 * (int64_t)pa_host::device_cu_count()) {
         prefill_mfma_kernel<KV, IO, 64, true><<<grid, threads, 0, stream>>>(a);

@@ -96,10 +96,13 @@ def test_prefill_random_cases(device, monkeypatch, seed):
     io_dtype = r.choice([torch.float32, torch.bfloat16])
     kernel = r.choice(["", "tile", "wide"]) if fast else ""
     split = r.choice([0, 0, 1, 3]) if fast and kernel != "wide" else 0
+    staging = r.choice(["", "lds", "regs"])  # the 16-row kernel's KV staging at head_dim 64
     if kernel:
         monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", kernel)
+    if staging:
+        monkeypatch.setenv("PAGED_HIP_PREFILL_STAGING", staging)
     print(f"prefill seed={seed} B={B} H={H} T={T} Hd={Hd} bs={bs} kv={kv_dtype} io={io_dtype} "
-          f"kernel={kernel or 'auto'} split={split} ctx={ctx} curs={curs}", flush=True)
+          f"kernel={kernel or 'auto'} staging={staging or 'auto'} split={split} ctx={ctx} curs={curs}", flush=True)
     b = _build(device, seed, lens, curs, T, H, Hd, bs, kv_dtype, io_dtype)
     got = paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t,
                                       split_blocks=split)

@@ -87,6 +87,47 @@ def test_chunked_prefill_config(device, seed, kv_dtype, tol):
     assert err <= tol
 
 
+@pytest.mark.parametrize("seed", [0, 2])
+@pytest.mark.parametrize("kv_dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_kv_staging_lds_and_registers_agree(device, monkeypatch, seed, kv_dtype, tol):
+    """The 16-row kernel's two KV stagings (LDS-direct copies into a per-wavefront ring, or loads
+    straight into the operand registers) run the same products in the same order: bit-identical
+    outputs on the chunked-prefill workload, unsplit and split, and within tolerance of the oracle."""
+    w = workloads.chunked_prefill(seed=seed, device=device, kv_dtype=kv_dtype)
+    lists = w["block_lists"]
+    b = workloads._batch(w["q"], w["k_pool"], w["v_pool"], lists, w["seq_lens"], w["chunk_lens"], device)
+    print(f"kv staging seed={seed} kv={kv_dtype} ctx={w['prev_lens']} chunk={w['chunk_lens']}", flush=True)
+    outs = {}
+    for staging in ("lds", "regs"):
+        monkeypatch.setenv("PAGED_HIP_PREFILL_STAGING", staging)
+        for split in (0, 3):
+            outs[staging, split] = run(b, split_blocks=split)
+    for split in (0, 3):
+        assert torch.equal(outs["lds", split], outs["regs", split]), split
+    err = max_err(outs["lds", 0], oracle_out(b))
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= tol
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_kv_staging_on_a_large_grid(device, monkeypatch, kv_dtype):
+    """8 requests x 8 heads x 256 rows (1024 workgroups, past the grid where fp32 KV switches to
+    register staging): both stagings bit-identical and within tolerance of the oracle."""
+    b = workloads.large_prefill(seed=3, device=device, batch=8, heads=8, head_dim=64, chunk=256, ctx_lo=0,
+                                ctx_hi=768, kv_dtype=kv_dtype)
+    print(f"kv staging large grid kv={kv_dtype}", flush=True)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_STAGING", "lds")
+    lds = run(b)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_STAGING", "regs")
+    regs = run(b)
+    assert torch.equal(lds, regs)
+    monkeypatch.delenv("PAGED_HIP_PREFILL_STAGING")
+    assert torch.equal(run(b), regs if kv_dtype == torch.float32 else lds)
+    err = max_err(lds, oracle_out(b))
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= (1e-4 if kv_dtype == torch.float32 else 2e-2)
+
+
 def test_wrappers_reject_mismatched_out(device):
     b = make_prefill(device, 23, [32, 0], [20, 5], T=20, H=2, Hd=64)
     for bad in (torch.empty(2, 2, 19, 64, device=device), torch.empty(2, 2, 20, 64, device=device, dtype=torch.bfloat16),
