@@ -631,7 +631,12 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
 //   13.3 -> 9.6 us (a 128/256 chunk mix), 8 x 8 heads 14.7 -> 12.0 us; fp32 KV 18.3 -> 18.3 us and
 //   21.6 -> 21.2 us on the same two, but 25.6 -> 29.9 us on 8 x 8 heads (1024 workgroups: its 64 KB
 //   of LDS per workgroup allow 2 per CU where the register-staged build fits 4).
-// So: LDS for bf16 KV always, for fp32 KV while the grid fits 2 workgroups per CU.
+// So: LDS for bf16 KV always, for fp32 KV while the grid fits 2 workgroups per CU. Also measured
+// on the LDS staging and not kept: a three-stage ring for bf16 KV (two blocks ahead): 9.6 ->
+// 9.35 us on the chunked workload, 11.7 -> 14.5 us on 8 x 8 heads (48 KB per workgroup, 3 per CU);
+// putting two tiles of the same (request, head) on each compute unit (tiles t and 15 - t, so the
+// pair's second read of a block can hit L1): bf16 9.6 -> 9.4 us, fp32 18.3 -> 20.4 us (the
+// requests' different lengths then unbalance the compute units).
 // PAGED_HIP_PREFILL_STAGING=lds / regs forces one of them (tests cover both).
 static bool prefill_stage_in_lds(bool fp32_kv, unsigned grid) {
   const char* env = getenv("PAGED_HIP_PREFILL_STAGING");
