@@ -22,9 +22,10 @@
 // registers has every 4-lane group of an instruction touching 4 cache lines; the compute unit's L1
 // serves one line per lane group per access, and on the chunked workload with bf16 KV that made
 // the walk L1-bound (11.3 us against 7.7-8.1 us for a copy without the walk's KV loads). At
-// head_dim 64 each wavefront instead copies its blocks' K and V slabs into its own two-stage LDS
-// ring with LDS-direct loads, which read the contiguous slab 16 bytes per lane (one line per lane
-// group), and reads the operands from LDS (prefill_stage_in_lds picks the staging per launch).
+// head_dim 64 (and 128 with bf16 KV) each wavefront instead copies its blocks' K and V slabs into
+// its own two-stage LDS ring with LDS-direct loads, which read the contiguous slab 16 bytes per
+// lane (one line per lane group), and reads the operands from LDS (prefill_stage_in_lds picks the
+// staging per launch).
 //
 // Split-K: when num_splits > 1 each unit's KV blocks are cut into ranges of split_blocks blocks,
 // one workgroup per range. Work items are ordered split-major, so the grid holds many
@@ -425,12 +426,12 @@ void prefill_mfma_kernel(const AttnArgs a) {
     // V rows r and r ^ 1 trade places in every other group of four, so that the two lane groups of
     // a 64-bit read pass land in different bank halves. The loads are untracked by the compiler:
     // the walk waits for them itself (vmcnt), one block ahead.
-    static_assert(HD == 64 && R == 1 && D == 1, "LDS staging: head_dim 64, one block per round and one ahead");
+    static_assert(R == 1 && kRowB <= 256, "LDS staging: one block per round, key rows of at most 256 bytes");
     constexpr int CPR = kRowB / 16;        // 16-byte chunks per row
     constexpr int RPB = 256 / kRowB;       // rows per 256 bytes (one pass over the banks)
     constexpr int NI = kSlab / (16 * kWave);  // LDS-direct instructions per slab
     auto ksw = [](int r) { return (r / RPB) & (CPR - 1); };
-    auto vpos = [](int r) { return kBf16 ? (r ^ ((r >> 2) & 1)) : r; };  // an involution
+    auto vpos = [](int r) { return kRowB == 128 ? (r ^ ((r >> 2) & 1)) : r; };  // an involution
     uint32_t kso[NI], vso[NI];
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
@@ -469,31 +470,23 @@ void prefill_mfma_kernel(const AttnArgs a) {
         const unsigned char* sb = ring + st * 2 * kSlab;
         Tile tt;
         tt.ok = ((okmask >> k) & 1) != 0;
-        if constexpr (kBf16) {
 #pragma unroll
-          for (int s2 = 0; s2 < QD / 8; ++s2) {
-            const int q = G * (QD / 8) + s2;
-            const u32x4 x = *reinterpret_cast<const u32x4*>(sb + c * kRowB + 16 * (q ^ ksw(c)));
+        for (int s2 = 0; s2 < KW / 4; ++s2) {  // K row c, head_dim chunks G * KW / 4 + s2
+          const int q = G * (KW / 4) + s2;
+          const u32x4 x = *reinterpret_cast<const u32x4*>(sb + c * kRowB + 16 * (q ^ ksw(c)));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) tt.k[4 * s2 + e] = x[e];
-          }
+          for (int e = 0; e < 4; ++e) tt.k[4 * s2 + e] = x[e];
+        }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const u32x2 x = *reinterpret_cast<const u32x2*>(sb + kSlab + vpos(4 * G + r) * kRowB + 8 * c);
+        for (int r = 0; r < 4; ++r) {  // V row 4G + r, head_dim [c * DT, c * DT + DT)
+          const unsigned char* vp = sb + kSlab + vpos(4 * G + r) * kRowB + 4 * VW * c;
+          if constexpr (VW == 2) {
+            const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
             tt.v[r][0] = x[0];
             tt.v[r][1] = x[1];
-          }
-        } else {
-#pragma unroll
-          for (int kk = 0; kk < QD / 4; ++kk) {
-            const int q = G * (QD / 4) + kk;
-            const u32x4 x = *reinterpret_cast<const u32x4*>(sb + c * kRowB + 16 * (q ^ ksw(c)));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) tt.k[4 * kk + e] = x[e];
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const u32x4 x = *reinterpret_cast<const u32x4*>(sb + kSlab + (4 * G + r) * kRowB + 16 * c);
+          } else {
+            static_assert(VW == 4, "V words per lane");
+            const u32x4 x = *reinterpret_cast<const u32x4*>(vp);
 #pragma unroll
             for (int e = 0; e < 4; ++e) tt.v[r][e] = x[e];
           }
@@ -631,6 +624,9 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
 //   13.3 -> 9.6 us (a 128/256 chunk mix), 8 x 8 heads 14.7 -> 12.0 us; fp32 KV 18.3 -> 18.3 us and
 //   21.6 -> 21.2 us on the same two, but 25.6 -> 29.9 us on 8 x 8 heads (1024 workgroups: its 64 KB
 //   of LDS per workgroup allow 2 per CU where the register-staged build fits 4).
+// bf16 KV at head_dim 128 (66 KB of LDS, 108 instead of 186 registers): 4 x 32 heads, 256-token
+// chunks over ~1k contexts 99 -> 69-72 us; 2 x 8 heads 9.0 -> 7.8 us; 1 x 32 heads, a 128-token chunk
+// 10.0 -> 8.5 us (fp32 KV at head_dim 128 would need 128 KB per workgroup: registers only).
 // So: LDS for bf16 KV always, for fp32 KV while the grid fits 2 workgroups per CU. Also measured
 // on the LDS staging and not kept: a three-stage ring for bf16 KV (two blocks ahead): 9.6 ->
 // 9.35 us on the chunked workload, 11.7 -> 14.5 us on 8 x 8 heads (48 KB per workgroup, 3 per CU);
@@ -662,7 +658,16 @@ static bool dispatch_prefill_io(const AttnArgs& a, dim3 grid, hipStream_t stream
     prefill_mfma_kernel<KV, IO, 64><<<grid, threads, 0, stream>>>(a);
     return true;
   }
-  if (a.head_dim == 128) { prefill_mfma_kernel<KV, IO, 128><<<grid, threads, 0, stream>>>(a); return true; }
+  if (a.head_dim == 128) {
+    if constexpr (!std::is_same<KV, float>::value) {
+      if (prefill_stage_in_lds(false, grid.x)) {
+        prefill_mfma_kernel<KV, IO, 128, false, true><<<grid, threads, 0, stream>>>(a);
+        return true;
+      }
+    }
+    prefill_mfma_kernel<KV, IO, 128><<<grid, threads, 0, stream>>>(a);
+    return true;
+  }
   return false;
 }
 
@@ -677,27 +682,31 @@ static bool prefill_fast_shape(int32_t head_dim, int32_t block_size) {
 }
 
 // Kernel choice between the wide-tile kernel (128 query rows per workgroup) and the 16-row one, by
-// the wide kernel's unit count U = B * H * ceil(T / 128) against the CU count, graph replay on
-// MI355X (16-row / wide, us):
-//   bf16 KV   U = 256: 102.7 / 49.7 (4 x 32 heads x 128, T 256, ~1k contexts), 172.6 / 75.1
-//             (2 x 32, T 512, ~2k), 278.0 / 111.7 (1 x 32, T 1024, 3k), 61.1 / 30.5 (head_dim 64);
-//             U = 128: 147.3 / 114.4 (2 x 32 x 128, T 256, 3-4k contexts), 19.8 / 20.6 (8 x 8 x 64,
-//             T 256, 0-700 contexts);
-//   fp32 KV   U = 256, head_dim 128: 227.6 / 214.6, 416.6 / 351.3, 688.8 / 556.1; head_dim 64:
-//             112.7 / 132.6; U = 128: 365.1 / 582.0 (head_dim 128), 34.3 / 83.3 (64).
-// So: the wide kernel from U >= 2 CUs always; for bf16 KV from U >= CUs, or U >= CUs / 2 when the
-// page table spans at least 128 blocks (2048-token contexts, the host's bound on the longest
-// request); for fp32 KV at head_dim 128 from U >= CUs. PAGED_HIP_PREFILL_KERNEL=wide / tile forces
-// one of them (tests use it to cover both at small sizes).
-static bool use_wide_prefill(int kv_dtype, int32_t head_dim, int32_t batch, int32_t num_heads, int32_t query_len,
-                             int32_t max_pages) {
+// the wide kernel's unit count U = B * H * ceil(T / 128) against the CU count (256), graph replay on
+// MI355X (16-row / wide, us). bf16 KV, 16-row kernel with its KV staged through LDS:
+//   U = 384: 52.6 / 35.9 (6 x 32 heads x 64, T 256, ~1k contexts);
+//   U = 256: 64.4 / 50.9 (4 x 32 x 128, T 256, ~1k), 95.4 / 63.9 (2 x 32, T 512, ~2k), 136.9 / 98.0
+//            (1 x 32, T 1024, ~3k), 32.7 / 30.3 (4 x 32 x 64, T 256, ~1k);
+//   U = 192: 45.4 / 35.0 (3 x 32 x 128, T 256, ~1k), 113.6 / 97.2 (same, 3-4k), 80.1 / 78.0
+//            (12 x 8 x 128, T 256, ~2k), 99.8 / 84.6 (2 x 32 x 128, T 384, ~3k);
+//   U = 128: 76.6 / 93.4 (2 x 32 x 128, T 256, 3-4k), 12.8 / 18.8 (8 x 8 x 64, T 256, 0-700), 81.3 /
+//            110.5 (4 x 16 x 128, T 256, 3-4k), 52.6 / 70.2 (4 x 32 x 128, T 128, ~2k), 72.2 / 85.4
+//            (1 x 32 x 128, T 512, ~3k);
+//   U = 64:  25.7 / 54.7 (2 x 16 x 128, T 256, ~2k).
+// fp32 KV (16-row kernel with registers at head_dim 128): U = 256, head_dim 128: 227.6 / 214.6,
+//   416.6 / 351.3, 688.8 / 556.1; head_dim 64: 112.7 / 132.6; U = 128: 365.1 / 582.0 (head_dim 128),
+//   34.3 / 83.3 (64).
+// So: the wide kernel from U >= 2 CUs always; for bf16 KV from U >= 3/4 of the CUs; for fp32 KV at
+// head_dim 128 from U >= CUs. PAGED_HIP_PREFILL_KERNEL=wide / tile forces one of them (tests use
+// it to cover both at small sizes).
+static bool use_wide_prefill(int kv_dtype, int32_t head_dim, int32_t batch, int32_t num_heads, int32_t query_len) {
   const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
   if (env != nullptr && strcmp(env, "wide") == 0) return true;
   if (env != nullptr && strcmp(env, "tile") == 0) return false;
   const int64_t units = prefill_wide_units(batch, num_heads, query_len);
   const int64_t cus = pa_host::device_cu_count();
   if (units >= 2 * cus) return true;
-  if (kv_dtype == PA_DTYPE_BF16) return units >= cus || (2 * units >= cus && max_pages >= 128);
+  if (kv_dtype == PA_DTYPE_BF16) return 4 * units >= 3 * cus;
   return head_dim == 128 && units >= cus;
 }
 
@@ -755,7 +764,7 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 
   if (!prefill_fast_shape(head_dim, block_size)) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
   if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
-      use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len, max_pages))
+      use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len))
     return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
 
   const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);

@@ -128,6 +128,23 @@ def test_kv_staging_on_a_large_grid(device, monkeypatch, kv_dtype):
     assert err <= (1e-4 if kv_dtype == torch.float32 else 2e-2)
 
 
+def test_kv_staging_head_dim_128(device, monkeypatch):
+    """bf16 KV at head_dim 128 through the 16-row kernel: LDS and register staging bit-identical and
+    within tolerance of the oracle (2 requests x 16 heads, 256-token chunks over 1-2k contexts)."""
+    b = workloads.large_prefill(seed=7, device=device, batch=2, heads=16, head_dim=128, chunk=256, ctx_lo=1024,
+                                ctx_hi=2048, kv_dtype=torch.bfloat16)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "tile")
+    print("kv staging head_dim 128", flush=True)
+    outs = {}
+    for staging in ("lds", "regs"):
+        monkeypatch.setenv("PAGED_HIP_PREFILL_STAGING", staging)
+        outs[staging] = run(b)
+    assert torch.equal(outs["lds"], outs["regs"])
+    err = max_err(outs["lds"], oracle_out(b))
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= 2e-2
+
+
 def test_wrappers_reject_mismatched_out(device):
     b = make_prefill(device, 23, [32, 0], [20, 5], T=20, H=2, Hd=64)
     for bad in (torch.empty(2, 2, 19, 64, device=device), torch.empty(2, 2, 20, 64, device=device, dtype=torch.bfloat16),
