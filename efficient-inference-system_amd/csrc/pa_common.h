@@ -109,6 +109,20 @@ __device__ __forceinline__ float wave_max(float x) { return group_max<64>(x); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// One LDS-direct load (global_load_lds_dwordx4): lane L reads the 16 bytes at base + voff
+// (bytes) and writes them to LDS at lds + 16L; base and lds are wavefront-uniform. Inline
+// assembly, so the compiler neither tracks it (the caller waits with vm_wait) nor moves memory
+// accesses across it.
+__device__ __forceinline__ void stage_load16(const void* base, uint32_t voff, const void* lds) {
+  const uint32_t m0 = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m0) : "memory");
+}
+// Wait until at most N vector memory loads of this wavefront are outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Number of keys query row i may attend (src/kernels/reference_paged_attention.py:33-42):
 // t <= (L - C) + i and t < L.
 __device__ __forceinline__ int valid_keys(int L, int C, int i) {

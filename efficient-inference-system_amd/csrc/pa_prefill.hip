@@ -176,20 +176,6 @@ constexpr int prefill_depth() {
                                         : (HD == 64 ? PA_PREFILL_DEPTH_BF16_64 : PA_PREFILL_DEPTH_BF16_128);
 }
 
-// One LDS-direct load (global_load_lds_dwordx4): lane L reads the 16 bytes at base + voff
-// (bytes) and writes them to LDS at lds + 16L; base and lds are wavefront-uniform. Inline
-// assembly, so the compiler neither tracks it (the caller waits with vm_wait) nor moves memory
-// accesses across it.
-__device__ __forceinline__ void stage_load16(const void* base, uint32_t voff, const void* lds) {
-  const uint32_t m0 = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds;
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m0) : "memory");
-}
-// Wait until at most N vector memory loads of this wavefront are outstanding.
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // OCC4: registers capped at 128 so that 4 wavefronts share a SIMD (4 workgroups per CU instead of
 // 3). Only fp32 KV at head_dim 64 is near the cap (129 registers unconstrained, 128 and two
 // spilled values capped); the launch takes the capped build when the grid would not fit on the

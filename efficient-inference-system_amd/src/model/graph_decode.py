@@ -28,7 +28,7 @@ list when that state is garbage collected, and the least recently used row is ta
 none is free.
 
 Steps of at most FUSED_STEP_ROWS rows (B * bucketed T: every decode step, and prefill chunks up
-to 384 rows) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
+to 512 rows) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
 shapes allow: per layer one launch for LayerNorm + q/k/v projections + KV append, the attention
 (decode or chunked prefill kernel), one for the output projection + residual, one for LayerNorm +
 fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. A fused launch reads its weight tile
@@ -71,20 +71,21 @@ T_BUCKETS = (16, 32, 64, 128, 256)
 
 # Largest step (rows = B * bucketed T) for which each fused launch beats torch's layers, per
 # dtype. Measured in HIP-graph replay on MI355X (fused vs torch, us), d_model 512, d_ff 2048,
-# vocab 5000:
-#   LayerNorm + q/k/v + append  fp32 8.5 vs 28.9 at 64 rows, 20.4 vs 27.0 at 256, 26.7 vs 27.7 at 384
-#   out_proj + residual         fp32 6.3 vs 8.2 at 256, 8.2 vs 8.3 at 384; bf16 6.2 vs 7.4 at 512
-#   LayerNorm + fc1 + GELU      fp32 14.1 vs 14.3 at 128, 19.3 vs 15.2 at 192; bf16 11.9 vs 13.5 at
-#                               192, 14.8 vs 13.9 at 256
-#   fc2 + residual              fp32 9.4 vs 10.4 at 32, 9.9 vs 9.1 at 48; bf16 6.5 vs 7.8 at 128,
-#                               9.7 vs 8.9 at 192
-#   LayerNorm + lm_head         fp32 11.0 vs 11.7 at 32, 14.3 vs 12.4 at 48; bf16 9.1 vs 10.7 at 48,
-#                               11.2 vs 11.0 at 64
+# vocab 5000, the fused kernels staging their weight and activation slices through LDS:
+#   LayerNorm + q/k/v + append  fp32 6.4 vs 28.7 at 64 rows, 14.7 vs 26.4 at 256, 26.6 vs 28.0 at 512;
+#                               bf16 19.4 vs 23.2 at 512
+#   out_proj + residual         fp32 7.0 vs 8.7 at 512; bf16 4.5 vs 7.3 at 512
+#   LayerNorm + fc1 + GELU      fp32 10.6 vs 13.9 at 128, 15.2 vs 14.8 at 192; bf16 10.8 vs 13.3 at
+#                               192, 13.6 vs 13.7 at 256
+#   fc2 + residual              fp32 8.5 vs 9.0 at 96, 9.2 vs 9.1 at 128; bf16 6.8 vs 8.2 at 256,
+#                               9.3 vs 8.9 at 384
+#   LayerNorm + lm_head         fp32 10.7 vs 11.8 at 48, 15.8 vs 11.8 at 64; bf16 9.1 vs 10.4 at 64,
+#                               13.6 vs 11.2 at 96
 FUSED_ROWS = {
-    torch.float32: {"qkv": 384, "out_proj": 384, "fc1": 128, "fc2": 32, "lm_head": 32},
-    torch.bfloat16: {"qkv": 384, "out_proj": 384, "fc1": 192, "fc2": 128, "lm_head": 48},
+    torch.float32: {"qkv": 512, "out_proj": 512, "fc1": 128, "fc2": 96, "lm_head": 48},
+    torch.bfloat16: {"qkv": 512, "out_proj": 512, "fc1": 192, "fc2": 256, "lm_head": 64},
 }
-FUSED_STEP_ROWS = 384  # steps above this run the torch layers (q/k/v and out_proj limits)
+FUSED_STEP_ROWS = 512  # steps above this run the torch layers (q/k/v and out_proj limits)
 
 
 def graphs_enabled() -> bool:

@@ -305,3 +305,35 @@ def test_linear_select_rows_rejects_bad_arguments(device):
         hip_linear.linear_select_rows_hip(x, 4, rows.cpu(), lin)
     with pytest.raises(ValueError):
         hip_linear.linear_select_rows_hip(x, 4, rows, lin, out=torch.empty(3, 32, device=device))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("K", [128, 256, 512, 1024, 2048])
+@pytest.mark.parametrize("M,N", [(1, 300), (5, 40), (8, 1536), (16, 5000)])
+def test_linear_lds_staging_matches_registers(device, monkeypatch, dtype, K, M, N):
+    """One-tile launches (<= 16 rows) stage their weight and activation slices through LDS: the
+    same products in the same order as loading the operands straight into registers, so the
+    outputs are bit-identical (LayerNorm + GELU + residual, narrow and wide layers, and the
+    row-selecting head over strided groups)."""
+    torch.manual_seed(K + M + N)
+    lin = nn.Linear(K, N).to(device, dtype)
+    ln = nn.LayerNorm(K).to(device, dtype)
+    with torch.no_grad():
+        ln.weight.uniform_(0.5, 1.5)
+        ln.bias.uniform_(-0.2, 0.2)
+    x = torch.randn(M, K, device=device, dtype=dtype)
+    res = torch.randn(M, N, device=device, dtype=dtype)
+    xs = torch.randn(M * 7, K, device=device, dtype=dtype)  # M groups of 7 rows
+    rows = torch.tensor([(3 * g) % 7 - (g % 2) * 7 for g in range(M)], dtype=torch.int32, device=device)
+    print(f"linear staging dtype={dtype} K={K} M={M} N={N}", flush=True)
+    outs = {}
+    for staging in ("lds", "regs"):
+        if staging == "regs":
+            monkeypatch.setenv("PAGED_HIP_LINEAR_STAGING", "regs")
+        outs[staging] = (hip_linear.linear_rows_hip(x, lin),
+                         hip_linear.linear_rows_hip(x, lin, ln=ln, gelu=True, residual=res),
+                         hip_linear.linear_select_rows_hip(xs, 7, rows, lin, ln=ln))
+    for a, b in zip(outs["lds"], outs["regs"]):
+        assert torch.equal(a, b)
+    err = (outs["lds"][1].double().cpu() - ref_linear(x, lin, ln=ln, gelu=True, residual=res)).abs().max().item()
+    assert err <= (2e-5 if dtype == torch.float32 else 0.1)
