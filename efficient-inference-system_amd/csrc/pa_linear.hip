@@ -61,7 +61,25 @@ struct LinArgs {
   int32_t cw_log2;    // output columns per workgroup: 1 << cw_log2 (4, 8 or 16)
   const int32_t* row_sel;  // when set: row m of the product is x row m * sel_group + row_sel[m]
   int32_t sel_group;       // (a negative entry counts from the group's end; clamped into the group)
+  unsigned long long* token_keys;  // when set: per row, the running minimum of token_key over the
+                                   // row's outputs (the row's greedy token in the low 32 bits)
 };
+
+// Greedy selection folded into a layer's epilogue: a key whose minimum over a row's columns picks
+// what torch.argmax picks on the row as stored (value rounded to the output type): the largest
+// value, NaN above every number, -0.0 equal to +0.0, and the lowest column among equals. High
+// word: the bitwise complement of the value's order-preserving bits; low word: the column.
+__device__ __forceinline__ unsigned long long token_key(float v, int n) {
+  uint32_t b = __float_as_uint(v);
+  uint32_t ord;
+  if (v != v) {
+    ord = 0xffffffffu;
+  } else {
+    if (v == 0.f) b = 0u;
+    ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return ((unsigned long long)(~ord) << 32) | (uint32_t)n;
+}
 
 // The x row that product row m reads.
 __device__ __forceinline__ int64_t lin_x_row(const LinArgs& a, int m) {
@@ -305,12 +323,30 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   __syncthreads();
 
   // ---- epilogue: one thread per (row, column) of the tile --------------------------------------
-  if (!live) return;
+  const bool keyed = a.token_keys != nullptr;  // uniform
+  if (!live && (!keyed || (int)threadIdx.x >= (kLinRows << a.cw_log2))) return;  // whole wavefronts past the tile
   float v = 0.f;
+  if (live) {
 #pragma unroll
-  for (int ww = 0; ww < kLinWaves; ++ww) v += sm_part[ww][ml][cc];
-  v += bias_v;
-  if (a.act == 1) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+    for (int ww = 0; ww < kLinWaves; ++ww) v += sm_part[ww][ml][cc];
+    v += bias_v;
+    if (a.act == 1) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+  }
+  if (keyed) {
+    // The row's cw threads are consecutive lanes: reduce their keys, one atomic per row.
+    unsigned long long key = ~0ull;
+    if (live) {
+      float vr = v + res_v;
+      if constexpr (BF) vr = bf16_to_f32(f32_to_bf16(vr));
+      key = token_key(vr, n);
+    }
+    for (int off = 1; off < cw; off <<= 1) {
+      const unsigned long long o = __shfl_xor(key, off);
+      key = o < key ? o : key;
+    }
+    if (cc == 0 && m < a.M) __hip_atomic_fetch_min(a.token_keys + m, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!live) return;
+  }
   if (a.k_pool != nullptr && seg > 0) {
     const int slot = a.slots[m];
     const int64_t blk = slot >= 0 ? slot / a.bs : -1;
@@ -469,7 +505,7 @@ extern "C" int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t gr
                                      const int32_t* row_index, int32_t in_features, const void* weight,
                                      const void* bias, int32_t out_features, const void* ln_weight,
                                      const void* ln_bias, float ln_eps, int32_t activation, void* out,
-                                     int64_t out_stride, int dtype, void* stream) {
+                                     int64_t out_stride, uint64_t* token_keys, int dtype, void* stream) {
   pa_host::clear_error();
   PA_CHECK_ARG(groups >= 0 && groups <= kLinMaxRows, "groups must be in [0, %d], got %d", kLinMaxRows, groups);
   PA_CHECK_ARG(group_rows > 0, "group_rows must be positive, got %d", group_rows);
@@ -490,6 +526,8 @@ extern "C" int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t gr
   a.act = activation; a.res = nullptr; a.res_stride = 0;
   a.out = out; a.out_stride = out_stride; a.bf16 = dtype == PA_DTYPE_BF16;
   a.row_sel = row_index; a.sel_group = group_rows;
+  PA_CHECK_ARG((reinterpret_cast<uintptr_t>(token_keys) & 7) == 0, "token_keys must be 8-byte aligned");
+  a.token_keys = reinterpret_cast<unsigned long long*>(token_keys);
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
 }
 

@@ -2,7 +2,7 @@
 
   linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
   linear_select_rows_hip  the same without residual for one selected row per group of rows
-                   (a step's greedy rows)                                    (pa_linear_select_rows)
+                   (a step's greedy rows), optionally with the greedy argmax  (pa_linear_select_rows)
   qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
                    one launch; returns q                                     (pa_qkv_append)
   embed_rows_hip   token + clamped position embedding of a [B, T] step       (pa_embed_rows)
@@ -86,10 +86,14 @@ def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | No
 
 def linear_select_rows_hip(x: torch.Tensor, group_rows: int, row_index: torch.Tensor, linear: nn.Linear, *,
                            ln: nn.LayerNorm | None = None, gelu: bool = False,
-                           out: torch.Tensor | None = None) -> torch.Tensor:
+                           out: torch.Tensor | None = None, token_keys: torch.Tensor | None = None) -> torch.Tensor:
     """out[g] = act(LN(x[g * group_rows + r_g]) W^T + b) with r_g = row_index[g] (negative values
     count from the group's end; clamped into the group), for the len(row_index) groups of rows of
-    x; x, the layer's parameters and out share one dtype (float32 or bfloat16)."""
+    x; x, the layer's parameters and out share one dtype (float32 or bfloat16).
+
+    token_keys (int64 [groups] device tensor holding -1, i.e. all bits set): the same launch folds
+    in each group's greedy token; afterwards token_keys.view(torch.int32)[0::2] holds
+    torch.argmax(out[g]) per group (see token_keys_to_tokens)."""
     _rows(x, "x")
     dt = x.dtype
     M, K = x.shape
@@ -109,15 +113,24 @@ def linear_select_rows_hip(x: torch.Tensor, group_rows: int, row_index: torch.Te
     _rows(out, "out", dt)
     if out.shape[0] < groups or out.shape[1] != N:
         raise ValueError(f"out must hold {groups} rows of {N} features")
+    if token_keys is not None and (token_keys.dtype != torch.int64 or token_keys.dim() != 1 or token_keys.numel() < groups
+                                   or token_keys.stride(0) != 1 or token_keys.device != x.device):
+        raise ValueError("token_keys must be a unit-stride int64 [groups] tensor on x's device")
     status = _lib.load().pa_linear_select_rows(
         x.data_ptr(), x.stride(0), groups, group_rows, row_index.data_ptr(), K,
         linear.weight.data_ptr(), _ptr(linear.bias), N,
         _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
         float(ln.eps) if ln is not None else 0.0,
-        1 if gelu else 0, out.data_ptr(), out.stride(0), _lib.dtype_code(dt), _stream(x.device),
+        1 if gelu else 0, out.data_ptr(), out.stride(0), _ptr(token_keys), _lib.dtype_code(dt), _stream(x.device),
     )
     _lib.check(status, "pa_linear_select_rows")
     return out
+
+
+def token_keys_to_tokens(token_keys: torch.Tensor) -> torch.Tensor:
+    """The greedy tokens folded into token_keys by linear_select_rows_hip: the low 32-bit word of
+    each key (a strided int32 view, no copy)."""
+    return token_keys.view(torch.int32)[0::2]
 
 
 def qkv_append_hip(x: torch.Tensor, ln: nn.LayerNorm, attn, k_pool: torch.Tensor, v_pool: torch.Tensor,

@@ -266,15 +266,21 @@ class _Captured:
                  tokens_only: bool = False):
         H, Hd = model.num_heads, model.head_dim
         self.B, self.Tb, self.pages = B, Tb, pages
+        # A graph whose callers take only the tokens computes ln_f + lm_head for each request's
+        # greedy row alone (the other rows' logits are never read), with the argmax folded into
+        # that launch (token keys, reset to all ones by the staging copy of every step).
+        self.select_head = tokens_only and hip_linear.model_supported(model)
         # Step descriptor (int32 words of pinned host memory the device reads):
-        #   [ids int64 B*Tb | first positions int64 B | current lengths B | greedy rows B]
+        #   [ids int64 B*Tb | first positions int64 B | current lengths B | greedy rows B |
+        #    token keys int64 B, all ones (select_head only)]
         #     staged into the device buffer `stage` by the metadata launch;
         #   [mirror rows B | first changed page B | list lengths B | lengths before B | appended B |
         #    update ids, mirror width words per request]  read by that launch in place.
         o_pos = 2 * B * Tb
         o_cur = o_pos + 2 * B
         o_sel = o_cur + B
-        self.stage_words = o_sel + B
+        o_key = o_sel + B  # even: the keys are 8-byte aligned in `stage`
+        self.stage_words = o_key + (2 * B if self.select_head else 0)
         o_mrow = self.stage_words
         o_first, o_npages = o_mrow + B, o_mrow + 2 * B
         o_prev = o_npages + B
@@ -283,6 +289,7 @@ class _Captured:
         self.layout = (o_cur, o_sel, o_mrow, o_first, o_npages, o_prev, o_app, o_upd, mirror_width)
         self.desc = MappedHostWords(o_upd + B * mirror_width, device)
         w = self.desc.words
+        w[o_key:self.stage_words] = -1
         self.ids_host = w[0:o_pos].view(np.int64).reshape(B, Tb)
         self.pos_host = w[o_pos:o_cur].view(np.int64)
         addr = self.desc.device_addr
@@ -294,7 +301,12 @@ class _Captured:
         self.pos = self.stage[o_pos:o_cur].view(torch.int64)
         self.cur = self.stage[o_cur:o_sel]
         self.rows = self.stage[o_sel:o_sel + B]
-        self.tokens = torch.zeros((B,), dtype=torch.int64, device=device)
+        if self.select_head:
+            self.keys = self.stage[o_key:self.stage_words].view(torch.int64)
+            self.tokens = hip_linear.token_keys_to_tokens(self.keys)
+        else:
+            self.keys = None
+            self.tokens = torch.zeros((B,), dtype=torch.int64, device=device)
         self.last_sel: list[int] = [0] * B
         lib = _lib.load()
         if Tb == 1:
@@ -311,9 +323,6 @@ class _Captured:
         self.embed_fused = (fused_decode_enabled() and emb_dt in hip_linear.DTYPES
                             and model.pos_emb.weight.dtype == emb_dt
                             and model.token_emb.embedding_dim % (4 if emb_dt == torch.float32 else 8) == 0)
-        # A graph whose callers take only the tokens computes ln_f + lm_head for each request's
-        # greedy row alone (the other rows' logits are never read).
-        self.select_head = tokens_only and hip_linear.model_supported(model)
         self.signature = _signature(pools)
         self.graph = None
         self.logits = None
@@ -376,9 +385,7 @@ class GraphedStep:
         else:
             x = self._torch_layers(cap, pools, x, pt, seq32, slots).reshape(B * Tb, -1)
         if cap.select_head:
-            logits = hip_linear.linear_select_rows_hip(x, Tb, cap.rows, m.lm_head, ln=m.ln_f)
-            argmax_rows_hip(logits.view(B, 1, -1), None, out=cap.tokens)
-            return logits
+            return hip_linear.linear_select_rows_hip(x, Tb, cap.rows, m.lm_head, ln=m.ln_f, token_keys=cap.keys)
         if cap.fused and B * Tb <= FUSED_ROWS[x.dtype]["lm_head"]:
             logits = hip_linear.linear_rows_hip(x, m.lm_head, ln=m.ln_f)
         else:
@@ -478,8 +485,8 @@ class GraphedStep:
         current_lengths, before clamping); rows: per request, the logits row whose argmax becomes
         its token (None: row 0; the tokens then mean nothing).
         Returns (logits [B, T, vocab] or None when want_logits is False, tokens): tokens is an
-        int64 [B] device tensor owned by the graph, overwritten by the next step of this batch
-        size and bucket. The caller checks ids and positions first (the model's
+        integer [B] device tensor owned by the graph (int64; int32 when the argmax is folded into
+        the head's launch), overwritten by the next step of this batch size and bucket. The caller checks ids and positions first (the model's
         check_token_inputs), before any cache state changes."""
         m = self.model
         B, T = input_ids.shape

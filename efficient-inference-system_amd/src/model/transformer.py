@@ -264,11 +264,12 @@ class TinyTransformerLM(nn.Module):
         current_lengths: as forward() (None, int, tensor) or a host list;
         select_rows: per request, the logits row whose argmax is its next token (default: its last
         real row, current_lengths - 1; negative rows count from the end as torch indexing does).
-        Returns (tokens, logits, caches): tokens int64 [B] on the model's device (on the graph
-        path a buffer the next step of the same shape overwrites: read it before that), logits
+        Returns (tokens, logits, caches): tokens an integer [B] tensor on the model's device
+        (int64; on the graph path a buffer the next step of the same shape overwrites, read it
+        before that: int32 when the argmax is folded into the lm_head launch), logits
         [B, T, vocab] when return_logits else None, and the per-layer caches as forward() returns
         them. On the hip_paged backend with batched caches the step replays a captured graph
-        whose last kernel is the argmax, so only the token ids need to leave the device."""
+        that ends in the greedy selection, so only the token ids need to leave the device."""
         B, T = input_ids.shape
         cur = self._host_lengths(current_lengths, B, T)
         rows = list(select_rows) if select_rows is not None else [c - 1 for c in cur]

@@ -337,3 +337,47 @@ def test_linear_lds_staging_matches_registers(device, monkeypatch, dtype, K, M, 
         assert torch.equal(a, b)
     err = (outs["lds"][1].double().cpu() - ref_linear(x, lin, ln=ln, gelu=True, residual=res)).abs().max().item()
     assert err <= (2e-5 if dtype == torch.float32 else 0.1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", ["plain", "ties", "zeros", "nan"])
+def test_linear_select_rows_folds_the_argmax(device, dtype, case):
+    """pa_linear_select_rows with token_keys: the low word of each group's key is torch.argmax of
+    the group's output row as stored (first index of the maximum; -0.0 == +0.0; the first NaN
+    wins), the outputs themselves unchanged; exact ties planted by duplicated weight rows."""
+    torch.manual_seed(11)
+    K, N, groups, rows = 512, 5000, 6, 9
+    lin = nn.Linear(K, N).to(device, dtype)
+    ln = nn.LayerNorm(K).to(device, dtype)
+    with torch.no_grad():
+        if case == "ties":
+            for dst, src in ((4000, 17), (4001, 17), (10, 4999)):  # same column values -> exact ties
+                lin.weight[dst] = lin.weight[src]
+                lin.bias[dst] = lin.bias[src]
+            lin.bias[17] += 50.0
+            lin.bias[4000] += 50.0
+            lin.bias[4001] += 50.0  # columns 17, 4000 and 4001 tie at the top: 17 wins
+        if case == "zeros":
+            lin.weight.zero_()
+            lin.bias.copy_(-torch.rand(N, device=device).to(dtype) - 1.0)
+            lin.bias[3000] = -0.0
+            lin.bias[200] = 0.0  # +0.0 (column 200) and -0.0 (column 3000) tie at the top: 200 wins
+        if case == "nan":
+            lin.bias[2500] = float("nan")
+            lin.bias[4100] = float("nan")  # the first NaN column wins
+    x = torch.randn(groups * rows, K, device=device, dtype=dtype)
+    idx = torch.tensor([r % rows - (r % 2) * rows for r in range(groups)], dtype=torch.int32, device=device)
+    keys = torch.full((groups,), -1, dtype=torch.int64, device=device)
+    print(f"folded argmax dtype={dtype} case={case}", flush=True)
+    out = hip_linear.linear_select_rows_hip(x, rows, idx, lin, ln=ln, token_keys=keys)
+    plain = hip_linear.linear_select_rows_hip(x, rows, idx, lin, ln=ln)
+    assert torch.equal(out, plain) if case != "nan" else torch.equal(out.isnan(), plain.isnan())
+    tokens = hip_linear.token_keys_to_tokens(keys).tolist()
+    want = torch.argmax(plain.float().cpu(), dim=1).tolist()
+    assert tokens == want
+    if case == "ties":
+        assert want == [17] * groups
+    if case == "zeros":
+        assert want == [200] * groups
+    if case == "nan":
+        assert want == [2500] * groups
