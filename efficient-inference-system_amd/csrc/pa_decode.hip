@@ -290,7 +290,11 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
 }
 
 // Merge the partial records (m, l, acc[HD]) of each (request, head) written by its active splits
-// (the number a split computes from the request's length): one wavefront per pair. The loads are
+// (the number a split computes from the request's length): one wavefront per pair. (A merge in
+// the split launch itself, by the split that completes a per-pair counter after an agent-scope
+// release, was measured and dropped: the fences made the small ragged decode, 8 x 8 heads x 64
+// over 128-1024 keys, take 12.4 / 19.2 / 33.4 us per layer at 32 / 16 / 8-block splits, against
+// 10.2 / 8.4 / 8.4 us with this second launch and 8.4 us unsplit.) The loads are
 // spread over the lanes and issued together: lane s reads split s's (m, l) for the maximum and
 // the denominator, and each lane's head_dim element is summed over the splits with the weights
 // broadcast from the lane that computed them, eight independent loads at a time. (A loop over
