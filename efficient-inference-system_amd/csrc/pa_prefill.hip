@@ -190,16 +190,20 @@ void prefill_mfma_kernel(const AttnArgs a) {
   constexpr int QD = Sh::QD, DT = Sh::DT, KW = Sh::KW, VW = Sh::VW;
   constexpr bool kBf16 = Sh::kBf16;
 
-  // Per wavefront: its merge rows (16 x (HD + 1) floats) and, with LDSK, a two-stage ring of
-  // (K slab, V slab) the merge rows reuse after the walk.
+  // Per wavefront: its merge rows (16 x (HD + 4) floats: 16-byte aligned rows whose stride is one
+  // 16-byte bank group past a multiple of 128 bytes, so 8 consecutive rows of a 16-byte access
+  // hit distinct banks) and, with LDSK, a two-stage ring of (K slab, V slab) the merge rows reuse
+  // after the walk.
   constexpr int kRowB = HD * (int)sizeof(KV);  // bytes of one key row
   constexpr int kSlab = BS * kRowB;            // bytes of one (block, head) K or V slab
-  constexpr int kOB = 16 * (HD + 1) * 4;
+  constexpr int kOS = HD + 4;                  // floats per merge row
+  constexpr int kOB = 16 * kOS * 4;
   constexpr int kWaveB = LDSK ? (4 * kSlab > kOB ? 4 * kSlab : kOB) : kOB;
+  static_assert(NW * kWave == 16 * 16, "merge: 16 threads per query column");
   __shared__ __attribute__((aligned(16))) unsigned char smem[NW * kWaveB];
   __shared__ float sm_m[NW][16];
   __shared__ float sm_l[NW][16];
-  auto sm_o = [&](int ww, int cc) -> float* { return reinterpret_cast<float*>(smem + ww * kWaveB) + cc * (HD + 1); };
+  auto sm_o = [&](int ww, int cc) -> float* { return reinterpret_cast<float*>(smem + ww * kWaveB) + cc * kOS; };
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -529,11 +533,23 @@ void prefill_mfma_kernel(const AttnArgs a) {
   }
 
   // ---- merge the wavefronts' states ---------------------------------------------------------
+  // Lane (G, c) holds head_dim d = (4G + r) * DT + t of query column c in oacc[t][r]: for each r
+  // the DT values over t are consecutive, so they go to LDS as DT / 4 16-byte vectors. Then 16
+  // threads per column combine the wavefronts' states, each over DT consecutive head_dim values,
+  // in one pass. (The earlier loop over 16 * HD / 256 outputs per thread, each with its own scalar
+  // LDS reads and max / exp chain, took 1.1-1.7 us per wavefront after the barrier; this one
+  // 0.5-0.7 us. Graph replay: chunked workload bf16 KV 10.0 -> 9.2 us, fp32 19.2 -> 18.3 us.)
+  // Measured and not kept: moving the q loads ahead of the inactive-split return and making all
+  // argument loads go out in one batch, which brings q, the lengths and the page-table chunk ~0.3
+  // us earlier: fp32 unchanged, bf16 KV 9.2 -> 9.4-9.7 us (the wavefronts of a (request, head)
+  // then request its first blocks more nearly at once).
   l = sum_xor32(sum_xor16(l));
 #pragma unroll
-  for (int t = 0; t < DT; ++t)
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sm_o(w, c)[(4 * G + r) * DT + t] = oacc[t][r];
+    for (int t4 = 0; t4 < DT / 4; ++t4)
+      *reinterpret_cast<f32x4*>(sm_o(w, c) + (4 * G + r) * DT + 4 * t4) =
+          f32x4{oacc[4 * t4][r], oacc[4 * t4 + 1][r], oacc[4 * t4 + 2][r], oacc[4 * t4 + 3][r]};
   if (G == 0) {
     sm_m[w][c] = m;
     sm_l[w][c] = l;
@@ -541,31 +557,40 @@ void prefill_mfma_kernel(const AttnArgs a) {
   __syncthreads();
 
   const int rows = a.T - i0 < 16 ? a.T - i0 : 16;
-  float* rec0 = nullptr;
-  if (nact > 1) rec0 = a.ws + ((int64_t)unit * a.num_splits) * 16 * (HD + 2);
-  for (int idx = threadIdx.x; idx < rows * HD; idx += NW * kWave) {
-    const int cc = idx / HD;
-    const int d = idx - cc * HD;
+  const int cc = threadIdx.x >> 4;
+  const int d0 = (threadIdx.x & 15) * DT;
+  if (cc < rows) {
     float M = kNegBig;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_m[ww][cc]);
-    float lsum = 0.f, A = 0.f;
+    float lsum = 0.f;
+    float A[DT];
+#pragma unroll
+    for (int e = 0; e < DT; ++e) A[e] = 0.f;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
       const float f = fast_exp2(sm_m[ww][cc] - M);
       lsum = fmaf(sm_l[ww][cc], f, lsum);
-      A = fmaf(sm_o(ww, cc)[d], f, A);
+#pragma unroll
+      for (int t4 = 0; t4 < DT / 4; ++t4) {
+        const f32x4 o = *reinterpret_cast<const f32x4*>(sm_o(ww, cc) + d0 + 4 * t4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) A[4 * t4 + e] = fmaf(o[e], f, A[4 * t4 + e]);
+      }
     }
     if (nact == 1) {
-      IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(i0 + cc) * a.o_st;
-      Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
+      IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(i0 + cc) * a.o_st + d0;
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+      for (int e = 0; e < DT; ++e) Elem<IO>::store(op + e, lsum > 0.f ? A[e] * inv : 0.f);
     } else {
-      float* rec = rec0 + ((int64_t)split * 16 + cc) * (HD + 2);
-      if (d == 0) {
+      float* rec = a.ws + (((int64_t)unit * a.num_splits + split) * 16 + cc) * (HD + 2);
+      if (d0 == 0) {
         rec[0] = M;
         rec[1] = lsum;
       }
-      rec[2 + d] = A;
+#pragma unroll
+      for (int e = 0; e < DT; ++e) rec[2 + d0 + e] = A[e];
     }
   }
 }
@@ -618,7 +643,12 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
 // 9.35 us on the chunked workload, 11.7 -> 14.5 us on 8 x 8 heads (48 KB per workgroup, 3 per CU);
 // putting two tiles of the same (request, head) on each compute unit (tiles t and 15 - t, so the
 // pair's second read of a block can hit L1): bf16 9.6 -> 9.4 us, fp32 18.3 -> 20.4 us (the
-// requests' different lengths then unbalance the compute units).
+// requests' different lengths then unbalance the compute units); two adjacent 16-row tiles per
+// wavefront in 8-wavefront workgroups of 32 rows, each staged block folded into both tiles (two
+// independent MFMA and softmax chains, half the block walks per wavefront at the same wavefronts
+// per SIMD; parity green): bf16 9.5 -> 10.2 us (chunked), 9.6 -> 10.1 (128/256 mix), 11.6 -> 14.1
+// (8 x 8 heads), 4.8 -> 6.8 (2 x 8 heads, 64 rows); fp32 18.5 -> 22.5, 20.8 -> 21.3, 24.5 -> 24.4,
+// 6.1 -> 9.3, so the walk is not bound by its per-block memory round trips either.
 // PAGED_HIP_PREFILL_STAGING=lds / regs forces one of them (tests cover both).
 static bool prefill_stage_in_lds(bool fp32_kv, unsigned grid) {
   const char* env = getenv("PAGED_HIP_PREFILL_STAGING");
