@@ -160,8 +160,15 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int nsplit = a.num_splits;
-  const int units = a.H * nsplit;  // workgroups per request
+  // The argument block spans three 64-byte lines. Left alone, the compiler loads the sizes the
+  // work-unit arithmetic needs, waits, and loads the lines with the pointers afterwards: a second
+  // dependent round trip before the first global load. The sizes pass through this statement
+  // together with the other prologue arguments, so all argument loads go out at once.
+  int nsplit = a.num_splits, nH = a.H, nB = a.B;
+  asm volatile("" : "+s"(nsplit), "+s"(nH), "+s"(nB)
+               : "s"(a.q), "s"(a.q_sb), "s"(a.q_sh), "s"(a.page_table), "s"(a.pt_stride), "s"(a.max_pages),
+                 "s"(a.seq_lens), "s"(a.cur_lens), "s"(a.order), "s"(a.k_pool), "s"(a.v_pool), "s"(a.split_blocks));
+  const int units = nH * nsplit;  // workgroups per request
   int bi, u;
 #if PA_DECODE_XCD
   // Keep all workgroups of a request on one die: workgroup x runs on die x % kXcds, so request
@@ -173,7 +180,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
     const int slot = x / kXcds;
     bi = (slot / units) * kXcds + die;
     u = slot % units;
-    if (bi >= a.B) return;
+    if (bi >= nB) return;
   }
 #else
   bi = blockIdx.x / units;
@@ -198,6 +205,16 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
 
   const int L = a.seq_lens[b];
   const int C = a.cur_lens[b];
+  // q is loaded before the inactive-split return below (a branch the loads could not be moved
+  // across), so it travels with the page-table and length loads.
+  const int r = lane % LPR;
+  const int g = lane / LPR;
+  float qv[EPL];
+  {
+    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + r * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[e] = Elem<IO>::load(qp + e) * a.scale_log2;
+  }
   const int n = valid_keys(L, C, 0);
   int nb = (n + BS - 1) / BS;
   nb = nb < a.max_pages ? nb : a.max_pages;
@@ -209,15 +226,6 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
     je = jb + a.split_blocks < nb ? jb + a.split_blocks : nb;
   }
 
-  const int r = lane % LPR;
-  const int g = lane / LPR;
-
-  float qv[EPL];
-  {
-    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + r * EPL;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[e] = Elem<IO>::load(qp + e) * a.scale_log2;
-  }
 
   float m = kNegBig, l = 0.f;
   float acc[EPL];

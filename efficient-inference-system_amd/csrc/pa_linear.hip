@@ -162,14 +162,25 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   const int G = lane >> 4;
   const int c = lane & 15;
 
+  // The argument block spans four 64-byte lines. Left alone, the compiler loads the sizes the
+  // tile arithmetic needs, waits, then loads the segment's weight pointer (an indexed load, a
+  // second round trip) and the activation pointer (a third) before the first global load. The
+  // sizes and the three weight pointers pass through this statement together with the other
+  // arguments the loads below need, so all argument loads go out at once.
+  int cwl = a.cw_log2, segn = a.seg_n;
+  const void *w0 = a.w[0], *w1 = a.w[1], *w2 = a.w[2];
+  asm volatile("" : "+s"(cwl), "+s"(segn), "+s"(w0), "+s"(w1), "+s"(w2)
+               : "s"(a.x), "s"(a.x_stride), "s"(a.M), "s"(a.K), "s"(a.row_sel), "s"(a.sel_group), "s"(a.ln_w),
+                 "s"(a.ln_b), "s"(a.res), "s"(a.res_stride), "s"(a.b[0]), "s"(a.b[1]), "s"(a.b[2]));
+
   // CW = 1 << cw_log2 output columns per workgroup (16, or 8 / 4 to spread a narrow layer over more
   // compute units: a launch is limited by how fast each workgroup can pull its weight tile); the
   // MFMA tile is always 16 wide, lanes c >= CW carry zero weights and load nothing.
-  const int cw = 1 << a.cw_log2;
-  const int tiles_per_seg = (a.seg_n + cw - 1) >> a.cw_log2;
+  const int cw = 1 << cwl;
+  const int tiles_per_seg = (segn + cw - 1) >> cwl;
   const int seg = blockIdx.x / tiles_per_seg;
-  const int n0 = (blockIdx.x - seg * tiles_per_seg) << a.cw_log2;
-  const T* W = static_cast<const T*>(a.w[seg]);
+  const int n0 = (blockIdx.x - seg * tiles_per_seg) << cwl;
+  const T* W = static_cast<const T*>(seg == 0 ? w0 : (seg == 1 ? w1 : w2));
   const int kb = w * KW + G * KL;
   const int r0 = blockIdx.y * kLinRows;  // first activation row of this workgroup
   const bool row_ok = r0 + c < a.M;
