@@ -50,6 +50,7 @@ template <> struct Elem<uint16_t> {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Unpack one 16-byte vector into EPL floats.
 template <typename T> struct Vec16;

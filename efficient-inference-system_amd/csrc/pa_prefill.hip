@@ -103,9 +103,18 @@ struct PrefillShape {
 // 0.4 us either way on single requests. bf16 KV: 12.3-12.7 us with 4, 13.4-13.8 with 8, 19.0 with
 // 16 (chunked workload), 99 against 128 us with 8 (4 x 32 heads x 128). Measured again on the current
 // kernel (three wavefronts per SIMD fit its registers at 6 per workgroup): 5 and 6 wavefronts, fp32
-// KV 21.5-21.6 and 22.1-22.4 us against 18.3; bf16 12.2 and 12.5-12.7 against 11.4-11.5.
+// KV 21.5-21.6 and 22.1-22.4 us against 18.3; bf16 12.2 and 12.5-12.7 against 11.4-11.5. With the
+// KV staged through LDS and the one-pass merge, 8 wavefronts for bf16 KV (4 per SIMD at 2
+// workgroups per CU): chunked 9.2 -> 9.6 us, 128/256 mix 9.4 -> 10.6, 8 x 8 heads 11.4 -> 15.3,
+// 4 x 32 heads x 128 58 -> 71, only 2 x 8 heads x 128 14.3 -> 12.4.
+#ifndef PA_PREFILL_WAVES_F32
+#define PA_PREFILL_WAVES_F32 4
+#endif
+#ifndef PA_PREFILL_WAVES_BF16
+#define PA_PREFILL_WAVES_BF16 4
+#endif
 template <typename KV>
-constexpr int prefill_waves() { return 4; }
+constexpr int prefill_waves() { return std::is_same<KV, float>::value ? PA_PREFILL_WAVES_F32 : PA_PREFILL_WAVES_BF16; }
 
 // KV tiles each wavefront keeps in flight ahead of the one it folds. Measured in graph replay
 // (16-row kernel): at head_dim 64 one tile is best (chunked workload 4 x 8 heads, bf16 KV 13.6 us
@@ -199,7 +208,9 @@ void prefill_mfma_kernel(const AttnArgs a) {
   constexpr int kOS = HD + 4;                  // floats per merge row
   constexpr int kOB = 16 * kOS * 4;
   constexpr int kWaveB = LDSK ? (4 * kSlab > kOB ? 4 * kSlab : kOB) : kOB;
-  static_assert(NW * kWave == 16 * 16, "merge: 16 threads per query column");
+  constexpr int TPC = NW * kWave / 16;  // merge: threads per query column
+  constexpr int VPT = HD / TPC;         // merge: consecutive head_dim values per thread
+  static_assert(HD % TPC == 0 && (VPT == 2 || VPT % 4 == 0), "merge: whole 8- or 16-byte pieces per thread");
   __shared__ __attribute__((aligned(16))) unsigned char smem[NW * kWaveB];
   __shared__ float sm_m[NW][16];
   __shared__ float sm_l[NW][16];
@@ -557,32 +568,38 @@ void prefill_mfma_kernel(const AttnArgs a) {
   __syncthreads();
 
   const int rows = a.T - i0 < 16 ? a.T - i0 : 16;
-  const int cc = threadIdx.x >> 4;
-  const int d0 = (threadIdx.x & 15) * DT;
+  const int cc = threadIdx.x / TPC;
+  const int d0 = (threadIdx.x % TPC) * VPT;
   if (cc < rows) {
     float M = kNegBig;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_m[ww][cc]);
     float lsum = 0.f;
-    float A[DT];
+    float A[VPT];
 #pragma unroll
-    for (int e = 0; e < DT; ++e) A[e] = 0.f;
+    for (int e = 0; e < VPT; ++e) A[e] = 0.f;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
       const float f = fast_exp2(sm_m[ww][cc] - M);
       lsum = fmaf(sm_l[ww][cc], f, lsum);
+      if constexpr (VPT == 2) {
+        const f32x2 o = *reinterpret_cast<const f32x2*>(sm_o(ww, cc) + d0);
+        A[0] = fmaf(o[0], f, A[0]);
+        A[1] = fmaf(o[1], f, A[1]);
+      } else {
 #pragma unroll
-      for (int t4 = 0; t4 < DT / 4; ++t4) {
-        const f32x4 o = *reinterpret_cast<const f32x4*>(sm_o(ww, cc) + d0 + 4 * t4);
+        for (int t4 = 0; t4 < VPT / 4; ++t4) {
+          const f32x4 o = *reinterpret_cast<const f32x4*>(sm_o(ww, cc) + d0 + 4 * t4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) A[4 * t4 + e] = fmaf(o[e], f, A[4 * t4 + e]);
+          for (int e = 0; e < 4; ++e) A[4 * t4 + e] = fmaf(o[e], f, A[4 * t4 + e]);
+        }
       }
     }
     if (nact == 1) {
       IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(i0 + cc) * a.o_st + d0;
       const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
-      for (int e = 0; e < DT; ++e) Elem<IO>::store(op + e, lsum > 0.f ? A[e] * inv : 0.f);
+      for (int e = 0; e < VPT; ++e) Elem<IO>::store(op + e, lsum > 0.f ? A[e] * inv : 0.f);
     } else {
       float* rec = a.ws + (((int64_t)unit * a.num_splits + split) * 16 + cc) * (HD + 2);
       if (d0 == 0) {
@@ -590,7 +607,7 @@ void prefill_mfma_kernel(const AttnArgs a) {
         rec[1] = lsum;
       }
 #pragma unroll
-      for (int e = 0; e < DT; ++e) rec[2 + d0 + e] = A[e];
+      for (int e = 0; e < VPT; ++e) rec[2 + d0 + e] = A[e];
     }
   }
 }
@@ -648,7 +665,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
 // independent MFMA and softmax chains, half the block walks per wavefront at the same wavefronts
 // per SIMD; parity green): bf16 9.5 -> 10.2 us (chunked), 9.6 -> 10.1 (128/256 mix), 11.6 -> 14.1
 // (8 x 8 heads), 4.8 -> 6.8 (2 x 8 heads, 64 rows); fp32 18.5 -> 22.5, 20.8 -> 21.3, 24.5 -> 24.4,
-// 6.1 -> 9.3, so the walk is not bound by its per-block memory round trips either.
+// 6.1 -> 9.3, so the walk is not bound by its per-block memory round trips either; one
+// 8-wavefront workgroup per heavy/light unit pair (the pair that shares a compute unit), the union
+// of their blocks dealt round-robin to its wavefronts from page-table rows staged in LDS, each
+// wavefront keeping a state per unit (parity green): every wavefront walks 8-10 blocks instead of
+// 3-15, but a block then costs 0.47 instead of 0.36 us and the prologue grows by 1.8 us (bf16
+// 9.0 -> 10.6 us, fp32 17.9 -> 20.0 us; with the blocks drawn from per-unit LDS counters instead
+// 12.5 and 20.6 us).
 // PAGED_HIP_PREFILL_STAGING=lds / regs forces one of them (tests cover both).
 static bool prefill_stage_in_lds(bool fp32_kv, unsigned grid) {
   const char* env = getenv("PAGED_HIP_PREFILL_STAGING");
