@@ -658,6 +658,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
 // So: LDS for bf16 KV always, for fp32 KV while the grid fits 2 workgroups per CU. Also measured
 // on the LDS staging and not kept: a three-stage ring for bf16 KV (two blocks ahead): 9.6 ->
 // 9.35 us on the chunked workload, 11.7 -> 14.5 us on 8 x 8 heads (48 KB per workgroup, 3 per CU);
+// measured again after the one-pass merge, 2 / 3 / 4 stages (1 / 2 / 3 blocks ahead): chunked
+// 9.0 / 9.0 / 9.0 us, 128/256 mix 8.9 / 9.1 / 9.3, 8 x 8 heads 10.7 / 13.6 / 13.2;
 // putting two tiles of the same (request, head) on each compute unit (tiles t and 15 - t, so the
 // pair's second read of a block can hit L1): bf16 9.6 -> 9.4 us, fp32 18.3 -> 20.4 us (the
 // requests' different lengths then unbalance the compute units); two adjacent 16-row tiles per
