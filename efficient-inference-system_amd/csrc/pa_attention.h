@@ -54,6 +54,12 @@ bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size);
 int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len);
 int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream);
 
+// Split-step prefill (32 query rows per workgroup, 8 wavefronts splitting the KV steps; bf16 KV
+// at head_dim 64). Defined in pa_prefill_wide.hip.
+bool prefill_split_supported(int kv_dtype, int head_dim, int block_size);
+int64_t prefill_split_units(int32_t batch, int32_t num_heads, int32_t query_len);
+int launch_prefill_split(const AttnArgs& a, int io_dtype, hipStream_t stream);
+
 // Generic one-wavefront-per-(request, head, query row) kernel for shapes without a tuned kernel
 // (any block_size, head_dim <= 512). Defined in pa_decode.hip.
 int launch_generic_attention(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream);

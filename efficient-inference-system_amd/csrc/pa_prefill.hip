@@ -751,6 +751,28 @@ static bool use_wide_prefill(int kv_dtype, int32_t head_dim, int32_t batch, int3
   return head_dim == 128 && units >= cus;
 }
 
+// Split-step kernel (32-row tiles, 8 wavefronts splitting the KV steps; bf16 KV at head_dim 64)
+// instead of the 16-row kernel, by its unit count U = B * H * ceil(T / 32) (one workgroup per CU
+// at most). Graph replay on MI355X, 16-row / split-step, us, contexts U[0, 768] unless noted:
+//   U = 256: 7.67 / 6.86 (4 x 8 heads, T 256), 8.72 / 7.03 (8 x 8, T 128), 12.78 / 10.39 (4 x 8,
+//            T 256, contexts 0.5-2k), 6.84 / 6.20 (2 x 16, T 256), 8.28 / 6.90 (4 x 16, T 128),
+//            6.78 / 6.19 (1 x 32, T 256); the chunked workload 9.2 / 8.2, its 128/256 mix 9.2 / 7.5;
+//   U = 192: 7.80 / 6.65 (3 x 8, T 256);
+//   U = 128: 6.50 / 6.02 (2 x 8, T 256), 7.25 / 6.62 (4 x 8, T 128), but 5.57 / 5.90 (8 x 8, T 64,
+//            contexts 0-512);
+//   U = 64:  4.92 / 5.10, 5.08 / 5.13, 5.43 / 5.81 (T 64), 7.66 / 7.30 (8 x 8, T 32);
+//   U = 384: 10.27 / 10.73 (two rounds); U = 512: 10.8 / 10.9.
+// So: from half the CUs to the CU count, for chunks longer than 64 rows.
+// PAGED_HIP_PREFILL_KERNEL=split forces it where it applies (tile forces the 16-row kernel).
+static bool use_split_prefill(int32_t batch, int32_t num_heads, int32_t query_len) {
+  const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
+  if (env != nullptr && strcmp(env, "split") == 0) return true;
+  if (env != nullptr && strcmp(env, "tile") == 0) return false;
+  const int64_t units = prefill_split_units(batch, num_heads, query_len);
+  const int64_t cus = pa_host::device_cu_count();
+  return query_len > 64 && 2 * units >= cus && units <= cus;
+}
+
 static int prefill_num_splits(int32_t max_pages, int32_t split_blocks) {
   if (split_blocks <= 0 || max_pages <= split_blocks) return 1;
   return (int)((max_pages + split_blocks - 1) / split_blocks);
@@ -807,6 +829,9 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
       use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len))
     return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
+  if (split_blocks <= 0 && prefill_split_supported(kv_dtype, head_dim, block_size) &&
+      use_split_prefill(batch, num_heads, query_len))
+    return launch_prefill_split(a, io_dtype, stream);
 
   const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);
   const int nsplit = prefill_num_splits(max_pages, split_blocks);

@@ -630,6 +630,331 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Split-step kernel for short chunks with bf16 KV: one workgroup of 8 wavefronts per (request,
+// head, tile of 32 query rows). Every wavefront holds the tile's 32 rows and takes every 8th
+// 32-key step of the tile's keys (steps w, w + 8, ...), streaming its steps' K and V tiles into its
+// own two-stage LDS ring with LDS-direct loads; the wavefronts' online-softmax states are merged
+// in LDS at the end. A step is the wide kernel's step on v_mfma_f32_32x32x16_bf16 (same operand
+// layouts, swizzles, masking and lazy rescale): 32 x 32 scores per MFMA chain and 16 scores per
+// lane per exchange, where the 16-row kernel's 16 x 16 blocks give 4. At chunk sizes where the
+// wide kernel's 128-row tiles leave most compute units idle (4 x 8 heads x 256 rows: 64 tiles),
+// this grid has one workgroup per compute unit.
+constexpr int kSplitWaves = 8;
+constexpr int kSplitRows = 32;
+
+template <typename IO, int HD>
+__global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(const AttnArgs a) {
+  constexpr int NW = kSplitWaves;
+  constexpr int KS = 32;                 // keys per step: two KV blocks
+  constexpr int QH = HD / 2;             // head_dim values per lane in the QK^T operands
+  constexpr int NQ = HD / 16;            // QK^T MFMAs per step (k = 16 each)
+  constexpr int DU = HD / 32;            // output tiles of 32 head_dim rows
+  constexpr int CPR = HD / 8;            // 16-byte chunks per key row
+  constexpr int RPI = kWave / CPR;       // key rows per LDS-direct load instruction (1 KB)
+  constexpr int NDMA = KS / RPI;         // such instructions per K (or V) tile
+  constexpr int RPB = 128 / HD;          // key rows per 256 bytes (one pass over the LDS banks)
+  constexpr int TILE = KS * HD;          // elements per K (or V) tile
+  constexpr int kRing = 2 * 2 * TILE * 2;          // bytes: two stages of (K, V)
+  constexpr int kOS = HD + 4;                       // floats per merge row
+  constexpr int kOB = kSplitRows * kOS * 4;         // bytes of a wavefront's merge rows
+  constexpr int kWaveB = kRing > kOB ? kRing : kOB;
+  static_assert(NDMA >= 1 && NDMA * RPI == KS && 16 % RPI == 0 && kWaveB % 16 == 0, "tile split");
+  constexpr int TPR = NW * kWave / kSplitRows;      // merge: threads per row
+  constexpr int VPT = HD / TPR;                     // merge: head_dim values per thread
+  static_assert(VPT % 4 == 0, "merge: 16-byte pieces");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[NW * kWaveB];
+  __shared__ float sm_m[NW][kSplitRows];
+  __shared__ float sm_l[NW][kSplitRows];
+  constexpr int kQRB = HD * (int)sizeof(IO);  // bytes of a q row
+  constexpr int kQS = kQRB + 16;               // LDS stride of the staged q rows
+  __shared__ __attribute__((aligned(16))) unsigned char sm_q[kSplitRows * kQS];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int G2 = lane >> 5;
+  const int c = lane & 31;
+
+  // Unit: (request, head) pair and 32-row tile; when the pairs divide over the dies, all tiles of
+  // a pair run on one die (workgroup x on die x % kXcds), so its KV is fetched into one L2.
+  const int ntiles = (a.T + kSplitRows - 1) / kSplitRows;
+  const int pairs = a.B * a.H;
+  int bh, qt;
+  {
+    const int x = blockIdx.x;
+    if (pairs % kXcds == 0) {
+      const int y = x / kXcds;
+      bh = (y / ntiles) * kXcds + x % kXcds;
+      qt = ntiles - 1 - y % ntiles;
+    } else {
+      bh = x / ntiles;
+      qt = ntiles - 1 - x % ntiles;
+    }
+  }
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int i0 = qt * kSplitRows;
+  const int i = i0 + c;
+
+  const int L = a.seq_lens[b];
+  const int C = a.cur_lens[b];
+  const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
+  const int last = (i0 + kSplitRows - 1) < (a.T - 1) ? (i0 + kSplitRows - 1) : (a.T - 1);
+  int nb = (valid_keys(L, C, last) + 15) / 16;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+  const int nsteps = (nb + 1) / 2;
+  const int mine = nsteps > w ? (nsteps - w + NW - 1) / NW : 0;  // this wavefront's steps
+
+  // B operand of S^T = K Q^T: q[i][G2*QH + 8s + e] for MFMA s, pre-scaled, rounded to bf16. Every
+  // wavefront needs the same 32 rows: they are read once per workgroup, 16 bytes per thread with
+  // consecutive threads along a row, into LDS rows padded by 16 bytes (the 8 rows of a 16-byte read
+  // pass then fall in distinct banks), and each lane reads its half row from there. (Loaded by
+  // every wavefront straight into its registers, the prologue took 3.6 instead of ~2.2 us: 8 copies
+  // of the tile, each load instruction touching 64 rows.) Rows that are not 16-byte aligned take
+  // element loads instead.
+  bf16x8 qb[NQ];
+  const float qsc = i < a.T ? a.scale_log2 : 0.f;
+  constexpr int64_t kIOB = sizeof(IO);
+  if ((((uint64_t)(size_t)a.q | (uint64_t)(a.q_sb * kIOB) | (uint64_t)(a.q_sh * kIOB) | (uint64_t)(a.q_st * kIOB)) &
+       15) == 0) {
+    constexpr int CH = kQRB / 16;  // 16-byte chunks per row
+    const unsigned char* qrow0 =
+        static_cast<const unsigned char*>(a.q) + ((int64_t)b * a.q_sb + (int64_t)h * a.q_sh) * kIOB;
+    for (int idx = threadIdx.x; idx < kSplitRows * CH; idx += NW * kWave) {
+      const int r = idx / CH, ch = idx - r * CH;
+      const int row = i0 + r < a.T ? i0 + r : 0;
+      *reinterpret_cast<u32x4*>(sm_q + r * kQS + 16 * ch) =
+          *reinterpret_cast<const u32x4*>(qrow0 + (int64_t)row * a.q_st * kIOB + 16 * ch);
+    }
+    __syncthreads();
+    constexpr int EPC = 16 / (int)sizeof(IO);  // elements per 16-byte chunk
+#pragma unroll
+    for (int s2 = 0; s2 < NQ; ++s2) {
+      float f[8];
+#pragma unroll
+      for (int k = 0; k < 8 / EPC; ++k) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(sm_q + c * kQS + (G2 * QH + 8 * s2 + EPC * k) * (int)kIOB);
+        if constexpr (sizeof(IO) == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) f[4 * k + e] = __uint_as_float(x[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            f[2 * e] = bf16_lo(x[e]);
+            f[2 * e + 1] = bf16_hi(x[e]);
+          }
+        }
+      }
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wd[e] = pack_bf16x2(f[2 * e] * qsc, f[2 * e + 1] * qsc);
+      qb[s2] = __builtin_bit_cast(bf16x8, (u32x4{wd[0], wd[1], wd[2], wd[3]}));
+    }
+  } else {
+    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
+                   (int64_t)(i < a.T ? i : 0) * a.q_st + G2 * QH;
+#pragma unroll
+    for (int s2 = 0; s2 < NQ; ++s2) {
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        wd[e] = pack_bf16x2(Elem<IO>::load(qp + 8 * s2 + 2 * e) * qsc, Elem<IO>::load(qp + 8 * s2 + 2 * e + 1) * qsc);
+      qb[s2] = __builtin_bit_cast(bf16x8, (u32x4{wd[0], wd[1], wd[2], wd[3]}));
+    }
+  }
+
+  f32x16 oacc[DU];
+#pragma unroll
+  for (int u = 0; u < DU; ++u)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[u][e] = 0.f;
+  float m = kNegBig, l = 0.f;
+
+  const uint16_t* kpool = static_cast<const uint16_t*>(a.k_pool);
+  const uint16_t* vpool = static_cast<const uint16_t*>(a.v_pool);
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+  const uint32_t nblk = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
+  auto ok_blk = [&](int e) { return (uint32_t)e < nblk; };
+
+  auto kswz = [](int r) { return (r / RPB) & (CPR - 1); };
+  auto vswz = [](int r) { return (4 * ((r / RPB) & 3)) & (CPR - 1); };
+  uint32_t kdo[NDMA], vdo[NDMA];  // byte offsets of this lane's source chunk in its block
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int r = n * RPI + lane / CPR;
+    const int p = lane % CPR;
+    kdo[n] = (uint32_t)(2 * ((r & 15) * HD + 8 * (p ^ kswz(r))));
+    vdo[n] = (uint32_t)(2 * ((r & 15) * HD + 8 * (p ^ vswz(r))));
+  }
+  const int kx = kswz(c);
+  const int vr4 = (c & 15) >> 2;
+  const int vx = vswz(4 * G2 + vr4);
+  auto v_off = [&](int d) {
+    const int hd = 32 * d + 16 * (c >> 4) + 4 * (c & 3);
+    return (4 * G2 + vr4) * HD + 8 * ((hd >> 3) ^ vx) + (hd & 4);
+  };
+  unsigned char* ring = smem + w * kWaveB;
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+  // This wavefront's steps st = w + NW * k, in chunks of 32 steps: lane 2k + j holds the page-table
+  // entry of block j of the chunk's step k (-1 past the request's blocks).
+  for (int k0 = 0; k0 < mine; k0 += kWave / 2) {
+    const int cnt = (mine - k0) < kWave / 2 ? (mine - k0) : kWave / 2;
+    int ent = -1;
+    {
+      const int blk = 2 * (w + NW * (k0 + lane / 2)) + (lane & 1);
+      if (lane < 2 * cnt && blk < nb) ent = pt[blk];
+    }
+    auto issue = [&](int stg, int k) {
+      const int e0 = __builtin_amdgcn_readlane(ent, 2 * k), e1 = __builtin_amdgcn_readlane(ent, 2 * k + 1);
+      const uint16_t* kb0 = kpool + ((int64_t)(ok_blk(e0) ? e0 : 0) * a.H + h) * (16 * HD);
+      const uint16_t* kb1 = kpool + ((int64_t)(ok_blk(e1) ? e1 : 0) * a.H + h) * (16 * HD);
+      const uint16_t* vb0 = vpool + ((int64_t)(ok_blk(e0) ? e0 : 0) * a.H + h) * (16 * HD);
+      const uint16_t* vb1 = vpool + ((int64_t)(ok_blk(e1) ? e1 : 0) * a.H + h) * (16 * HD);
+      unsigned char* dk = ring + stg * 4 * TILE;
+      unsigned char* dv = dk + 2 * TILE;
+#pragma unroll
+      for (int n = 0; n < NDMA; ++n) {
+        const bool second = n * RPI >= 16;
+        lds_direct_load16(second ? kb1 : kb0, kdo[n], dk + n * 1024);
+        lds_direct_load16(second ? vb1 : vb0, vdo[n], dv + n * 1024);
+      }
+    };
+    issue(0, 0);
+    for (int k = 0; k < cnt; ++k) {
+      if (k + 1 < cnt) {
+        issue((k + 1) & 1, k + 1);
+        vm_wait<2 * NDMA>();
+      } else {
+        vm_wait<0>();
+      }
+      const uint16_t* skx = reinterpret_cast<const uint16_t*>(ring + (k & 1) * 4 * TILE);
+      const uint16_t* svx = skx + TILE;
+      const int st = w + NW * (k0 + k);
+      const int e0 = __builtin_amdgcn_readlane(ent, 2 * k), e1 = __builtin_amdgcn_readlane(ent, 2 * k + 1);
+      // ---- S^T = K Q^T ---------------------------------------------------------------------------
+      f32x16 sacc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < NQ; ++s2) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(skx + c * HD + 8 * ((G2 * (CPR / 2) + s2) ^ kx));
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s2], sacc, 0, 0, 0);
+      }
+      // ---- online softmax (keys st*32 + 8j + 4*G2 + r of this step), in place ---------------------
+      const bool ok0 = ok_blk(e0), ok1 = ok_blk(e1);
+      const bool full = ok0 && ok1 && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
+      if (!full) {
+        const int t0 = st * KS + 4 * G2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool okb = j < 2 ? ok0 : ok1;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 8 * j + r;
+            sacc[4 * j + r] = (okb && t < n_c) ? sacc[4 * j + r] : -INFINITY;
+          }
+        }
+      }
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sacc[e]);
+      mloc = max_xor32(mloc);
+      const bool grow = mloc > m + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float mnew = grow ? mloc : m;
+        const float alpha = fast_exp2(m - mnew);
+        l *= alpha;
+#pragma unroll
+        for (int u = 0; u < DU; ++u) oacc[u] *= alpha;
+        m = mnew;
+      }
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sacc[e] = fast_exp2(sacc[e] - m);
+        ps += sacc[e];
+      }
+      l += sum_xor32(ps);
+      // ---- O^T += V^T P^T ------------------------------------------------------------------------
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        uint32_t pw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(sacc[8 * mm + 2 * q], sacc[8 * mm + 2 * q + 1]);
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
+#pragma unroll
+        for (int d = 0; d < DU; ++d) {
+          const uint16_t* vp = svx + v_off(d) + 16 * mm * HD;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vp));
+          const s16x4 hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vp + 8 * HD));
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[d], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // ---- merge: lane (G2, c) holds O[query c][32d + 8j + 4*G2 + r] in oacc[d][4j + r] --------------
+  float* mrow = reinterpret_cast<float*>(ring) + c * kOS;
+#pragma unroll
+  for (int d = 0; d < DU; ++d)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<f32x4*>(mrow + 32 * d + 8 * j + 4 * G2) =
+          f32x4{oacc[d][4 * j], oacc[d][4 * j + 1], oacc[d][4 * j + 2], oacc[d][4 * j + 3]};
+  if (G2 == 0) {
+    sm_m[w][c] = m;
+    sm_l[w][c] = l;
+  }
+  __syncthreads();
+  const int row = threadIdx.x / TPR;
+  const int d0 = (threadIdx.x % TPR) * VPT;
+  if (i0 + row < a.T) {
+    float M = kNegBig;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_m[ww][row]);
+    float lsum = 0.f, A[VPT];
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) A[e] = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float f = fast_exp2(sm_m[ww][row] - M);
+      lsum = fmaf(sm_l[ww][row], f, lsum);
+      const float* src = reinterpret_cast<const float*>(smem + ww * kWaveB) + row * kOS + d0;
+#pragma unroll
+      for (int t4 = 0; t4 < VPT / 4; ++t4) {
+        const f32x4 o = *reinterpret_cast<const f32x4*>(src + 4 * t4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) A[4 * t4 + e] = fmaf(o[e], f, A[4 * t4 + e]);
+      }
+    }
+    IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(i0 + row) * a.o_st + d0;
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) Elem<IO>::store(op + e, lsum > 0.f ? A[e] * inv : 0.f);
+  }
+}
+
+bool prefill_split_supported(int kv_dtype, int head_dim, int block_size) {
+  return kv_dtype == PA_DTYPE_BF16 && block_size == 16 && head_dim == 64;
+}
+
+int64_t prefill_split_units(int32_t batch, int32_t num_heads, int32_t query_len) {
+  return (int64_t)batch * num_heads * ((query_len + kSplitRows - 1) / kSplitRows);
+}
+
+int launch_prefill_split(const AttnArgs& a, int io_dtype, hipStream_t stream) {
+  const int64_t units = prefill_split_units(a.B, a.H, a.T);
+  if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
+  const dim3 grid((unsigned)units), block(kSplitWaves * kWave);
+  if (io_dtype == PA_DTYPE_F32) prefill_split_kernel<float, 64><<<grid, block, 0, stream>>>(a);
+  else prefill_split_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
+  PA_CHECK_LAUNCH("split prefill kernel");
+  return PA_OK;
+}
+
 bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size) {
   return (kv_dtype == PA_DTYPE_BF16 || kv_dtype == PA_DTYPE_F32) && block_size == 16 &&
          (head_dim == 64 || head_dim == 128);

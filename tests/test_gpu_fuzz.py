@@ -94,7 +94,7 @@ def test_prefill_random_cases(device, monkeypatch, seed):
     lens = [c0 + min(c, T) for c0, c in zip(ctx, curs)]  # the cache after appending the chunk
     kv_dtype = r.choice([torch.float32, torch.bfloat16])
     io_dtype = r.choice([torch.float32, torch.bfloat16])
-    kernel = r.choice(["", "tile", "wide"]) if fast else ""
+    kernel = r.choice(["", "tile", "wide", "split"]) if fast else ""
     split = r.choice([0, 0, 1, 3]) if fast and kernel != "wide" else 0
     staging = r.choice(["", "lds", "regs"])  # the 16-row kernel's KV staging at head_dim 64
     if kernel:

@@ -128,6 +128,53 @@ def test_kv_staging_on_a_large_grid(device, monkeypatch, kv_dtype):
     assert err <= (1e-4 if kv_dtype == torch.float32 else 2e-2)
 
 
+@pytest.mark.parametrize("seed", [0, 2, 4])
+def test_split_step_kernel_chunked(device, monkeypatch, seed):
+    """The split-step kernel (8 wavefronts per 32-row tile, each taking every 8th 32-key step
+    through its own LDS ring, states merged in LDS) on the chunked-prefill workload with bf16 KV,
+    against the oracle on the same bf16 values."""
+    w = workloads.chunked_prefill(seed=seed, device=device, kv_dtype=torch.bfloat16)
+    b = workloads._batch(w["q"], w["k_pool"], w["v_pool"], w["block_lists"], w["seq_lens"], w["chunk_lens"], device)
+    print(f"split-step seed={seed} ctx={w['prev_lens']} chunk={w['chunk_lens']}", flush=True)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "split")
+    err = max_err(run(b), oracle_out(b))
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= 2e-2
+
+
+@pytest.mark.parametrize("T,ctx,curs", [
+    (40, [0, 37, 300], [40, 1, 25]),         # rows past T in the last tile, a one-token chunk
+    (8, [16, 0], [8, 3]),                    # one partial tile, an empty context
+    (96, [700, 0, 33], [96, 80, 17]),        # padded rows, contexts off block boundaries
+    (64, [9000], [64]),                      # 286 steps: two 32-step chunks per wavefront
+])
+@pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
+def test_split_step_kernel_ragged(device, monkeypatch, T, ctx, curs, io_dtype):
+    """The split-step kernel forced on ragged shapes with bf16 KV, fp32 and bf16 q/out."""
+    b = make_prefill(device, 17, ctx, curs, T, 8, 64, kv_dtype=torch.bfloat16)
+    if io_dtype == torch.bfloat16:
+        b = workloads._batch(b.q.to(torch.bfloat16), b.k_pool, b.v_pool, b.block_lists, b.seq_lens, b.cur_lens, device)
+    print(f"split-step ragged T={T} ctx={ctx} curs={curs} io={io_dtype}", flush=True)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "split")
+    err = max_err(run(b), oracle_out(b))
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= (2e-2 if io_dtype == torch.float32 else 3e-2)
+
+
+def test_split_step_kernel_negative_pages_and_strided_views(device, monkeypatch):
+    """-1 page-table entries past a request's blocks and strided q/out views (the layout the model
+    passes) through the split-step kernel."""
+    H, Hd, T = 8, 64, 48
+    b = make_prefill(device, 19, [130, 20], [48, 30], T, H, Hd, kv_dtype=torch.bfloat16)
+    qv = b.q.transpose(1, 2).contiguous().transpose(1, 2)  # [B, H, T, Hd] view of [B, T, H, Hd]
+    pt = torch.cat([b.page_table, torch.full((2, 3), -1, dtype=torch.int32, device=device)], dim=1)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "split")
+    out = paged_attention_prefill_hip(qv, b.k_pool, b.v_pool, pt, b.seq_lens_t, b.cur_lens_t)
+    err = max_err(out, oracle_out(b))
+    print(f"split-step strided max err {err:.2e}", flush=True)
+    assert err <= 2e-2
+
+
 def test_kv_staging_head_dim_128(device, monkeypatch):
     """bf16 KV at head_dim 128 through the 16-row kernel: LDS and register staging bit-identical and
     within tolerance of the oracle (2 requests x 16 heads, 256-token chunks over 1-2k contexts)."""
