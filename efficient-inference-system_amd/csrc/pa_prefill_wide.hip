@@ -698,6 +698,15 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(cons
 
   const int L = a.seq_lens[b];
   const int C = a.cur_lens[b];
+  // The first page-table chunk (see the walk below) is read together with the lengths, for every
+  // block of the table's row, and cut to the request's blocks once the lengths are known: one
+  // dependent round trip less before the first KV load.
+  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+  int ent0 = -1;
+  {
+    const int blk = 2 * (w + NW * (lane / 2)) + (lane & 1);
+    if (blk < a.max_pages) ent0 = pt[blk];
+  }
   const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
   const int last = (i0 + kSplitRows - 1) < (a.T - 1) ? (i0 + kSplitRows - 1) : (a.T - 1);
   int nb = (valid_keys(L, C, last) + 15) / 16;
@@ -772,7 +781,6 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(cons
 
   const uint16_t* kpool = static_cast<const uint16_t*>(a.k_pool);
   const uint16_t* vpool = static_cast<const uint16_t*>(a.v_pool);
-  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
   const uint32_t nblk = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
   auto ok_blk = [&](int e) { return (uint32_t)e < nblk; };
 
@@ -803,7 +811,7 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(cons
     int ent = -1;
     {
       const int blk = 2 * (w + NW * (k0 + lane / 2)) + (lane & 1);
-      if (lane < 2 * cnt && blk < nb) ent = pt[blk];
+      if (lane < 2 * cnt && blk < nb) ent = k0 == 0 ? ent0 : pt[blk];
     }
     auto issue = [&](int stg, int k) {
       const int e0 = __builtin_amdgcn_readlane(ent, 2 * k), e1 = __builtin_amdgcn_readlane(ent, 2 * k + 1);
