@@ -640,6 +640,11 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
 // lane per exchange, where the 16-row kernel's 16 x 16 blocks give 4. At chunk sizes where the
 // wide kernel's 128-row tiles leave most compute units idle (4 x 8 heads x 256 rows: 64 tiles),
 // this grid has one workgroup per compute unit.
+// Measured and not kept (graph replay, interleaved with the kept kernel on one box): touching a
+// wavefront's next three steps right after its first ring load (one LDS-direct load per step into
+// a junk area, each lane a different 128-byte line of the step's four slabs, so that the later ring
+// loads would hit L2): chunked workload 8.06 -> 9.6 us, and 1.2-1.5 us slower on every other shape
+// (each such load sends 64 lines through the compute unit's L1, ahead of the ring loads).
 constexpr int kSplitWaves = 8;
 constexpr int kSplitRows = 32;
 
