@@ -39,6 +39,7 @@ the named groups; both are for profiling one workload alone.)
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import math
 import os
@@ -426,6 +427,20 @@ def _ragged_decode(res, device, steps, with_cpu):
         }
 
 
+@contextlib.contextmanager
+def _forced_prefill_kernel(name):
+    """Force pa_prefill's kernel choice (tile | split | wide) for the calls inside the block."""
+    prev = os.environ.get("PAGED_HIP_PREFILL_KERNEL")
+    os.environ["PAGED_HIP_PREFILL_KERNEL"] = name
+    try:
+        yield
+    finally:
+        if prev is None:
+            del os.environ["PAGED_HIP_PREFILL_KERNEL"]
+        else:
+            os.environ["PAGED_HIP_PREFILL_KERNEL"] = prev
+
+
 def _chunked_prefill(res, device, steps, with_cpu):
     import torch
 
@@ -470,6 +485,13 @@ def _chunked_prefill(res, device, steps, with_cpu):
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
             "mfma_frac_graph": round(flops / (graph_ms * 1e-3) / 1e12 / peak, 4),
         }
+        if tag == "bf16kv":  # the default choice here is the split-step kernel; the 16-row one beside it
+            with _forced_prefill_kernel("tile"):
+                res[f"chunked_prefill_{tag}"]["attention_us_graph_16row_kernel"] = round(1e3 * time_graph_call(attn), 2)
+            res[f"chunked_prefill_{tag}"]["kernel"] = ("split-step (8 wavefronts share one 32-row tile's 32-key steps, "
+                                                       "one workgroup per CU)")
+        else:
+            res[f"chunked_prefill_{tag}"]["kernel"] = "16-row tiles (4 wavefronts per tile, KV staged through LDS)"
         if with_cpu:  # the pools already hold the appended chunks
             log(f"CPU timings: chunked prefill ({tag})")
             res[f"chunked_prefill_{tag}"]["cpu"] = cpu_call_times(
@@ -515,15 +537,8 @@ def _mid_prefill(res, device, steps):
     flops = workloads.prefill_flops(b.extra["prev_lens"], b.cur_lens, H, Hd)
     call = lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
     ms = time_call(call, steps)
-    prev = os.environ.get("PAGED_HIP_PREFILL_KERNEL")
-    os.environ["PAGED_HIP_PREFILL_KERNEL"] = "tile"
-    try:
+    with _forced_prefill_kernel("tile"):
         ms_tile = time_call(call, steps)
-    finally:
-        if prev is None:
-            del os.environ["PAGED_HIP_PREFILL_KERNEL"]
-        else:
-            os.environ["PAGED_HIP_PREFILL_KERNEL"] = prev
     cold_ms = time_cold_prefill(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t, copies=12)
     tfs = flops / (ms * 1e-3) / 1e12
     res["mid_prefill_bf16kv"] = {
