@@ -818,8 +818,13 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(cons
       const int blk = 2 * (w + NW * (k0 + lane / 2)) + (lane & 1);
       if (lane < 2 * cnt && blk < nb) ent = k0 == 0 ? ent0 : pt[blk];
     }
+    // A walk of one chunk starts at the tile's index modulo its step count, so the tiles of a
+    // (request, head) pair (on one die) ask for different steps first and meet the rest in L2.
+    const int rot = (mine <= kWave / 2 && cnt > 1) ? qt % cnt : 0;
+    auto rk = [&](int k) { const int r = k + rot; return r < cnt ? r : r - cnt; };
     auto issue = [&](int stg, int k) {
-      const int e0 = __builtin_amdgcn_readlane(ent, 2 * k), e1 = __builtin_amdgcn_readlane(ent, 2 * k + 1);
+      const int kr = rk(k);
+      const int e0 = __builtin_amdgcn_readlane(ent, 2 * kr), e1 = __builtin_amdgcn_readlane(ent, 2 * kr + 1);
       const uint16_t* kb0 = kpool + ((int64_t)(ok_blk(e0) ? e0 : 0) * a.H + h) * (16 * HD);
       const uint16_t* kb1 = kpool + ((int64_t)(ok_blk(e1) ? e1 : 0) * a.H + h) * (16 * HD);
       const uint16_t* vb0 = vpool + ((int64_t)(ok_blk(e0) ? e0 : 0) * a.H + h) * (16 * HD);
@@ -843,8 +848,9 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(cons
       }
       const uint16_t* skx = reinterpret_cast<const uint16_t*>(ring + (k & 1) * 4 * TILE);
       const uint16_t* svx = skx + TILE;
-      const int st = w + NW * (k0 + k);
-      const int e0 = __builtin_amdgcn_readlane(ent, 2 * k), e1 = __builtin_amdgcn_readlane(ent, 2 * k + 1);
+      const int kr = rk(k);
+      const int st = w + NW * (k0 + kr);
+      const int e0 = __builtin_amdgcn_readlane(ent, 2 * kr), e1 = __builtin_amdgcn_readlane(ent, 2 * kr + 1);
       // ---- S^T = K Q^T ---------------------------------------------------------------------------
       f32x16 sacc;
 #pragma unroll
