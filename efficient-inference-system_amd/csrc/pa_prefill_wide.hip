@@ -27,6 +27,9 @@
 // Rounding matches the 16-row bf16 kernel: q*scale and the softmax weights are rounded to bf16
 // (nearest even) for the products, scores and accumulators stay fp32. The running max is updated
 // lazily (see kRescaleSlack) and interior steps skip the causal/length mask.
+//
+// The file also holds the split-step kernel (prefill_split_kernel, below): the same bf16 step on
+// 32-row tiles for short chunks, with a tile's steps split over 8 wavefronts instead of its rows.
 #include "pa_attention.h"
 
 namespace pa {
