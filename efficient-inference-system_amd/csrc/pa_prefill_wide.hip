@@ -126,18 +126,25 @@ __device__ __forceinline__ bool wide_lpt_unit(const AttnArgs& a, int ntiles, int
 // lazy-rescale test) are paid once per NSUB * 32 keys. Measured on the large-prefill workload
 // (8 x 32 heads, chunk 512 over 1.8-3.7k contexts), same box, head_dim 64: NSUB 2 with 2 stages
 // 133-137 us, with 3 stages 148-150 us (48 KB of LDS: 3 workgroups per CU instead of 4), NSUB 1
-// 140-146 us. Head_dim 128 (NSUB 1, 164 registers: 3 workgroups per CU either way) uses 3 stages.
+// 140-146 us. Head_dim 128 takes one of two shapes by grid size (wide128_pair below).
 #ifndef WIDE_NSUB64
 #define WIDE_NSUB64 2
 #endif
 #ifndef WIDE_NST64
 #define WIDE_NST64 2
 #endif
-template <int HD>
-constexpr int wide_nsub() { return HD == 64 ? WIDE_NSUB64 : 1; }
+constexpr int kWideNsub64 = WIDE_NSUB64;
 // LDS stages of K and V tiles (2 or 3): loads are issued NST - 1 steps ahead of their use.
-template <int HD>
-constexpr int wide_stages() { return HD == 64 ? WIDE_NST64 : 3; }
+constexpr int kWideStages64 = WIDE_NST64;
+// Head_dim 128, bf16 KV: NSUB 2 with 2 stages (174 registers, 64 KB of LDS: 2 workgroups per CU)
+// when the grid fits in one round at 2 workgroups per CU, else NSUB 1 with 2 stages (154
+// registers, 32 KB: 3 per CU, registers being the limit). Measured in one process per build,
+// interleaved, bench.py's workloads (8 x 32 heads, 512-token chunks: 1024 units; 4 x 32 heads,
+// 256-token chunks: 256 units; and 12 x 32 heads over uniform 2688-token contexts: 1536 units):
+//   NSUB 1, 3 stages (the earlier choice)  250 / 58 / 392-394 us
+//   NSUB 1, 2 stages                       244 / 58 / 377-381 us
+//   NSUB 2, 2 stages                       241-245 / 49-52 / 419-421 us
+static bool wide128_pair(int64_t units) { return units <= 2 * (int64_t)pa_host::device_cu_count(); }
 
 template <typename IO, int HD, int NSUB, int NST>
 __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const AttnArgs a) {
@@ -999,11 +1006,13 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
       else prefill_wide_f32_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
     }
   } else if (io_dtype == PA_DTYPE_F32) {
-    if (a.head_dim == 64) prefill_wide_kernel<float, 64, wide_nsub<64>(), wide_stages<64>()><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<float, 128, wide_nsub<128>(), wide_stages<128>()><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<float, 64, kWideNsub64, kWideStages64><<<grid, block, 0, stream>>>(a);
+    else if (wide128_pair(units)) prefill_wide_kernel<float, 128, 2, 2><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<float, 128, 1, 2><<<grid, block, 0, stream>>>(a);
   } else {
-    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64, wide_nsub<64>(), wide_stages<64>()><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<uint16_t, 128, wide_nsub<128>(), wide_stages<128>()><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64, kWideNsub64, kWideStages64><<<grid, block, 0, stream>>>(a);
+    else if (wide128_pair(units)) prefill_wide_kernel<uint16_t, 128, 2, 2><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<uint16_t, 128, 1, 2><<<grid, block, 0, stream>>>(a);
   }
   PA_CHECK_LAUNCH("wide prefill kernel");
   return PA_OK;
