@@ -509,16 +509,23 @@ def _large_prefill(res, device, steps):
         b = workloads.large_prefill(seed=0, device=device, kv_dtype=kv_dtype)
         H, Hd = b.q.shape[1], b.q.shape[3]
         flops = workloads.prefill_flops(b.extra["prev_lens"], b.cur_lens, H, Hd)
-        ms = time_call(lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t,
-                                                           b.cur_lens_t), max(3, steps // 2))
+        call = lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+        ms = time_call(call, max(3, steps // 2))
+        graph_ms = time_graph_call(call, calls=10 if tag == "bf16kv" else 4, replays=3)
         peak = 157.3 if tag == "fp32" else 2500.0
         tfs = flops / (ms * 1e-3) / 1e12
         res[f"large_prefill_{tag}"] = {
             "workload": f"{b.batch} requests, {H} heads x {Hd}, context {b.extra['prev_lens']} + chunk 512 each, "
                         f"{'bf16' if tag == 'bf16kv' else 'fp32'} KV, fp32 q/out "
                         "(wide-tile kernel: 128 query rows per workgroup, KV staged through LDS)",
-            "attention_us": round(1e3 * ms, 1), "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1),
+            "attention_us": round(1e3 * ms, 1), "attention_us_graph": round(1e3 * graph_ms, 1),
+            "timing": "attention_us: eager calls through the Python wrapper, averaged (host gaps between calls); "
+                      "attention_us_graph: the same call replayed back to back from a HIP graph, with no gap between "
+                      "launches (sustained load)",
+            "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1),
+            "TFLOPs_graph": round(flops / (graph_ms * 1e-3) / 1e12, 1),
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
+            "mfma_frac_graph": round(flops / (graph_ms * 1e-3) / 1e12 / peak, 4),
         }
         del b
         torch.cuda.empty_cache()
