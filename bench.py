@@ -10,7 +10,8 @@ HIP events on the stream the kernel is launched on.
 
 Also reported on the same line:
   roofline       the decode kernel against MI355X's 8 TB/s HBM peak (and HBM traffic per launch
-                 when a counter summary is available under profiles/);
+                 when a counter summary is available under profiles/), and against what this box
+                 delivers to a plain streaming read and to a copy, measured right after;
   cpu_baseline   the oracle (C restatement of the reference's paged attention, fp64
                  accumulation) over the same batch on this host's cores, plus the rate of the
                  reference's own per-token torch loop on a small slice of it;
@@ -31,7 +32,8 @@ Also reported on the same line:
   continuous_batching_saturated  the fp32 model on the same request mix with every request
                  arriving at once (the serving path's capacity at max batch 8), GPU only.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-e2e]
-                       [--no-secondary] [--no-decode] [--calibrate-copy] [--e2e-model fp32|bf16|both]
+                       [--no-secondary] [--no-decode] [--calibrate-copy] [--no-box-calibration]
+                       [--e2e-model fp32|bf16|both]
                        [--only GROUP[,GROUP...]]
 (--no-decode skips the headline decode measurement and --only restricts the secondary workloads to
 the named groups; both are for profiling one workload alone.)
@@ -168,26 +170,35 @@ def cpu_baseline(batch, chunk: int = 32) -> dict:
     }
 
 
-def reference_loop_rate(batch, tokens: int = 256) -> dict:
-    """The reference's own CPU path (its per-token torch loop, restated in oracle/reference_loop.py)
-    on one request cut to `tokens` keys, all heads: seconds per (key x head), and the time the whole
-    batch would take at that rate."""
+def reference_loop_rate(batch, requests: int = 8, tokens: int = 2048) -> dict:
+    """The reference's own CPU path (its per-key torch loop, restated in oracle/reference_loop.py)
+    on the first `requests` requests, each cut to its first `tokens` keys, all heads: seconds per
+    (key x head), and the time the whole batch would take at that rate."""
     import torch
 
     from oracle.reference_loop import paged_attention_loop
 
     torch.set_num_threads(cpu_threads())
-    nblk = (tokens + 15) // 16
-    ids = torch.tensor(batch.block_lists[0][:nblk], device=batch.q.device, dtype=torch.long)
-    k = batch.k_pool.index_select(0, ids).float().cpu()
-    v = batch.v_pool.index_select(0, ids).float().cpu()
-    q = batch.q[:1].cpu()
+    rows = list(range(min(requests, batch.batch)))
+    cut = [min(tokens, batch.seq_lens[r]) for r in rows]
+    lists, ids, pos = [], [], 0
+    for r, n in zip(rows, cut):
+        nblk = (n + 15) // 16
+        ids += batch.block_lists[r][:nblk]
+        lists.append(list(range(pos, pos + nblk)))
+        pos += nblk
+    idx = torch.tensor(ids, device=batch.q.device, dtype=torch.long)
+    k = batch.k_pool.index_select(0, idx).float().cpu()
+    v = batch.v_pool.index_select(0, idx).float().cpu()
+    q = batch.q[:len(rows)].cpu()
     t0 = time.perf_counter()
-    paged_attention_loop(q, k, v, [list(range(nblk))], [tokens], [1])
+    paged_attention_loop(q, k, v, lists, cut, [1] * len(rows))
     dt = time.perf_counter() - t0
-    per = dt / (tokens * q.shape[1])
+    per = dt / (sum(cut) * q.shape[1])
     whole = per * sum(batch.seq_lens) * q.shape[1]
-    return {"seconds_per_key_head": per, "sample": f"request 0 cut to {tokens} keys x {q.shape[1]} heads ({dt:.2f} s)",
+    return {"seconds_per_key_head": per,
+            "sample": f"requests 0..{len(rows) - 1} cut to their first {tokens} keys ({sum(cut)} keys) x "
+                      f"{q.shape[1]} heads: {dt:.2f} s",
             "extrapolated_batch_seconds": whole,
             "extrapolated_GBps": batch.decode_bytes() / whole / 1e9, "threads": torch.get_num_threads()}
 
@@ -576,6 +587,39 @@ def calibration_copy(device, nbytes: int = 1 << 32) -> None:
     log(f"calibration copy: 3 x {nbytes} bytes read and written")
 
 
+def box_bandwidth(device, nbytes: int = 4 << 30, reps: int = 10) -> dict:
+    """What this box's HBM delivers, measured in the same process right after the decode timing:
+    a streaming read of `nbytes` with the decode kernel's 16-byte non-temporal loads
+    (pa_hbm_read_probe; the best of five grid sizes) and torch's device copy of nbytes / 2
+    (counted as read + write bytes). HIP events on the stream the kernels run on."""
+    import torch
+
+    from src.kernels import _lib
+
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    stream = torch.cuda.current_stream(device)
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    best = (0.0, 0)
+    for per_cu in (1, 2, 4, 8, 16):
+        wgs = cus * per_cu
+        sink = torch.zeros(wgs, dtype=torch.int32, device=device)
+        call = lambda: _lib.check(lib.pa_hbm_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), wgs,
+                                                        stream.cuda_stream), "pa_hbm_read_probe")
+        ms = time_call(call, reps)
+        best = max(best, (nbytes / (ms * 1e-3) / 1e9, wgs))
+    del buf
+    half = nbytes // 2
+    a = torch.zeros(half, dtype=torch.uint8, device=device)
+    b = torch.empty_like(a)
+    ms = time_call(lambda: b.copy_(a), reps)
+    copy = 2 * half / (ms * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return {"read_probe_GBps": round(best[0], 1), "read_probe_workgroups": best[1],
+            "copy_GBps": round(copy, 1), "bytes": nbytes}
+
+
 def init_weights_normal(model, std: float = 0.02) -> None:
     import torch
 
@@ -604,11 +648,14 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True,
     from src.serving.metrics import summarize_run
     from src.serving.scheduler import ContinuousBatchingScheduler
 
+    # The weights are drawn on the host (CPU generator, seed 42) and then moved, so the GPU run and
+    # the CPU baseline run the same model.
     torch.manual_seed(42)
     model = TinyTransformerLM(vocab_size=5000, d_model=512, num_heads=8, num_layers=6, d_ff=2048, max_seq_len=1024,
                               attention_backend=backend, kv_block_size=16, kv_pool_initial_blocks=64,
-                              kv_pool_growth_factor=2.0).to(device).eval()
+                              kv_pool_growth_factor=2.0)
     init_weights_normal(model)
+    model = model.to(device).eval()
     if dtype is not None:
         model = model.to(dtype)
     graphs_prepared = 0
@@ -647,7 +694,25 @@ def continuous_batching(device, backend: str = "hip_paged", warmup: bool = True,
         "wall_s": wall,
         "graphs_captured_in_warmup": graphs_prepared,
         "graphs_captured_in_run": (model._graph_step.captures - graphs_prepared) if model._graph_step else 0,
+        "_tokens": {r.request_id: list(r.generated_token_ids) for r in done},
     }
+
+
+def token_agreement(a: dict, b: dict) -> dict:
+    """Per-request agreement of two runs' greedy tokens (request id -> generated ids). A request's
+    greedy tokens depend only on its own prompt, so two runs agree request by request even when
+    they batched the requests differently; they may part at a near-tie of two logits, after which
+    the rest of that request differs."""
+    same = [rid for rid in a if a[rid] == b.get(rid)]
+    firsts = []
+    for rid in a:
+        x, y = a[rid], b.get(rid, [])
+        if x != y:
+            firsts.append(next((i for i, (u, v) in enumerate(zip(x, y)) if u != v), min(len(x), len(y))))
+    total = sum(len(x) for x in a.values())
+    agree = sum(sum(1 for u, v in zip(a[rid], b.get(rid, [])) if u == v) for rid in a)
+    return {"requests": len(a), "requests_identical": len(same), "tokens": total, "tokens_equal": agree,
+            "first_difference_positions": sorted(firsts)}
 
 
 def continuous_batching_pair(device, with_cpu: bool = True) -> dict:
@@ -655,11 +720,13 @@ def continuous_batching_pair(device, with_cpu: bool = True) -> dict:
     import torch
 
     gpu = continuous_batching(device, "hip_paged")
+    gpu_tokens = gpu.pop("_tokens")
     if not with_cpu:
         return gpu
     torch.set_num_threads(cpu_threads())
     log(f"continuous batching on the CPU ({torch.get_num_threads()} threads)")
     cpu = continuous_batching(torch.device("cpu"), "paged_reference", warmup=False)
+    gpu["token_agreement_with_cpu"] = token_agreement(gpu_tokens, cpu.pop("_tokens"))
     cpu["threads"] = torch.get_num_threads()
     cpu["host"] = cpu_info()
     cpu["kind"] = "port: this package's paged_reference backend (vectorised torch) on the CPU, same trace and weights"
@@ -679,7 +746,10 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the headline decode (profiling runs)")
     ap.add_argument("--only", default=",".join(SECONDARY),
                     help="comma-separated secondary workload groups to run: " + ", ".join(SECONDARY))
-    ap.add_argument("--calibrate-copy", action="store_true", help="also run a copy kernel of known size")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a copy kernel of known size (scales HBM counters in a profiling run)")
+    ap.add_argument("--no-box-calibration", action="store_true",
+                    help="skip the read-probe and copy bandwidth measured after the decode timing")
     ap.add_argument("--e2e-model", choices=("fp32", "bf16", "both"), default="both",
                     help="end-to-end runs: the fp32 model (with its CPU baseline), the bf16 model, or both")
     args = ap.parse_args()
@@ -723,6 +793,12 @@ def main() -> int:
         ms, wall_ms, _ = time_decode(batch, args.steps, args.warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         log(f"decode: {ms:.3f} ms/call (events), {wall_ms:.3f} ms/call (wall), {gbs:.1f} GB/s")
+        # Measured after the decode timing: right after a heavy copy the same decode calls measured
+        # ~4% slower on one box, so the calibration must not run ahead of the timed region.
+        box = None
+        if not args.no_box_calibration:
+            box = box_bandwidth(dev)
+            log(f"box: read probe {box['read_probe_GBps']} GB/s, copy {box['copy_GBps']} GB/s")
         result.update({
             "value": round(gbs, 2),
             "ms_per_step": round(ms, 4),
@@ -743,6 +819,18 @@ def main() -> int:
                 "traffic": pmc_traffic_bytes(),
             },
         })
+        if box is not None:
+            # the same kernel against what this box's HBM delivers to a plain read and a copy, so a
+            # slower box and a slower kernel can be told apart
+            result["roofline"].update({
+                "hbm_read_probe_GBps": box["read_probe_GBps"],
+                "frac_vs_read_probe": round(gbs / box["read_probe_GBps"], 4),
+                "hbm_copy_GBps": box["copy_GBps"],
+                "frac_vs_copy": round(gbs / box["copy_GBps"], 4),
+                "calibration": f"read probe: {box['bytes']} bytes read once with 16-byte non-temporal loads "
+                               f"({box['read_probe_workgroups']} workgroups of 512, best of 5 grid sizes); "
+                               f"copy: torch copy of {box['bytes'] // 2} bytes, read + write counted",
+            })
         if not args.no_cpu_baseline:
             log("CPU baseline (oracle over the batch)")
             result["cpu_baseline"] = cpu_baseline(batch)
@@ -761,6 +849,7 @@ def main() -> int:
         if args.e2e_model in ("bf16", "both"):
             log("end-to-end continuous batching with the model in bf16")
             bf = continuous_batching(dev, dtype=torch.bfloat16)
+            bf.pop("_tokens")
             bf["model_dtype"] = "bf16 (weights, activations, KV pools; fp32 accumulation)"
             result["continuous_batching_bf16_model"] = bf
         if args.e2e_model in ("fp32", "both"):
@@ -769,6 +858,7 @@ def main() -> int:
             # capacity, comparable with the CPU baseline's compute-bound rate above.
             log("end-to-end continuous batching, saturated (200 requests arriving at once)")
             sat = continuous_batching(dev, rate=1.0e6)
+            sat.pop("_tokens")
             sat["arrivals"] = "the same 200-request mix, Poisson at 1e6 req/s (all within ~1 ms)"
             result["continuous_batching_saturated"] = sat
     print(json.dumps(result), flush=True)

@@ -130,8 +130,15 @@ def large_decode_lengths(seed: int = 0, batch: int = 256, lo: int = 512, hi: int
 
 
 def large_decode(seed: int = 0, device="cpu", batch: int = 256, heads: int = 32, head_dim: int = 128,
-                 lo: int = 512, hi: int = 32768, kv_dtype: torch.dtype = torch.bfloat16) -> PagedBatch:
+                 lo: int = 512, hi: int = 32768, kv_dtype: torch.dtype = torch.bfloat16,
+                 rows: list[int] | None = None) -> PagedBatch:
+    """The large ragged decode batch. With `rows`, only those requests of the batch (their
+    lengths, in that order) over a pool sized and shuffled for them alone; the pool and q values
+    are then drawn afresh, not taken from the full batch."""
     lens = large_decode_lengths(seed, batch, lo, hi)
+    if rows is not None:
+        lens = [lens[r] for r in rows]
+        batch = len(lens)
     need = sum(math.ceil(L / BLOCK) for L in lens)
     pool_blocks = math.ceil(1.1 * need)
     g = torch.Generator().manual_seed(seed + 100003)

@@ -59,3 +59,14 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=120)
     assert p.returncode == 2
     assert "one GPU" in p.stderr
+
+
+def test_token_agreement_counts():
+    a = {0: [5, 6, 7], 1: [1, 2, 3, 4], 2: [9]}
+    b = {0: [5, 6, 7], 1: [1, 2, 8, 8], 2: [9]}
+    r = bench.token_agreement(a, b)
+    assert r == {"requests": 3, "requests_identical": 2, "tokens": 8, "tokens_equal": 6,
+                 "first_difference_positions": [2]}
+    assert bench.token_agreement(a, a)["requests_identical"] == 3
+    # a request missing from the second run counts as different from its first token
+    assert bench.token_agreement({3: [1, 2]}, {})["first_difference_positions"] == [0]

@@ -1,8 +1,8 @@
 """End-to-end continuous batching on the benchmark model and trace, on the GPU.
 
 Model: vocab 5000, d_model 512, 8 heads, 6 layers, d_ff 2048, max_seq_len 1024, KV block 16,
-weights N(0, 0.02), biases 0, LayerNorms (1, 0). Trace: the first requests of the 200-request
-Poisson trace at 32 req/s (seed 42, the benchmark mix). Scheduler: max batch 8, chunk 256,
+weights N(0, 0.02), biases 0, LayerNorms (1, 0). Trace: all 200 requests of the Poisson trace at
+32 req/s (seed 42, the benchmark mix). Scheduler: max batch 8, chunk 256,
 1536-token budget. The hip_paged model runs the real executors with its captured graphs (bucketed
 chunks, on-device argmax, pool growth), with the executors' timer fixed at 3 ms per call so that
 the scheduler's decisions do not depend on the box's speed.
@@ -32,7 +32,7 @@ from src.serving.scheduler import ContinuousBatchingScheduler
 
 pytestmark = pytest.mark.gpu
 
-N_REQUESTS = 28
+N_REQUESTS = 200
 TIE = 2e-4
 
 
@@ -97,6 +97,7 @@ EVENT_KEYS = ("phase", "batch_size", "tokens_scheduled", "prefill_tokens", "deco
               "padding_waste_tokens", "dispatch_time_ms", "finish_time_ms")
 
 
+@pytest.mark.timeout(900)
 def test_continuous_batching_benchmark_model_lockstep(device, monkeypatch):
     monkeypatch.setattr(cg, "timed_section", StepTimer)
     hip = benchmark_model("hip_paged", device)
@@ -106,7 +107,8 @@ def test_continuous_batching_benchmark_model_lockstep(device, monkeypatch):
     print(f"C4 lockstep: {N_REQUESTS} requests, {captured} graphs captured ahead", flush=True)
 
     ref_states: dict[int, list] = {}
-    stats = {"steps": 0, "max_err": 0.0, "prefill_steps": 0, "near_ties": set(), "tokens": 0}
+    stats = {"steps": 0, "max_err": 0.0, "prefill_steps": 0, "near_ties": set(), "tokens": 0, "near_tie_tokens": 0,
+             "near_tie_flips": 0}
 
     def ref_pools():
         return ref._ensure_layer_block_pools()
@@ -140,10 +142,15 @@ def test_continuous_batching_benchmark_model_lockstep(device, monkeypatch):
             top2 = torch.topk(row, 2).values
             if (top2[0] - top2[1]).item() < TIE:
                 stats["near_ties"].add(rid)
+                stats["near_tie_tokens"] += 1
+                stats["near_tie_flips"] += int(tokens[b]) != int(torch.argmax(row))
             else:
                 assert tokens[b] == int(torch.argmax(row)), (rid, plan.phase)
             stats["tokens"] += 1
         compare_pools()
+        if stats["steps"] % 500 == 0:
+            print(f"  step {stats['steps']}: {stats['tokens']} tokens checked, max logits err {stats['max_err']:.2e}",
+                  flush=True)
 
     def on_release(r):
         ref.release_request_caches(ref_states.pop(r.request_id))
@@ -151,7 +158,8 @@ def test_continuous_batching_benchmark_model_lockstep(device, monkeypatch):
     done, events = run(hip, device, observer=observe, on_release=on_release, keep_logits=True)
     compare_pools()
     print(f"C4 lockstep: {stats['steps']} steps ({stats['prefill_steps']} prefill), {stats['tokens']} tokens "
-          f"checked, max logits err {stats['max_err']:.2e}, near-tie requests {sorted(stats['near_ties'])}, "
+          f"checked, max logits err {stats['max_err']:.2e}, {stats['near_tie_tokens']} near-tie tokens "
+          f"({stats['near_tie_flips']} of them not the reference's argmax) in requests {sorted(stats['near_ties'])}, "
           f"pool capacity {hip.layer_block_pools[0].capacity_blocks} blocks, "
           f"graph captures {hip._graph_step.captures}", flush=True)
     assert len(done) == N_REQUESTS and all(r.num_generated_tokens == r.max_new_tokens for r in done)

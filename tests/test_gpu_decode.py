@@ -196,3 +196,44 @@ def test_large_ragged_decode_parity(device):
     print(f"  all {b.batch} requests: max err {worst:.2e}", flush=True)
     del b
     torch.cuda.empty_cache()
+
+
+def test_large_ragged_decode_bf16_against_unrounded_fp32(device):
+    """Large ragged decode shape (32 heads x 128, block 16, lengths of the 256-request batch) on 16
+    of its requests chosen from the shortest to the longest (the 32k one included): K and V are
+    drawn in fp32, the kernel runs on their bf16 rounding, and each request is compared with the
+    oracle on the UNROUNDED fp32 values (bf16-KV tolerance 2e-2) and on the same bf16 values
+    (1e-4)."""
+    lens_all = workloads.large_decode_lengths(0)
+    by_len = sorted(range(len(lens_all)), key=lambda i: lens_all[i])
+    rows = sorted({by_len[round(j * (len(by_len) - 1) / 15)] for j in range(16)})
+    assert len(rows) == 16 and max(lens_all[r] for r in rows) == max(lens_all)
+    b = workloads.large_decode(seed=0, device=device, rows=rows, kv_dtype=torch.float32)
+    print(f"large decode vs unrounded fp32: requests {rows}, lengths {b.seq_lens}", flush=True)
+    kb, vb = b.k_pool.to(torch.bfloat16), b.v_pool.to(torch.bfloat16)
+    got = paged_attention_decode_hip(b.q, kb, vb, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    torch.cuda.synchronize()
+    # only the blocks the requests use go to the host, renumbered in list order
+    ids = torch.tensor([i for x in b.block_lists for i in x], device=device, dtype=torch.long)
+    lists, pos = [], 0
+    for x in b.block_lists:
+        lists.append(list(range(pos, pos + len(x))))
+        pos += len(x)
+    q = b.q.cpu()
+    want32 = oracle.paged_attention(q, oracle._np(b.k_pool.index_select(0, ids)),
+                                    oracle._np(b.v_pool.index_select(0, ids)), lists, b.seq_lens, b.cur_lens,
+                                    nthreads=NTHREADS)
+    want16 = oracle.paged_attention(q, oracle._np(kb.index_select(0, ids)), oracle._np(vb.index_select(0, ids)),
+                                    lists, b.seq_lens, b.cur_lens, nthreads=NTHREADS)
+    g = got.float().cpu().numpy()
+    e32 = np.abs(g - want32).reshape(len(rows), -1).max(axis=1)
+    e16 = np.abs(g - want16).reshape(len(rows), -1).max(axis=1)
+    for r, L, a, c in zip(rows, b.seq_lens, e32, e16):
+        print(f"  request {r:3d} L={L:5d}: max err vs unrounded fp32 {a:.2e}, vs same bf16 values {c:.2e}",
+              flush=True)
+    print(f"  worst: {e32.max():.2e} vs unrounded fp32 (bound 2e-2), {e16.max():.2e} vs bf16 values (1e-4)",
+          flush=True)
+    assert float(e32.max()) <= 2e-2
+    assert float(e16.max()) <= 1e-4
+    del b, kb, vb
+    torch.cuda.empty_cache()

@@ -93,12 +93,24 @@ def test_noalloc_without_split_and_over_the_limit(device):
     got = call(lb, b, 0, noalloc=True)  # no split: the scratch is not touched
     assert torch.equal(got, call(lb, b, 0, noalloc=False))
     # 64 requests x 64 heads x 2048 pages in 1-block splits need far more than the array: the
-    # call is refused on the host before anything is launched (the pointers are never read)
+    # call is refused on the host before anything is launched. Every pointer is a real device
+    # buffer of the stated size, and every request is empty (length 0, a page table of -1), so a
+    # launch, had the host check been skipped, would only write zeros into `out` (no split record
+    # is written for an empty request) and the assertion on `out` below would report it.
     B, H, Hd, pages = 64, 64, 128, 2048
     assert lb.pa_decode_workspace_size(B, H, Hd, pages, 1) > SCRATCH_BYTES
-    A = 0x10000
-    st = lb.pa_decode_noalloc(A, 0, 0, A, 0, 0, _lib.PA_DTYPE_F32, A, A, _lib.PA_DTYPE_BF16, 4096,
-                              A, pages, pages, A, A, None, B, H, Hd, 16, 0.1, 1,
-                              torch.cuda.current_stream(device).cuda_stream)
+    q = torch.zeros(B, H, 1, Hd, device=device)
+    out = torch.full_like(q, float("nan"))
+    k = torch.zeros(1, H, 16, Hd, dtype=torch.bfloat16, device=device)
+    v = torch.zeros_like(k)
+    pt = torch.full((B, pages), -1, dtype=torch.int32, device=device)
+    lens = torch.zeros(B, dtype=torch.int32, device=device)
+    cur = torch.ones(B, dtype=torch.int32, device=device)
+    st = lb.pa_decode_noalloc(q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+                              _lib.PA_DTYPE_F32, k.data_ptr(), v.data_ptr(), _lib.PA_DTYPE_BF16, k.shape[0],
+                              pt.data_ptr(), pt.stride(0), pages, lens.data_ptr(), cur.data_ptr(), None,
+                              B, H, Hd, 16, 0.1, 1, torch.cuda.current_stream(device).cuda_stream)
+    torch.cuda.synchronize()
     assert st == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"fixed scratch" in lb.pa_last_error_message()
+    assert bool(torch.isnan(out).all()), "the refused call must not launch"
