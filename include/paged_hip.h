@@ -296,6 +296,16 @@ int pa_embed_rows(const int64_t* ids, const int64_t* pos_start, int32_t batch, i
 int pa_argmax_rows(const void* logits, int64_t row_stride, int32_t batch, int32_t rows_per_request,
                    const int32_t* row_index, int32_t vocab, int dtype, int64_t* tokens, void* stream);
 
+/*
+ * pa_hbm_read_probe: reads `bytes` (a multiple of 16) of device memory at `src` once, with the
+ * 16-byte non-temporal vector loads pa_decode streams KV tiles with, over `workgroups`
+ * workgroups of 512 threads; `sink` is a device buffer of `workgroups` uint32 words, which the
+ * probe may write for a non-zero buffer (a buffer of zeros leaves it untouched). No counterpart
+ * in the reference: it lets a benchmark state the read bandwidth the box delivers beside the
+ * decode kernel's, separating the box from the kernel.
+ */
+int pa_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, int32_t workgroups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
