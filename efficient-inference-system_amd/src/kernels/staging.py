@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 
 import numpy as np
 import torch
@@ -142,13 +143,21 @@ def upload_into(arr: np.ndarray, dst: torch.Tensor) -> None:
 _HOST_MAPPED_COHERENT = 0x2 | 0x40000000  # hipHostMallocMapped | hipHostMallocCoherent
 
 
+def _free_mapped(host_ptr: int, event) -> tuple[int, int, int]:
+    """Wait for the last launch recorded on `event`, then free the pinned words and the event;
+    returns the three HIP statuses. Holds no reference to the MappedHostWords it frees."""
+    return (_hip.event_sync(event), _hip.host_free(ctypes.c_void_p(host_ptr)), _hip.event_destroy(event))
+
+
 class MappedHostWords:
     """int32 words of pinned host memory that kernels read (and write) directly: allocated with
     hipHostMalloc as mapped, coherent memory, so a kernel sees the host's latest stores without a
     copy call and without stale cache lines. The host must not rewrite words a launch reads until
     that launch has run: mark(stream) after enqueueing such a launch, wait() before the next
     rewrite (an event; free when the launch has already finished). close() frees it, once no
-    launch that reads it can run again (the graphs captured with its device address are gone)."""
+    launch that reads it can run again (the graphs captured with its device address are gone).
+    An object dropped without close() is freed the same way when it is collected (its owner, a
+    captured step, drops the graph with it); at interpreter exit the process releases it."""
 
     def __init__(self, words: int, device: torch.device):
         hip = _runtime()
@@ -165,6 +174,8 @@ class MappedHostWords:
         self.device_ptr = dptr.value
         self.event = ev
         self.pending = False
+        self._finalizer = weakref.finalize(self, _free_mapped, ptr.value, ev)
+        self._finalizer.atexit = False
 
     def device_addr(self, word: int = 0) -> int:
         return self.device_ptr + 4 * word
@@ -182,8 +193,10 @@ class MappedHostWords:
         """Wait for the last marked launch, then free the memory and the event (idempotent)."""
         if self.host_ptr is None:
             return
-        self.wait()
         self.words = None
-        _check(_hip.host_free(ctypes.c_void_p(self.host_ptr)), "hipHostFree")
-        _check(_hip.event_destroy(self.event), "hipEventDestroy")
+        self.pending = False
+        sync, free, destroy = self._finalizer()
         self.host_ptr = self.device_ptr = self.event = None
+        _check(sync, "hipEventSynchronize")
+        _check(free, "hipHostFree")
+        _check(destroy, "hipEventDestroy")

@@ -188,3 +188,27 @@ def test_dropped_graphs_free_their_descriptors(device, monkeypatch):
         pos += T
     runner = graphed._graph_step
     assert runner.captured and all(c.desc.host_ptr is not None for c in runner.captured.values())
+
+
+def test_step_descriptors_are_freed_with_the_model(device):
+    """Each captured step owns pinned, mapped descriptor words and an event; dropping the model
+    without releasing its graphs frees them when the captures are collected."""
+    import gc
+
+    from src.kernels.staging import MappedHostWords
+
+    words = MappedHostWords(64, device)
+    fin = words._finalizer
+    del words
+    gc.collect()
+    assert not fin.alive
+
+    m = make(device)
+    with torch.no_grad():
+        assert m.prepare_graphs(2, device) > 0
+    fins = [cap.desc._finalizer for cap in m._graph_step.captured.values()]
+    assert fins and all(f.alive for f in fins)
+    del m
+    gc.collect()
+    torch.cuda.synchronize()
+    assert not any(f.alive for f in fins)
