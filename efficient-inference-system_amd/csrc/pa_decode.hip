@@ -193,8 +193,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
   // The first chunk of this wave's page-table entries (block jb0 + w + lane * NW) does not depend
   // on the request's length: load it now, clamped into the row, so that it travels with the
   // length loads instead of after them (one dependent memory round trip less before the first
-  // KV tile; graph replay: single decode 3.27 -> 3.19 us, ragged 8 x 8 heads 9.16 -> 9.08 us per
-  // layer). Entries past the request's blocks are discarded below.
+  // KV tile). Entries past the request's blocks are discarded below.
   const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
   const int jb0 = nsplit > 1 ? split * a.split_blocks : 0;
   int ids0 = -1;
@@ -298,15 +297,11 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
 }
 
 // Merge the partial records (m, l, acc[HD]) of each (request, head) written by its active splits
-// (the number a split computes from the request's length): one wavefront per pair. (A merge in
-// the split launch itself, by the split that completes a per-pair counter after an agent-scope
-// release, was measured and dropped: the fences made the small ragged decode, 8 x 8 heads x 64
-// over 128-1024 keys, take 12.4 / 19.2 / 33.4 us per layer at 32 / 16 / 8-block splits, against
-// 10.2 / 8.4 / 8.4 us with this second launch and 8.4 us unsplit.) The loads are
+// (the number a split computes from the request's length): one wavefront per pair. The loads are
 // spread over the lanes and issued together: lane s reads split s's (m, l) for the maximum and
 // the denominator, and each lane's head_dim element is summed over the splits with the weights
-// broadcast from the lane that computed them, eight independent loads at a time. (A loop over
-// the splits with one dependent load chain per split cost 4-10 us at 4-8 splits.)
+// broadcast from the lane that computed them, eight independent loads at a time (a loop over the
+// splits with one dependent load chain per split is several times slower).
 template <typename IO>
 __global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
   const int bh = blockIdx.x;

@@ -91,7 +91,7 @@ __device__ __forceinline__ int64_t lin_x_row(const LinArgs& a, int m) {
 }
 
 // Wavefronts per workgroup (they split K): 16 at K = 2048 keeps more of the 128 KB weight tile in
-// flight per compute unit (fc2 of the benchmark model, 8 rows: 9.3 -> 8.2 us inside a graph).
+// flight per compute unit.
 template <int K>
 constexpr int lin_waves() { return K >= 2048 ? 16 : 8; }
 
@@ -134,10 +134,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // L1 serves one line per 4-lane group per access; LDS-direct copies of each wavefront's slice
 // read every row contiguously (one line per 4-lane group) and the operands are then read from LDS,
 // with each row's 16-byte chunks XOR-swizzled by row so that the 16 rows of a read hit every bank
-// once. Measured inside graphs (registers -> LDS, us), benchmark model, 8 rows: LayerNorm + q/k/v
-// fp32 4.73 -> 4.41, bf16 4.11 -> 4.02; out_proj 3.46 -> 3.29, 2.97 -> 2.82; LayerNorm + fc1 +
-// GELU 4.82 -> 4.53, 4.25 -> 4.15; fc2 7.26 -> 6.72, 4.23 -> 3.42; LayerNorm + lm_head 6.88 ->
-// 5.92, 5.57 -> 4.82; 256 rows: q/k/v fp32 17.3 -> 13.9, fc2 fp32 28.9 -> 16.5, bf16 9.5 -> 6.5.
+// once.
 template <int K, bool LN, typename T, bool STG = false>
 __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(const LinArgs a) {
   constexpr bool BF = sizeof(T) == 2;
@@ -383,10 +380,8 @@ static bool small_linear_k_supported(int32_t K) {
 #endif
 
 // Column tile width: the widest of 16, 8, 4 columns whose grid still has 192 workgroups with a
-// LayerNorm prologue (each workgroup normalises its rows again) or 128 without (else 4).
-// Measured inside graphs at 8 rows, fp32 / bf16 (us): fc2 (K 2048, N 512) 8.2 / 4.8 with 16
-// columns, 7.2 / 4.2 with 4; out_proj (K 512, N 512) 3.6 / 2.6 -> 3.3 / 2.7; LayerNorm + fc1
-// (N 2048) 4.9 / 3.9 with 16, 4.7 / 4.0 with 8, 6.4 / 5.3 with 4; lm_head (N 5000) best with 16.
+// LayerNorm prologue (each workgroup normalises its rows again) or 128 without (else 4), so
+// narrow layers spread their weight stream over more compute units.
 static int lin_cw_log2(const LinArgs& a) {
   if (PA_LIN_FORCE_CW_LOG2) return PA_LIN_FORCE_CW_LOG2;
   const int64_t target = a.ln_w != nullptr ? 192 : 128;

@@ -20,8 +20,7 @@
 //
 // KV staging. The K operand puts key row c on lane c, so a load straight into the operand
 // registers has every 4-lane group of an instruction touching 4 cache lines; the compute unit's L1
-// serves one line per lane group per access, and on the chunked workload with bf16 KV that made
-// the walk L1-bound (11.3 us against 7.7-8.1 us for a copy without the walk's KV loads). At
+// serves one line per lane group per access, which made the walk L1-bound with bf16 KV. At
 // head_dim 64 (and 128 with bf16 KV) each wavefront instead copies its blocks' K and V slabs into
 // its own two-stage LDS ring with LDS-direct loads, which read the contiguous slab 16 bytes per
 // lane (one line per lane group), and reads the operands from LDS (prefill_stage_in_lds picks the
@@ -32,8 +31,8 @@
 // equal-sized items instead of a few long ones. A unit with one active split writes its output
 // directly; otherwise each split writes its (m, l, acc) rows to the workspace and
 // prefill_merge_kernel combines them. (A same-launch merge by the last split to finish needs
-// agent-scope fences, which write back the die-local L2 in every workgroup: on MI355X that made
-// split launches 5-20x slower than the second launch.)
+// agent-scope fences, which write back the die-local L2 in every workgroup: slower on MI355X than
+// the second launch.)
 #include <stdlib.h>
 #include <string.h>
 
@@ -46,13 +45,10 @@ namespace pa {
 // Work unit -> ((request, head) pair, 16-row query tile). The tiles of one pair read the same KV
 // blocks, and workgroup x runs on die x % kXcds, each die with its own L2. When the pairs divide
 // evenly over the dies, pair p's tiles all go to die p % kXcds, so each die's L2 holds only its
-// pairs' KV (chunked workload, 4 x 8 heads: 1.4 MB per die instead of all 11 MB on every die;
-// fp32 KV 23.1 -> 22.0 us, bf16 KV 13.5 -> 12.3 us, graph replay, three interleaved runs).
-// Within a die, its i-th workgroup and the one half a die's worth later share a compute unit under
-// round-robin dispatch: the first half of the die's pairs walks its tiles from the last
-// (heaviest) one, the second half from the first, so a heavy tile pairs with a light one
-// (chunked workload, fp32 KV: 24.6 -> 23.9 us). Otherwise units stay pair-major with the same
-// descending / ascending halves over all pairs.
+// pairs' KV. Within a die, its i-th workgroup and the one half a die's worth later share a compute
+// unit under round-robin dispatch: the first half of the die's pairs walks its tiles from the last
+// (heaviest) one, the second half from the first, so a heavy tile pairs with a light one.
+// Otherwise units stay pair-major with the same descending / ascending halves over all pairs.
 __device__ __forceinline__ void prefill_unit(int unit, int ntiles, int pairs, int& bh, int& qt) {
   int y = unit, lanes = 1, lane = 0;
   if (pairs % kXcds == 0) {
@@ -96,17 +92,9 @@ struct PrefillShape {
   static constexpr int VW = kBf16 ? DT / 2 : DT;  // 32-bit words per V row per lane per block
 };
 
-// Wavefronts per workgroup of the 16-row kernel (they split each tile's KV blocks). Measured in
-// graph replay with the die-aware unit order: fp32 KV 20.4 us with 4, 22.5 us with 8, 27.8 us with
-// 8 and two tiles in flight, 29.2 us with 16 on the chunked-prefill workload (4 x 8 heads x 64);
-// 217 against 252 us with 8 on 4 x 32 heads x 128, 256-token chunks over 0.6-1.2k contexts; within
-// 0.4 us either way on single requests. bf16 KV: 12.3-12.7 us with 4, 13.4-13.8 with 8, 19.0 with
-// 16 (chunked workload), 99 against 128 us with 8 (4 x 32 heads x 128). Measured again on the current
-// kernel (three wavefronts per SIMD fit its registers at 6 per workgroup): 5 and 6 wavefronts, fp32
-// KV 21.5-21.6 and 22.1-22.4 us against 18.3; bf16 12.2 and 12.5-12.7 against 11.4-11.5. With the
-// KV staged through LDS and the one-pass merge, 8 wavefronts for bf16 KV (4 per SIMD at 2
-// workgroups per CU): chunked 9.2 -> 9.6 us, 128/256 mix 9.4 -> 10.6, 8 x 8 heads 11.4 -> 15.3,
-// 4 x 32 heads x 128 58 -> 71, only 2 x 8 heads x 128 14.3 -> 12.4.
+// Wavefronts per workgroup of the 16-row kernel (they split each tile's KV blocks): four, two per
+// SIMD at the kernel's register use. More wavefronts per tile lengthen the merge and leave fewer
+// workgroups per CU, which measured slower for both KV types.
 #ifndef PA_PREFILL_WAVES_F32
 #define PA_PREFILL_WAVES_F32 4
 #endif
@@ -116,14 +104,8 @@ struct PrefillShape {
 template <typename KV>
 constexpr int prefill_waves() { return std::is_same<KV, float>::value ? PA_PREFILL_WAVES_F32 : PA_PREFILL_WAVES_BF16; }
 
-// KV tiles each wavefront keeps in flight ahead of the one it folds. Measured in graph replay
-// (16-row kernel): at head_dim 64 one tile is best (chunked workload 4 x 8 heads, bf16 KV 13.6 us
-// at 1, 14.5 at 2, 15.0 at 3; fp32 22.8 us at 1, 29.5 at 2, where the registers cost a
-// wavefront per SIMD; with 4 wavefronts per workgroup and the die-aware order, 20.0 at 1 and 20.9
-// at 2); at head_dim 128, 4 requests x 32 heads, 256-token chunks over ~1k contexts, bf16 KV
-// 109.6 us at 1, 102-105 at 2 or 3; fp32 KV spills beyond 1. Measured again on the current kernel
-// (chunked workload, three interleaved runs): bf16 KV 11.5-11.7 us at 1, 11.9-12.0 at 2, 12.1-12.7
-// at 3; fp32 KV 18.4-18.8 at 1, 19.8-20.0 at 2 (and 8 x 8 heads fp32 25 -> 54 us).
+// KV tiles each wavefront keeps in flight ahead of the one it folds: one, except two for bf16 KV
+// at head_dim 128. More costs registers (a wavefront per SIMD) without hiding more latency.
 #ifndef PA_PREFILL_DEPTH_F32_64
 #define PA_PREFILL_DEPTH_F32_64 1
 #endif
@@ -136,43 +118,12 @@ constexpr int prefill_waves() { return std::is_same<KV, float>::value ? PA_PREFI
 #ifndef PA_PREFILL_DEPTH_BF16_128
 #define PA_PREFILL_DEPTH_BF16_128 2
 #endif
-// KV blocks folded per softmax round. One: folding two blocks per round (interleaved QK^T chains,
-// one max/sum exchange and rescale test per 32 keys) measured slower at head_dim 64 in graph replay
-// on the chunked workload (fp32 KV 18.8 -> 22.1-22.6 us with 218 instead of 129 registers; bf16
-// 11.6 -> 12.0-12.2 us; 8 x 8 heads bf16 15.0 -> 20.2 us), and does not fit two wavefronts per SIMD
-// at head_dim 128. Starting each tile's walk at a tile-dependent rotation, so the tiles of one
-// pair do not request a block at the same moment, changed nothing (18.7-18.8 us).
-// Also measured on the chunked workload (graph replay, three interleaved runs, one box) and not
-// kept: software-pipelining the walk so that block k+1's QK^T MFMAs overlap block k's softmax
-// (three-tile ring, with or without branch-free masking and rescaling): fp32 KV 18.5 -> 19.4-20.5
-// us, bf16 11.5 -> 11.9-12.2 us; two or four independent QK^T accumulators instead of one chain:
-// fp32 18.4 -> 19.0-19.3 us; 8-wavefront workgroups that own a heavy and a light tile and deal the
-// union of their blocks to all 8 wavefronts (every wavefront within one block of the mean, no
-// wavefront alone on its SIMD): fp32 18.4 -> 21.4 us, bf16 11.5 -> 13.4 us. A per-wavefront trace
-// of the last one showed why: a SIMD finishes the same number of blocks at the same time either
-// way (a heavy tile's wavefront left alone on its SIMD runs about a third faster per block), while
-// loading both units' queries and merging 8 partial states per unit lengthen the prologue (1.1 ->
-// 1.9 us) and the epilogue. Dealing the 16-byte chunks of each K (and q) row round-robin to the
-// four lane groups, so that one load instruction reads one 64-byte line per key row instead of
-// 16 bytes from each of four lines: no change (fp32 18.2-18.4 us, bf16 11.4-11.6 us). fp32 KV
-// through the bf16 matrix cores (every fp32 operand split into bf16 hi + lo, products hi*hi +
-// hi*lo + lo*hi accumulated in fp32: 3.5x less matrix-pipe time, ~1e-5 error): 18.5 -> 17.6 us.
-// So the kernel is not matrix-bound: with bf16 KV (1/16 of the fp32 MFMA time, half the bytes)
-// it still takes 11.5 us. Timing copies without the KV loads in the walk take 7.7-8.1 us (bf16)
-// and 15.6-17.4 us (fp32): with register staging the loads cost about a third of the bf16 time.
-// Counters (TCP_TCP_LATENCY / TA_TCP_STATE_READ, TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ,
-// TA_ADDR_STALLED_BY_TC_CYCLES, TCP_TOTAL_CACHE_ACCESSES) place that cost in the compute unit's L1:
-// a load instruction spends ~1,170 cycles there, an L2 request ~160, L2 hits 88%, the address path
-// waits on L1 a quarter of the time, and ~210 L1 accesses per (tile, bf16 block) item match one
-// access per lane for the K rows: what the LDS staging removes. Not kept, each measured in graph
-// replay against the register-staged kernel: two query tiles per
-// workgroup folding every KV tile into both (half the loads per item; one wavefront per SIMD at
-// 256 workgroups): fp32 18.3 -> 23.1 us, bf16 11.4 -> 12.2 (a 128/256 chunk mix 13.4 -> 12.4);
-// non-temporal KV loads: fp32 18.2 -> 19.2, bf16 unchanged; a tile-dependent rotation of each
-// tile's walk: bf16 11.4 -> 11.6; KV pools of 200 to 32768 blocks, ids scattered or sorted: within
-// 0.4 us (not translation-bound); the wavefronts' states rescaled before the LDS merge so the final
-// pass is plain sums: unchanged. The lazy rescale test per lane and one lane read per block for
-// the block address (about 60 instead of 100 instructions per bf16 block): bf16 11.5 -> 11.3 us.
+// KV blocks folded per softmax round: one. Two per round (interleaved QK^T chains, one max / sum
+// exchange and rescale test per 32 keys) costs more registers than it saves and does not fit two
+// wavefronts per SIMD at head_dim 128. The walk is bound neither by the matrix cores (bf16 KV has
+// 1/16 of fp32's MFMA time and is not 16x faster) nor by its instruction count; with K loaded
+// straight into the operand registers (key row per lane, four cache lines per 4-lane group) it
+// is bound by the compute unit's L1, which the LDS staging of prefill_stage_in_lds removes.
 template <typename KV, int HD, bool OCC4>
 constexpr int prefill_round() { return 1; }
 
@@ -186,10 +137,8 @@ constexpr int prefill_depth() {
 }
 
 // OCC4: registers capped at 128 so that 4 wavefronts share a SIMD (4 workgroups per CU instead of
-// 3). Only fp32 KV at head_dim 64 is near the cap (129 registers unconstrained, 128 and two
-// spilled values capped); the launch takes the capped build when the grid would not fit on the
-// GPU at 3 workgroups per CU (8 x 8 heads x 256 rows, 1024 workgroups: 39.3 -> 33.3 us), and the
-// unconstrained one otherwise (chunked workload, 512 workgroups: 20.4 us against 21.3 capped).
+// 3). Only fp32 KV at head_dim 64 is near the cap; the launch takes the capped build when the grid
+// would not fit on the GPU at 3 workgroups per CU, and the unconstrained one otherwise.
 template <typename KV, typename IO, int HD, bool OCC4 = false, bool LDSK = false>
 __global__ __launch_bounds__(prefill_waves<KV>() * kWave) __attribute__((amdgpu_waves_per_eu(OCC4 ? 4 : 1)))
 void prefill_mfma_kernel(const AttnArgs a) {
@@ -375,9 +324,8 @@ void prefill_mfma_kernel(const AttnArgs a) {
       }
     // ---- O^T += V^T P^T -----------------------------------------------------------------------
     // fp32 KV at head_dim 128: the PV MFMAs run at raised wavefront priority, so a wavefront that
-    // reaches them issues ahead of co-resident ones still in their softmax (4 requests x 32
-    // heads, 256-token chunks over ~1k contexts: 292.5 -> 267.9 us over three interleaved runs;
-    // no change at head_dim 64 or for bf16 KV, where it stays off).
+    // reaches them issues ahead of co-resident ones still in their softmax (faster there; no
+    // change at head_dim 64 or for bf16 KV, where it stays off).
     constexpr bool kPrio = !kBf16 && HD == 128;
     if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
     if constexpr (!kBf16) {
@@ -547,13 +495,7 @@ void prefill_mfma_kernel(const AttnArgs a) {
   // Lane (G, c) holds head_dim d = (4G + r) * DT + t of query column c in oacc[t][r]: for each r
   // the DT values over t are consecutive, so they go to LDS as DT / 4 16-byte vectors. Then 16
   // threads per column combine the wavefronts' states, each over DT consecutive head_dim values,
-  // in one pass. (The earlier loop over 16 * HD / 256 outputs per thread, each with its own scalar
-  // LDS reads and max / exp chain, took 1.1-1.7 us per wavefront after the barrier; this one
-  // 0.5-0.7 us. Graph replay: chunked workload bf16 KV 10.0 -> 9.2 us, fp32 19.2 -> 18.3 us.)
-  // Measured and not kept: moving the q loads ahead of the inactive-split return and making all
-  // argument loads go out in one batch, which brings q, the lengths and the page-table chunk ~0.3
-  // us earlier: fp32 unchanged, bf16 KV 9.2 -> 9.4-9.7 us (the wavefronts of a (request, head)
-  // then request its first blocks more nearly at once).
+  // in one pass, with vector LDS reads instead of a scalar read and max / exp chain per output.
   l = sum_xor32(sum_xor16(l));
 #pragma unroll
   for (int r = 0; r < 4; ++r)
@@ -647,33 +589,11 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnArgs a) {
   }
 }
 
-// KV staging of the 16-row kernel at head_dim 64 (graph replay, MI355X):
-//   through LDS: bf16 KV chunked workload 11.3 -> 9.7 us (4 x 8 heads, four 256-token chunks),
-//   13.3 -> 9.6 us (a 128/256 chunk mix), 8 x 8 heads 14.7 -> 12.0 us; fp32 KV 18.3 -> 18.3 us and
-//   21.6 -> 21.2 us on the same two, but 25.6 -> 29.9 us on 8 x 8 heads (1024 workgroups: its 64 KB
-//   of LDS per workgroup allow 2 per CU where the register-staged build fits 4).
-// bf16 KV at head_dim 128 (66 KB of LDS, 108 instead of 186 registers): 4 x 32 heads, 256-token
-// chunks over ~1k contexts 99 -> 69-72 us; 2 x 8 heads 9.0 -> 7.8 us; 1 x 32 heads, a 128-token chunk
-// 10.0 -> 8.5 us (fp32 KV at head_dim 128 would need 128 KB per workgroup: registers only).
-// So: LDS for bf16 KV always, for fp32 KV while the grid fits 2 workgroups per CU. Also measured
-// on the LDS staging and not kept: a three-stage ring for bf16 KV (two blocks ahead): 9.6 ->
-// 9.35 us on the chunked workload, 11.7 -> 14.5 us on 8 x 8 heads (48 KB per workgroup, 3 per CU);
-// measured again after the one-pass merge, 2 / 3 / 4 stages (1 / 2 / 3 blocks ahead): chunked
-// 9.0 / 9.0 / 9.0 us, 128/256 mix 8.9 / 9.1 / 9.3, 8 x 8 heads 10.7 / 13.6 / 13.2;
-// putting two tiles of the same (request, head) on each compute unit (tiles t and 15 - t, so the
-// pair's second read of a block can hit L1): bf16 9.6 -> 9.4 us, fp32 18.3 -> 20.4 us (the
-// requests' different lengths then unbalance the compute units); two adjacent 16-row tiles per
-// wavefront in 8-wavefront workgroups of 32 rows, each staged block folded into both tiles (two
-// independent MFMA and softmax chains, half the block walks per wavefront at the same wavefronts
-// per SIMD; parity green): bf16 9.5 -> 10.2 us (chunked), 9.6 -> 10.1 (128/256 mix), 11.6 -> 14.1
-// (8 x 8 heads), 4.8 -> 6.8 (2 x 8 heads, 64 rows); fp32 18.5 -> 22.5, 20.8 -> 21.3, 24.5 -> 24.4,
-// 6.1 -> 9.3, so the walk is not bound by its per-block memory round trips either; one
-// 8-wavefront workgroup per heavy/light unit pair (the pair that shares a compute unit), the union
-// of their blocks dealt round-robin to its wavefronts from page-table rows staged in LDS, each
-// wavefront keeping a state per unit (parity green): every wavefront walks 8-10 blocks instead of
-// 3-15, but a block then costs 0.47 instead of 0.36 us and the prologue grows by 1.8 us (bf16
-// 9.0 -> 10.6 us, fp32 17.9 -> 20.0 us; with the blocks drawn from per-unit LDS counters instead
-// 12.5 and 20.6 us).
+// KV staging of the 16-row kernel: through LDS for bf16 KV always (both head_dims), and for fp32
+// KV at head_dim 64 only while the grid fits 2 workgroups per CU: its 64 KB of LDS per workgroup
+// halves the workgroups a CU holds against the register-staged build, which wins on larger grids
+// (fp32 KV at head_dim 128 would need 128 KB per workgroup: registers only). The ring has two
+// stages (one block ahead); deeper rings cost workgroups per CU without hiding more.
 // PAGED_HIP_PREFILL_STAGING=lds / regs forces one of them (tests cover both).
 static bool prefill_stage_in_lds(bool fp32_kv, unsigned grid) {
   const char* env = getenv("PAGED_HIP_PREFILL_STAGING");
@@ -723,23 +643,11 @@ static bool prefill_fast_shape(int32_t head_dim, int32_t block_size) {
 }
 
 // Kernel choice between the wide-tile kernel (128 query rows per workgroup) and the 16-row one, by
-// the wide kernel's unit count U = B * H * ceil(T / 128) against the CU count (256), graph replay on
-// MI355X (16-row / wide, us). bf16 KV, 16-row kernel with its KV staged through LDS:
-//   U = 384: 52.6 / 35.9 (6 x 32 heads x 64, T 256, ~1k contexts);
-//   U = 256: 64.4 / 50.9 (4 x 32 x 128, T 256, ~1k), 95.4 / 63.9 (2 x 32, T 512, ~2k), 136.9 / 98.0
-//            (1 x 32, T 1024, ~3k), 32.7 / 30.3 (4 x 32 x 64, T 256, ~1k);
-//   U = 192: 45.4 / 35.0 (3 x 32 x 128, T 256, ~1k), 113.6 / 97.2 (same, 3-4k), 80.1 / 78.0
-//            (12 x 8 x 128, T 256, ~2k), 99.8 / 84.6 (2 x 32 x 128, T 384, ~3k);
-//   U = 128: 76.6 / 93.4 (2 x 32 x 128, T 256, 3-4k), 12.8 / 18.8 (8 x 8 x 64, T 256, 0-700), 81.3 /
-//            110.5 (4 x 16 x 128, T 256, 3-4k), 52.6 / 70.2 (4 x 32 x 128, T 128, ~2k), 72.2 / 85.4
-//            (1 x 32 x 128, T 512, ~3k);
-//   U = 64:  25.7 / 54.7 (2 x 16 x 128, T 256, ~2k).
-// fp32 KV (16-row kernel with registers at head_dim 128): U = 256, head_dim 128: 227.6 / 214.6,
-//   416.6 / 351.3, 688.8 / 556.1; head_dim 64: 112.7 / 132.6; U = 128: 365.1 / 582.0 (head_dim 128),
-//   34.3 / 83.3 (64).
-// So: the wide kernel from U >= 2 CUs always; for bf16 KV from U >= 3/4 of the CUs; for fp32 KV at
-// head_dim 128 from U >= CUs. PAGED_HIP_PREFILL_KERNEL=wide / tile forces one of them (tests use
-// it to cover both at small sizes).
+// the wide kernel's unit count U = B * H * ceil(T / 128) against the CU count. The wide kernel
+// shares each staged KV step among 128 rows but needs enough units to fill the GPU: it is taken
+// from U >= 2 CUs always, for bf16 KV from U >= 3/4 of the CUs, and for fp32 KV at head_dim 128
+// from U >= CUs (the crossovers measured on MI355X). PAGED_HIP_PREFILL_KERNEL=wide / tile forces
+// one of them (tests use it to cover both at small sizes).
 static bool use_wide_prefill(int kv_dtype, int32_t head_dim, int32_t batch, int32_t num_heads, int32_t query_len) {
   const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
   if (env != nullptr && strcmp(env, "wide") == 0) return true;
@@ -753,17 +661,10 @@ static bool use_wide_prefill(int kv_dtype, int32_t head_dim, int32_t batch, int3
 
 // Split-step kernel (32-row tiles, 8 wavefronts splitting the KV steps; bf16 KV at head_dim 64)
 // instead of the 16-row kernel, by its unit count U = B * H * ceil(T / 32) (one workgroup per CU
-// at most). Graph replay on MI355X, 16-row / split-step, us, contexts U[0, 768] unless noted:
-//   U = 256: 7.67 / 6.86 (4 x 8 heads, T 256), 8.72 / 7.03 (8 x 8, T 128), 12.78 / 10.39 (4 x 8,
-//            T 256, contexts 0.5-2k), 6.84 / 6.20 (2 x 16, T 256), 8.28 / 6.90 (4 x 16, T 128),
-//            6.78 / 6.19 (1 x 32, T 256); the chunked workload 9.2 / 8.2, its 128/256 mix 9.2 / 7.5;
-//   U = 192: 7.80 / 6.65 (3 x 8, T 256);
-//   U = 128: 6.50 / 6.02 (2 x 8, T 256), 7.25 / 6.62 (4 x 8, T 128), but 5.57 / 5.90 (8 x 8, T 64,
-//            contexts 0-512);
-//   U = 64:  4.92 / 5.10, 5.08 / 5.13, 5.43 / 5.81 (T 64), 7.66 / 7.30 (8 x 8, T 32);
-//   U = 384: 10.27 / 10.73 (two rounds); U = 512: 10.8 / 10.9.
-// So: from half the CUs to the CU count, for chunks longer than 64 rows.
-// PAGED_HIP_PREFILL_KERNEL=split forces it where it applies (tile forces the 16-row kernel).
+// at most): it is taken from half the CUs to the CU count for chunks longer than 64 rows, where it
+// measured faster on MI355X; below half the CUs or for short chunks the 16-row kernel's extra
+// workgroups win. PAGED_HIP_PREFILL_KERNEL=split forces it where it applies (tile forces the
+// 16-row kernel).
 static bool use_split_prefill(int32_t batch, int32_t num_heads, int32_t query_len) {
   const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
   if (env != nullptr && strcmp(env, "split") == 0) return true;

@@ -123,10 +123,9 @@ __device__ __forceinline__ bool wide_lpt_unit(const AttnArgs& a, int ntiles, int
 }
 
 // NSUB = 32-key sub-tiles per step: the per-step costs (barrier, mask test, max/sum exchange,
-// lazy-rescale test) are paid once per NSUB * 32 keys. Measured on the large-prefill workload
-// (8 x 32 heads, chunk 512 over 1.8-3.7k contexts), same box, head_dim 64: NSUB 2 with 2 stages
-// 133-137 us, with 3 stages 148-150 us (48 KB of LDS: 3 workgroups per CU instead of 4), NSUB 1
-// 140-146 us. Head_dim 128 takes one of two shapes by grid size (wide128_pair below).
+// lazy-rescale test) are paid once per NSUB * 32 keys. Head_dim 64 uses NSUB 2 with 2 stages
+// (a third stage's LDS costs a workgroup per CU). Head_dim 128 takes one of two shapes by grid
+// size (wide128_pair below).
 #ifndef WIDE_NSUB64
 #define WIDE_NSUB64 2
 #endif
@@ -138,12 +137,8 @@ constexpr int kWideNsub64 = WIDE_NSUB64;
 constexpr int kWideStages64 = WIDE_NST64;
 // Head_dim 128, bf16 KV: NSUB 2 with 2 stages (174 registers, 64 KB of LDS: 2 workgroups per CU)
 // when the grid fits in one round at 2 workgroups per CU, else NSUB 1 with 2 stages (154
-// registers, 32 KB: 3 per CU, registers being the limit). Measured in one process per build,
-// interleaved, bench.py's workloads (8 x 32 heads, 512-token chunks: 1024 units; 4 x 32 heads,
-// 256-token chunks: 256 units; and 12 x 32 heads over uniform 2688-token contexts: 1536 units):
-//   NSUB 1, 3 stages (the earlier choice)  250 / 58 / 392-394 us
-//   NSUB 1, 2 stages                       244 / 58 / 377-381 us
-//   NSUB 2, 2 stages                       241-245 / 49-52 / 419-421 us
+// registers, 32 KB: 3 per CU, registers being the limit): the wider step pays only when no second
+// round of workgroups needs the CU slots it holds.
 static bool wide128_pair(int64_t units) { return units <= 2 * (int64_t)pa_host::device_cu_count(); }
 
 template <typename IO, int HD, int NSUB, int NST>
@@ -162,9 +157,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   constexpr int TILE = KS * HD;          // elements per K (or V) tile
 
   static_assert(NST == 2 || NST == 3, "stages");
-  // Stage s: K tile at sbuf + 2 * s * TILE, V tile right after it. (One array addressed through
-  // per-stage pointers: 154-160 registers at head_dim 128 against 164 with one array per tile;
-  // large prefill 252-273 against 268-273 us, four interleaved runs.)
+  // Stage s: K tile at sbuf + 2 * s * TILE, V tile right after it (one array addressed through
+  // per-stage pointers takes fewer registers than one array per tile).
   __shared__ __attribute__((aligned(16))) uint16_t sbuf[NST * 2 * TILE];
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -355,9 +349,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
     // ---- O^T += V^T P^T: MFMA (u2, mm, d) contracts keys 32u2 + 16mm + 8jj + 4*G2 + r at slot
     // (G2, 4jj + r), i.e. the lane's registers 8mm + 4jj + r ----------------------------------
     // The PV MFMAs run at raised wavefront priority, so a wavefront that reaches them issues
-    // ahead of co-resident wavefronts still in their softmax and the matrix pipe stays fed
-    // (large prefill, head_dim 128: 297 -> 290 us averaged over six interleaved runs; the same
-    // around the QK^T MFMAs costs 20 registers and a wavefront per SIMD).
+    // ahead of co-resident wavefronts still in their softmax and the matrix pipe stays fed (the
+    // same around the QK^T MFMAs costs 20 registers and a wavefront per SIMD).
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int u2 = 0; u2 < NSUB; ++u2)
@@ -395,7 +388,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
       else __builtin_amdgcn_s_waitcnt(0x0F70);                                           // vmcnt(0)
       __syncthreads();
       // The next stage's loads are issued at raised priority too, so they start right after
-      // the barrier (286.0 -> 278.2 us, head_dim 128, three interleaved runs).
+      // the barrier.
       __builtin_amdgcn_s_setprio(1);
       if (st + NST - 1 < nsteps) issue_loads(st + NST - 1, en, skn, svn);
       __builtin_amdgcn_s_setprio(0);
@@ -585,8 +578,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
     }
     l += sum_xor32(ps);
     // ---- O^T += V^T P^T: four keys (one row group j) at a time ----------------------------------
-    // At raised wavefront priority, as in the bf16 kernel (large prefill: head_dim 128 1775 -> 1757
-    // us, head_dim 64 934 -> 912 us over three interleaved runs).
+    // At raised wavefront priority, as in the bf16 kernel.
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -650,11 +642,6 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
 // lane per exchange, where the 16-row kernel's 16 x 16 blocks give 4. At chunk sizes where the
 // wide kernel's 128-row tiles leave most compute units idle (4 x 8 heads x 256 rows: 64 tiles),
 // this grid has one workgroup per compute unit.
-// Measured and not kept (graph replay, interleaved with the kept kernel on one box): touching a
-// wavefront's next three steps right after its first ring load (one LDS-direct load per step into
-// a junk area, each lane a different 128-byte line of the step's four slabs, so that the later ring
-// loads would hit L2): chunked workload 8.06 -> 9.6 us, and 1.2-1.5 us slower on every other shape
-// (each such load sends 64 lines through the compute unit's L1, ahead of the ring loads).
 constexpr int kSplitWaves = 8;
 constexpr int kSplitRows = 32;
 
@@ -732,10 +719,9 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(cons
   // B operand of S^T = K Q^T: q[i][G2*QH + 8s + e] for MFMA s, pre-scaled, rounded to bf16. Every
   // wavefront needs the same 32 rows: they are read once per workgroup, 16 bytes per thread with
   // consecutive threads along a row, into LDS rows padded by 16 bytes (the 8 rows of a 16-byte read
-  // pass then fall in distinct banks), and each lane reads its half row from there. (Loaded by
-  // every wavefront straight into its registers, the prologue took 3.6 instead of ~2.2 us: 8 copies
-  // of the tile, each load instruction touching 64 rows.) Rows that are not 16-byte aligned take
-  // element loads instead.
+  // pass then fall in distinct banks), and each lane reads its half row from there, instead of 8
+  // copies of the tile loaded by every wavefront with each load instruction touching 64 rows.
+  // Rows that are not 16-byte aligned take element loads instead.
   bf16x8 qb[NQ];
   const float qsc = i < a.T ? a.scale_log2 : 0.f;
   constexpr int64_t kIOB = sizeof(IO);

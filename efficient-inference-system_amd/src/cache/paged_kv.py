@@ -201,19 +201,19 @@ class PagedKVCacheState:
         if k_new.is_cuda:
             BatchedPagedKVCache(states=[self], pool=self.pool).append_batch(k_new, v_new, current_lengths=[length])
             return
-        _, num_heads, _, head_dim = k_new.shape
-        self.pool.ensure_initialized(num_heads, head_dim, k_new.dtype, k_new.device)
-        offset = 0
-        while offset < length:
-            block_offset = self.seq_len % self.pool.block_size
-            if block_offset == 0:
-                self.block_ids.append(self.pool.allocate_block())
-            block_id = self.block_ids[-1]
-            take = min(self.pool.block_size - block_offset, length - offset)
-            self.pool.k_blocks[block_id, :, block_offset:block_offset + take, :] = k_new[0, :, offset:offset + take, :]
-            self.pool.v_blocks[block_id, :, block_offset:block_offset + take, :] = v_new[0, :, offset:offset + take, :]
-            self.seq_len += take
-            offset += take
+        # Host bookkeeping shared with the device path (the reference's block order), then one
+        # scatter per pool: the token at position p goes to slot p % block_size of block
+        # block_ids[p // block_size].
+        _, num_heads, query_len, head_dim = k_new.shape
+        if length > query_len:
+            raise ValueError(f"append of {length} tokens from {query_len} new rows")
+        start = BatchedPagedKVCache(states=[self], pool=self.pool).host_append(
+            [length], query_len, num_heads, head_dim, k_new.dtype, k_new.device)[0]
+        bs = self.pool.block_size
+        pos = torch.arange(start, start + length)
+        blocks = torch.tensor(self.block_ids, dtype=torch.long)[pos // bs]
+        for pool_blocks, new in ((self.pool.k_blocks, k_new), (self.pool.v_blocks, v_new)):
+            pool_blocks[blocks, :, pos % bs, :] = new[0, :, :length, :].transpose(0, 1).to(pool_blocks.dtype)
 
     def release(self) -> None:
         self.pool.release_blocks(list(self.block_ids))
