@@ -51,6 +51,8 @@ struct LinArgs {
   int64_t res_stride;
   void* out;          // segment 0's rows (and all segments' when there is no pool)
   int64_t out_stride;
+  void* out_copy;     // when set: the same rows written a second time (row stride out_copy_stride)
+  int64_t out_copy_stride;
   void* k_pool;       // when set: segments 1 and 2 are scattered into the K / V pools
   void* v_pool;
   int32_t pool_bf16;
@@ -63,6 +65,18 @@ struct LinArgs {
   int32_t sel_group;       // (a negative entry counts from the group's end; clamped into the group)
   unsigned long long* token_keys;  // when set: per row, the running minimum of token_key over the
                                    // row's outputs (the row's greedy token in the low 32 bits)
+  // Second layer folded into the first (small_linear_kernel with F2; fp32, one 16-row tile, 16
+  // columns per workgroup): with h = this workgroup's 16 output columns n0.. of the first layer
+  // (after bias and activation), out2[m][j] += sum_c h[m][c] * w2[j][n0 + c] for j < n2, by
+  // device-scope atomic adds; workgroup 0 also adds res2[m][j] + b2[j]. out2 must hold zeros
+  // before the launch.
+  const void* w2;     // [n2, seg_n] row-major (torch Linear weight of the second layer)
+  const void* b2;     // [n2] or null
+  const void* res2;   // [M, res2_stride] or null
+  int64_t res2_stride;
+  void* out2;         // [M, out2_stride]
+  int64_t out2_stride;
+  int32_t n2;         // second layer's output features, <= threads per workgroup
 };
 
 // Greedy selection folded into a layer's epilogue: a key whose minimum over a row's columns picks
@@ -135,7 +149,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // read every row contiguously (one line per 4-lane group) and the operands are then read from LDS,
 // with each row's 16-byte chunks XOR-swizzled by row so that the 16 rows of a read hit every bank
 // once.
-template <int K, bool LN, typename T, bool STG = false>
+template <int K, bool LN, typename T, bool STG = false, bool F2 = false>
 __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(const LinArgs a) {
   constexpr bool BF = sizeof(T) == 2;
   constexpr int kLinWaves = lin_waves<K>();
@@ -150,7 +164,9 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   constexpr bool STG_X = STG_W && 2 * 16 * RB * kLinWaves <= 128 * 1024;
   constexpr int kStageB = STG_W ? (STG_X ? 32 : 16) * RB : 16;  // LDS bytes per wavefront
 
+  static_assert(!F2 || (!BF && kLinWaves * kWave >= 256), "the folded second layer is fp32");
   __shared__ float sm_part[kLinWaves][16][17];
+  __shared__ float sm_h[F2 ? kLinRows : 1][F2 ? 17 : 1];
   __shared__ float sm_red[2][kLinWaves][kLinRows];
   __shared__ __attribute__((aligned(16))) unsigned char sm_stage[kLinWaves * kStageB];
 
@@ -222,6 +238,29 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
     if constexpr (PRE) {
       load_words(lgv, static_cast<const T*>(a.ln_w) + kb, true);
       load_words(lbv, static_cast<const T*>(a.ln_b) + kb, true);
+    }
+  }
+  // F2: thread j < n2 owns output j of the second layer; its 16 weights w2[j][n0 .. n0 + 16) and,
+  // in workgroup 0, the residual rows and bias it adds, are loaded now with everything else.
+  float w2v[F2 ? 16 : 1], r2v[F2 ? kLinRows : 1];
+  float b2v = 0.f;
+  if constexpr (F2) {
+    const int j = (int)threadIdx.x < a.n2 ? (int)threadIdx.x : a.n2 - 1;
+    const f32x4* wp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.w2) + (int64_t)j * a.seg_n + n0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f32x4 t = wp[e];
+      w2v[4 * e] = t[0]; w2v[4 * e + 1] = t[1]; w2v[4 * e + 2] = t[2]; w2v[4 * e + 3] = t[3];
+    }
+#pragma unroll
+    for (int m2 = 0; m2 < kLinRows; ++m2) r2v[m2] = 0.f;
+    if (blockIdx.x == 0) {
+      if (a.b2 != nullptr) b2v = static_cast<const float*>(a.b2)[j];
+      if (a.res2 != nullptr) {
+#pragma unroll
+        for (int m2 = 0; m2 < kLinRows; ++m2)
+          if (m2 < a.M) r2v[m2] = static_cast<const float*>(a.res2)[(int64_t)m2 * a.res2_stride + j];
+      }
     }
   }
   const int ml = (threadIdx.x >> a.cw_log2) & 15;  // epilogue thread (row ml, column cc) of the tile
@@ -331,6 +370,32 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
   __syncthreads();
 
   // ---- epilogue: one thread per (row, column) of the tile --------------------------------------
+  if constexpr (F2) {
+    // h[ml][cc] (bias and activation applied; zero past the rows and columns) into LDS, then thread
+    // j folds the 16 columns into output j of every row and adds it to out2.
+    if ((int)threadIdx.x < (kLinRows << a.cw_log2)) {
+      float v = 0.f;
+      if (live) {
+#pragma unroll
+        for (int ww = 0; ww < kLinWaves; ++ww) v += sm_part[ww][ml][cc];
+        v += bias_v;
+        if (a.act == 1) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+      }
+      sm_h[ml][cc] = v;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x >= a.n2) return;
+    float* o2 = static_cast<float*>(a.out2) + threadIdx.x;
+#pragma unroll
+    for (int m2 = 0; m2 < kLinRows; ++m2) {
+      if (m2 >= a.M) break;
+      float v = r2v[m2] + b2v;
+#pragma unroll
+      for (int cc2 = 0; cc2 < 16; ++cc2) v = fmaf(sm_h[m2][cc2], w2v[cc2], v);
+      atomicAdd(o2 + (int64_t)m2 * a.out2_stride, v);
+    }
+    return;
+  }
   const bool keyed = a.token_keys != nullptr;  // uniform
   if (!live && (!keyed || (int)threadIdx.x >= (kLinRows << a.cw_log2))) return;  // whole wavefronts past the tile
   float v = 0.f;
@@ -369,6 +434,8 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
     return;
   }
   Elem<T>::store(static_cast<T*>(a.out) + (int64_t)m * a.out_stride + seg * a.seg_n + n, v + res_v);
+  if (a.out_copy != nullptr)
+    Elem<T>::store(static_cast<T*>(a.out_copy) + (int64_t)m * a.out_copy_stride + seg * a.seg_n + n, v + res_v);
 }
 
 static bool small_linear_k_supported(int32_t K) {
@@ -436,6 +503,28 @@ static int launch_small_linear(LinArgs a, hipStream_t stream) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// LayerNorm + first layer + activation + second layer in one launch (fp32, at most 16 rows): one
+// workgroup per 16 columns of the first layer, each adding its share of the second layer to out2.
+static int launch_mlp_rows(LinArgs a, hipStream_t stream) {
+  a.cw_log2 = 4;
+  const dim3 grid((unsigned)(a.seg_n / 16), 1u);
+  const bool stg = lin_stage_in_lds();
+#define PA_MLP_CASE(KK)                                                                              \
+  case KK:                                                                                           \
+    if (stg) small_linear_kernel<KK, true, float, true, true><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a); \
+    else small_linear_kernel<KK, true, float, false, true><<<grid, lin_waves<KK>() * kWave, 0, stream>>>(a);    \
+    break;
+  switch (a.K) {
+    PA_MLP_CASE(128)
+    PA_MLP_CASE(256)
+    PA_MLP_CASE(512)
+    default: PA_FAIL(PA_ERR_UNSUPPORTED, "mlp rows: d_model must be 128, 256 or 512, got %d", a.K);
+  }
+#undef PA_MLP_CASE
+  PA_CHECK_LAUNCH("mlp rows kernel");
+  return PA_OK;
+}
+
 // Token + position embedding of a [B, T] step: row b*T + t = tok[ids[b, t]] + pos[min(p0[b] + t,
 // max_pos - 1)]; an id outside the vocabulary gives a zero token row. One workgroup per row;
 // 16-byte vectors (4 fp32 or 8 bf16 values), the sum in fp32, rounded once for bf16.
@@ -484,7 +573,8 @@ extern "C" int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int
                               const void* weight, const void* bias, int32_t out_features,
                               const void* ln_weight, const void* ln_bias, float ln_eps,
                               int32_t activation, const void* residual, int64_t residual_stride,
-                              void* out, int64_t out_stride, int dtype, void* stream) {
+                              void* out, int64_t out_stride, void* out_copy, int64_t out_copy_stride,
+                              int dtype, void* stream) {
   pa_host::clear_error();
   PA_CHECK_ARG(rows >= 0 && rows <= kLinMaxRows, "rows must be in [0, %d], got %d", kLinMaxRows, rows);
   PA_CHECK_ARG(out_features > 0 && in_features > 0, "bad sizes: in=%d out=%d", in_features, out_features);
@@ -497,13 +587,15 @@ extern "C" int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int
   PA_CHECK_ARG(aligned16(x) && aligned16(weight) && x_stride % vec == 0 && (!ln_weight || (aligned16(ln_weight) &&
                aligned16(ln_bias))), "x, weight and LayerNorm parameters must be 16-byte aligned, x_stride a multiple of %d", vec);
   PA_CHECK_ARG(x_stride >= in_features && out_stride >= out_features &&
-               (residual == nullptr || residual_stride >= out_features), "row strides smaller than the rows");
+               (residual == nullptr || residual_stride >= out_features) &&
+               (out_copy == nullptr || out_copy_stride >= out_features), "row strides smaller than the rows");
   LinArgs a{};
   a.x = x; a.x_stride = x_stride; a.M = rows; a.K = in_features;
   a.ln_w = ln_weight; a.ln_b = ln_bias; a.ln_eps = ln_eps;
   a.w[0] = weight; a.b[0] = bias; a.seg_n = out_features; a.nseg = 1;
   a.act = activation; a.res = residual; a.res_stride = residual_stride;
   a.out = out; a.out_stride = out_stride; a.bf16 = dtype == PA_DTYPE_BF16;
+  a.out_copy = out_copy; a.out_copy_stride = out_copy_stride;
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
 }
 
@@ -535,6 +627,36 @@ extern "C" int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t gr
   PA_CHECK_ARG((reinterpret_cast<uintptr_t>(token_keys) & 7) == 0, "token_keys must be 8-byte aligned");
   a.token_keys = reinterpret_cast<unsigned long long*>(token_keys);
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pa_mlp_rows(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,
+                           const void* ln_weight, const void* ln_bias, float ln_eps,
+                           const void* fc1_weight, const void* fc1_bias, int32_t d_ff, int32_t activation,
+                           const void* fc2_weight, const void* fc2_bias,
+                           const void* residual, int64_t residual_stride,
+                           void* out, int64_t out_stride, int dtype, void* stream) {
+  pa_host::clear_error();
+  PA_CHECK_ARG(dtype == PA_DTYPE_F32, "mlp rows: dtype must be fp32, got %d", dtype);
+  PA_CHECK_ARG(rows >= 0 && rows <= kLinRows, "mlp rows: rows must be in [0, %d], got %d", kLinRows, rows);
+  PA_CHECK_ARG(d_model > 0 && d_ff > 0 && d_ff % 16 == 0, "bad sizes: d_model=%d d_ff=%d (d_ff a multiple of 16)",
+               d_model, d_ff);
+  PA_CHECK_ARG(activation == 0 || activation == 1, "bad activation %d", activation);
+  if (rows == 0) return PA_OK;
+  PA_CHECK_ARG(x && ln_weight && ln_bias && fc1_weight && fc2_weight && out, "null pointer argument");
+  PA_CHECK_ARG(aligned16(x) && aligned16(fc1_weight) && aligned16(fc2_weight) && aligned16(ln_weight) &&
+               aligned16(ln_bias) && x_stride % 4 == 0,
+               "x, weights and LayerNorm parameters must be 16-byte aligned, x_stride a multiple of 4");
+  PA_CHECK_ARG(x_stride >= d_model && out_stride >= d_model && (residual == nullptr || residual_stride >= d_model),
+               "row strides smaller than the rows");
+  LinArgs a{};
+  a.x = x; a.x_stride = x_stride; a.M = rows; a.K = d_model;
+  a.ln_w = ln_weight; a.ln_b = ln_bias; a.ln_eps = ln_eps;
+  a.w[0] = fc1_weight; a.b[0] = fc1_bias; a.seg_n = d_ff; a.nseg = 1;
+  a.act = activation; a.res = nullptr; a.res_stride = 0;
+  a.out = nullptr; a.out_stride = 0; a.bf16 = 0;
+  a.w2 = fc2_weight; a.b2 = fc2_bias; a.res2 = residual; a.res2_stride = residual_stride;
+  a.out2 = out; a.out2_stride = out_stride; a.n2 = d_model;
+  return launch_mlp_rows(a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int pa_qkv_append(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,

@@ -98,7 +98,8 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _c_void_p, _i32,  # weight, bias, out_features
          _c_void_p, _c_void_p, _f32,  # LayerNorm weight, bias, eps
          _i32, _c_void_p, _i64,  # activation, residual, stride
-         _c_void_p, _i64, _int, _c_void_p],  # out, stride, dtype, stream
+         _c_void_p, _i64, _c_void_p, _i64,  # out, stride, out copy, stride
+         _int, _c_void_p],  # dtype, stream
     ),
     "pa_linear_select_rows": (
         _int,
@@ -115,6 +116,15 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _i64,  # q_out, stride
          _c_void_p, _c_void_p, _int, _i64,  # k pool, v pool, pool dtype, num_blocks
          _c_void_p, _i32, _i32, _i32, _int, _c_void_p],  # slots, heads, head_dim, block_size, dtype, stream
+    ),
+    "pa_mlp_rows": (
+        _int,
+        [_c_void_p, _i64, _i32, _i32,  # x, stride, rows, d_model
+         _c_void_p, _c_void_p, _f32,  # LayerNorm weight, bias, eps
+         _c_void_p, _c_void_p, _i32, _i32,  # fc1 weight, bias, d_ff, activation
+         _c_void_p, _c_void_p,  # fc2 weight, bias
+         _c_void_p, _i64,  # residual, stride
+         _c_void_p, _i64, _int, _c_void_p],  # out (accumulated), stride, dtype, stream
     ),
     "pa_embed_rows": (
         _int,

@@ -6,6 +6,8 @@
   qkv_append_hip   LayerNorm, q/k/v projections and the KV append of a cached attention layer in
                    one launch; returns q                                     (pa_qkv_append)
   embed_rows_hip   token + clamped position embedding of a [B, T] step       (pa_embed_rows)
+  mlp_rows_hip     LayerNorm + fc1 + GELU + fc2 (+ residual) of at most 16 fp32 rows in one
+                   launch, accumulated into a zeroed output                  (pa_mlp_rows)
 
 They stand in for the nn.LayerNorm / nn.Linear / nn.GELU calls and the append of the
 reference's cached forward (src/model/transformer.py:30-35, src/model/attention.py:46-64) on
@@ -56,9 +58,11 @@ def supported(linear: nn.Linear) -> bool:
 
 
 def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | None = None, gelu: bool = False,
-                    residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                    residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                    copy_to: torch.Tensor | None = None) -> torch.Tensor:
     """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 1024); x, the layer's
-    parameters, residual and out share one dtype (float32 or bfloat16)."""
+    parameters, residual and out share one dtype (float32 or bfloat16). copy_to: the same rows are
+    also written there (it may be residual itself)."""
     _rows(x, "x")
     dt = x.dtype
     M, K = x.shape
@@ -72,13 +76,18 @@ def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | No
     _rows(out, "out", dt)
     if residual is not None:
         _rows(residual, "residual", dt)
+    if copy_to is not None:
+        _rows(copy_to, "copy_to", dt)
+        if copy_to.shape[0] < M or copy_to.shape[1] < N:
+            raise ValueError(f"copy_to must hold {M} rows of {N} features")
     status = _lib.load().pa_linear_rows(
         x.data_ptr(), x.stride(0), M, K,
         linear.weight.data_ptr(), _ptr(linear.bias), N,
         _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
         float(ln.eps) if ln is not None else 0.0,
         1 if gelu else 0, _ptr(residual), residual.stride(0) if residual is not None else 0,
-        out.data_ptr(), out.stride(0), _lib.dtype_code(dt), _stream(x.device),
+        out.data_ptr(), out.stride(0), _ptr(copy_to), copy_to.stride(0) if copy_to is not None else 0,
+        _lib.dtype_code(dt), _stream(x.device),
     )
     _lib.check(status, "pa_linear_rows")
     return out
@@ -186,6 +195,46 @@ def embed_rows_hip(ids: torch.Tensor, pos_start: torch.Tensor, token_emb: nn.Emb
         _stream(ids.device),
     )
     _lib.check(status, "pa_embed_rows")
+    return out
+
+
+MLP_MAX_ROWS = 16
+MLP_FEATURES = (128, 256, 512)
+
+
+def mlp_supported(model) -> bool:
+    """True when the model's MLP blocks fit pa_mlp_rows: fp32, d_model 128/256/512, d_ff a
+    multiple of 16 (on top of model_supported)."""
+    return (model.lm_head.weight.dtype == torch.float32 and model_supported(model)
+            and all(blk.mlp[0].in_features in MLP_FEATURES and blk.mlp[0].out_features % 16 == 0
+                    and blk.mlp[2].out_features == blk.mlp[0].in_features for blk in model.blocks))
+
+
+def mlp_rows_hip(x: torch.Tensor, ln: nn.LayerNorm, fc1: nn.Linear, fc2: nn.Linear, out: torch.Tensor, *,
+                 residual: torch.Tensor | None = None, gelu: bool = True) -> torch.Tensor:
+    """out[m] += fc2(act(fc1(LN(x[m])))) + residual[m] for the (at most 16) rows of x, fp32, in one
+    launch: the fc1 column tiles add their shares of fc2 to `out` with atomic adds (so the sum's
+    order, and its last bits, vary from run to run). `out` holds the starting value: zeros, or
+    the residual rows themselves (then pass residual=None)."""
+    _rows(x, "x", torch.float32)
+    M, D = x.shape
+    if M > MLP_MAX_ROWS:
+        raise ValueError(f"mlp_rows_hip takes at most {MLP_MAX_ROWS} rows, got {M}")
+    if fc1.in_features != D or fc2.in_features != fc1.out_features or fc2.out_features != D:
+        raise ValueError("fc1 must map d_model -> d_ff and fc2 d_ff -> d_model")
+    _same_dtype(torch.float32, ln.weight, ln.bias, fc1.weight, fc1.bias, fc2.weight, fc2.bias)
+    _rows(out, "out", torch.float32)
+    if out.shape[0] < M or out.shape[1] != D:
+        raise ValueError(f"out must hold {M} rows of {D} features")
+    if residual is not None:
+        _rows(residual, "residual", torch.float32)
+    status = _lib.load().pa_mlp_rows(
+        x.data_ptr(), x.stride(0), M, D, ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps),
+        fc1.weight.data_ptr(), _ptr(fc1.bias), fc1.out_features, 1 if gelu else 0,
+        fc2.weight.data_ptr(), _ptr(fc2.bias), _ptr(residual), residual.stride(0) if residual is not None else 0,
+        out.data_ptr(), out.stride(0), _lib.PA_DTYPE_F32, _stream(x.device),
+    )
+    _lib.check(status, "pa_mlp_rows")
     return out
 
 

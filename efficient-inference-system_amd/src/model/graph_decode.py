@@ -31,7 +31,11 @@ Steps of at most FUSED_STEP_ROWS rows (B * bucketed T: every decode step, and pr
 to 512 rows) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
 shapes allow: per layer one launch for LayerNorm + q/k/v projections + KV append, the attention
 (decode or chunked prefill kernel), one for the output projection + residual, one for LayerNorm +
-fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. A fused launch reads its weight tile
+fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. Steps of at most 16 rows of an fp32
+model (every decode step at batch <= 16) fold the last two into one launch: the output projection
+writes x1 into the MLP's input buffer and over the residual stream, and each fc1 column tile of
+the MLP launch adds its share of fc2 to the residual stream with atomic adds (four launches per
+layer; PAGED_HIP_DECODE_FOLD=0 keeps five). A fused launch reads its weight tile
 once per 16 rows, so above a per-layer row count (FUSED_ROWS) that layer runs through torch
 instead. Set PAGED_HIP_FUSED_DECODE=0 to use the torch layers throughout.
 
@@ -94,6 +98,12 @@ def graphs_enabled() -> bool:
 
 def fused_decode_enabled() -> bool:
     return os.environ.get("PAGED_HIP_FUSED_DECODE", "1") != "0"
+
+
+def folded_decode_enabled() -> bool:
+    """Four launches per layer in steps of at most 16 rows (fc2 folded into the fc1 launch);
+    PAGED_HIP_DECODE_FOLD=0 keeps five."""
+    return os.environ.get("PAGED_HIP_DECODE_FOLD", "1") != "0"
 
 
 def bucket_for(T: int) -> int | None:
@@ -319,6 +329,10 @@ class _Captured:
         # stays valid for the graph's lifetime.
         self.ws = _workspace(device, ws_bytes) if ws_bytes else None
         self.fused = B * Tb <= FUSED_STEP_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
+        # Steps of at most 16 rows of an fp32 model (every decode step at batch <= 16): per layer
+        # four launches, the MLP in one (fc1 column tiles adding their fc2 shares with atomic adds).
+        self.folded = (self.fused and B * Tb <= hip_linear.MLP_MAX_ROWS and folded_decode_enabled()
+                       and hip_linear.mlp_supported(model))
         emb_dt = model.token_emb.weight.dtype
         self.embed_fused = (fused_decode_enabled() and emb_dt in hip_linear.DTYPES
                             and model.pos_emb.weight.dtype == emb_dt
@@ -422,6 +436,9 @@ class GraphedStep:
         lim = FUSED_ROWS[x.dtype]
         rows = B * Tb
         fc1_fused, fc2_fused = rows <= lim["fc1"], rows <= lim["fc2"]
+        # Folded MLP: x stays the residual buffer; out_proj writes x1 into x1_buf (the MLP's input)
+        # and into x itself, and the MLP launch adds fc2's output (fc1 tile by fc1 tile) to x.
+        x1_buf = torch.empty_like(x) if cap.folded else None
         for blk, pool in zip(m.blocks, pools):
             k_pool, v_pool = _pool_tensors(pool)
             a = blk.attn
@@ -431,7 +448,12 @@ class GraphedStep:
                 o = paged_attention_decode_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
             else:
                 o = paged_attention_prefill_hip(q4, k_pool, v_pool, pt, seq32, cap.cur, split_blocks=cap.split_blocks)
-            x1 = hip_linear.linear_rows_hip(o.transpose(1, 2).reshape(rows, a.d_model), a.out_proj, residual=x)
+            o2 = o.transpose(1, 2).reshape(rows, a.d_model)
+            if cap.folded:
+                hip_linear.linear_rows_hip(o2, a.out_proj, residual=x, out=x1_buf, copy_to=x)
+                hip_linear.mlp_rows_hip(x1_buf, blk.ln2, blk.mlp[0], blk.mlp[2], x)
+                continue
+            x1 = hip_linear.linear_rows_hip(o2, a.out_proj, residual=x)
             if fc1_fused:
                 h = hip_linear.linear_rows_hip(x1, blk.mlp[0], ln=blk.ln2, gelu=True)
             else:

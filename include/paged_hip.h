@@ -221,12 +221,16 @@ int pa_zero_blocks(void* k_pool, void* v_pool, int pool_dtype, int64_t num_block
  *   torch.nn.LayerNorm); bias and residual may be NULL; activation 0 = none, 1 = exact (erf)
  *   GELU (torch.nn.GELU()). x, weight and LayerNorm parameters 16-byte aligned, x_stride a
  *   multiple of 16 bytes.
+ *   out_copy (or NULL): the same rows are also written there (row stride out_copy_stride); it may be
+ *   `residual` itself (each element is read and written by one thread). A decode step uses it to
+ *   seed the buffer pa_mlp_rows accumulates into with the out_proj rows (x + attention output).
  */
 int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int32_t in_features,
                    const void* weight, const void* bias, int32_t out_features,
                    const void* ln_weight, const void* ln_bias, float ln_eps,
                    int32_t activation, const void* residual, int64_t residual_stride,
-                   void* out, int64_t out_stride, int dtype, void* stream);
+                   void* out, int64_t out_stride, void* out_copy, int64_t out_copy_stride,
+                   int dtype, void* stream);
 
 /*
  * pa_linear_select_rows: pa_linear_rows over one selected row per group of x, without a residual:
@@ -295,6 +299,24 @@ int pa_embed_rows(const int64_t* ids, const int64_t* pos_start, int32_t batch, i
  */
 int pa_argmax_rows(const void* logits, int64_t row_stride, int32_t batch, int32_t rows_per_request,
                    const int32_t* row_index, int32_t vocab, int dtype, int64_t* tokens, void* stream);
+
+/*
+ * pa_mlp_rows: out[m] += fc2(act(fc1(LayerNorm(x[m])))) + residual[m] for rows m < rows (at most
+ * 16), fp32 (dtype must be PA_DTYPE_F32), in one launch: one workgroup per 16 columns of fc1 adds
+ * its share of fc2 to `out` with device-scope atomic adds (the sum's order, and its last bits, vary
+ * from run to run), so `out` must hold its starting value when the launch runs (zeros, or the
+ * residual rows themselves: pa_linear_rows' `out_copy`).
+ * d_model is 128, 256 or 512, d_ff a multiple of 16; fc1_weight is [d_ff, d_model] and
+ * fc2_weight [d_model, d_ff] row-major (torch Linear weights), 16-byte aligned; activation 0 =
+ * none, 1 = exact GELU; biases and residual may be NULL. Replaces the MLP block and its residual
+ * add of the reference's transformer block (src/model/transformer.py:32-35) on decode steps.
+ */
+int pa_mlp_rows(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,
+                const void* ln_weight, const void* ln_bias, float ln_eps,
+                const void* fc1_weight, const void* fc1_bias, int32_t d_ff, int32_t activation,
+                const void* fc2_weight, const void* fc2_bias,
+                const void* residual, int64_t residual_stride,
+                void* out, int64_t out_stride, int dtype, void* stream);
 
 /*
  * pa_hbm_read_probe: reads `bytes` (a multiple of 16) of device memory at `src` once, with the

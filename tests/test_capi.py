@@ -33,7 +33,7 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
         "pa_argmax_rows", "pa_decode", "pa_decode_noalloc", "pa_decode_workspace_size", "pa_embed_rows",
         "pa_hbm_read_probe", "pa_kv_append", "pa_last_error_message",
-        "pa_linear_rows", "pa_linear_select_rows",
+        "pa_linear_rows", "pa_linear_select_rows", "pa_mlp_rows",
         "pa_pack_metadata", "pa_pack_metadata_mirror", "pa_prefill", "pa_prefill_workspace_size", "pa_qkv_append", "pa_version",
         "pa_zero_blocks",
     ])
@@ -91,25 +91,25 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     F32, BF16 = _lib.PA_DTYPE_F32, _lib.PA_DTYPE_BF16
     lin = lib.pa_linear_rows
     # more than 1024 rows
-    assert lin(A, 512, 1025, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 512, 1025, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None, 0, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"rows must be in [0, 1024]" in lib.pa_last_error_message()
     # unknown activation
-    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 2, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 2, None, 0, A, 512, None, 0, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # unknown element type
-    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, 7, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None, 0, 7, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"bad dtype" in lib.pa_last_error_message()
     # misaligned activations
-    assert lin(A + 4, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A + 4, 512, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None, 0, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # bf16 rows must start on 16-byte boundaries: a row stride of 516 bf16 values does not
-    assert lin(A, 516, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, BF16, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 516, 4, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None, 0, BF16, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"multiple of 8" in lib.pa_last_error_message()
     # LayerNorm weight without bias
-    assert lin(A, 512, 4, 512, A, None, 512, A, None, 1e-5, 0, None, 0, A, 512, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lin(A, 512, 4, 512, A, None, 512, A, None, 1e-5, 0, None, 0, A, 512, None, 0, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # in_features without a kernel
-    assert lin(A, 96, 4, 96, A, None, 32, None, None, 0.0, 0, None, 0, A, 32, F32, None) == _lib.PA_ERR_UNSUPPORTED
+    assert lin(A, 96, 4, 96, A, None, 32, None, None, 0.0, 0, None, 0, A, 32, None, 0, F32, None) == _lib.PA_ERR_UNSUPPORTED
     assert b"in_features" in lib.pa_last_error_message()
     # no rows: nothing to do
-    assert lin(None, 0, 0, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 0, BF16, None) == _lib.PA_OK
+    assert lin(None, 0, 0, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 0, None, 0, BF16, None) == _lib.PA_OK
     # the row-selecting form: group_rows must be positive, row_index present, at most 1024 groups
     sel = lib.pa_linear_select_rows
     assert sel(A, 512, 2, 0, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
