@@ -25,6 +25,7 @@ struct AttnArgs {
   int32_t num_splits;    // workgroups per work unit along the KV axis, >= 1
   int32_t split_blocks;  // KV blocks per split when num_splits > 1
   float* ws;             // partial (m, l, acc[head_dim]) records of the splits
+  int32_t* counters;     // decode, same-launch merge: per (request, head) arrivals (zero between calls)
 };
 
 // Wave-wide partner exchange on gfx950 without an LDS round trip: v_permlane16_swap /

@@ -148,6 +148,9 @@ __device__ __forceinline__ void stream_tiles(int cnt, int ids, int tok_base, int
   }
 }
 
+template <typename IO, bool COH>
+__device__ __forceinline__ void merge_pair(const AttnArgs& a, int bh, int nact, int lane);
+
 template <typename KV, typename IO, int HD, int NW>
 __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs a) {
   constexpr int BS = 16;
@@ -287,12 +290,36 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
       Elem<IO>::store(op + d, lsum > 0.f ? A / lsum : 0.f);
     } else {
       float* rec = a.ws + (((int64_t)b * a.H + h) * nsplit + split) * (HD + 2);
-      if (d == 0) {
-        rec[0] = M;
-        rec[1] = lsum;
+      if (a.counters != nullptr) {  // same-launch merge: device-scope stores
+        if (d == 0) {
+          __hip_atomic_store(rec, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(rec + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __hip_atomic_store(rec + 2 + d, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        if (d == 0) {
+          rec[0] = M;
+          rec[1] = lsum;
+        }
+        rec[2 + d] = A;
       }
-      rec[2 + d] = A;
     }
+  }
+  // Same-launch merge: once every wavefront's record stores have completed (at device scope),
+  // one thread counts this split in; the split that arrives last resets the counter and merges
+  // all records with device-scope loads.
+  if (nact > 1 && a.counters != nullptr) {
+    __shared__ int sm_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int32_t* cnt = a.counters + (int64_t)b * a.H + h;
+      const int last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nact - 1;
+      if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sm_last = last;
+    }
+    __syncthreads();
+    if (sm_last && threadIdx.x < kWave) merge_pair<IO, true>(a, b * a.H + h, nact, threadIdx.x);
   }
 }
 
@@ -302,30 +329,32 @@ __global__ __launch_bounds__(NW * kWave) void decode_fast_kernel(const AttnArgs 
 // the denominator, and each lane's head_dim element is summed over the splits with the weights
 // broadcast from the lane that computed them, eight independent loads at a time (a loop over the
 // splits with one dependent load chain per split is several times slower).
-template <typename IO>
-__global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
-  const int bh = blockIdx.x;
+// A record word: a plain load, or (COH) a device-scope load that sees the other splits' stores
+// of this launch.
+template <bool COH>
+__device__ __forceinline__ float rec_load(const float* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+
+template <typename IO, bool COH>
+__device__ __forceinline__ void merge_pair(const AttnArgs& a, int bh, int nact, int lane) {
   const int b = bh / a.H, h = bh % a.H;
   const int HD = a.head_dim;
-  const int lane = threadIdx.x;
-  int nb = (valid_keys(a.seq_lens[b], a.cur_lens[b], 0) + 15) / 16;
-  nb = nb < a.max_pages ? nb : a.max_pages;
-  const int nact = nb > 0 ? (nb + a.split_blocks - 1) / a.split_blocks : 1;
-  if (nact == 1) return;  // the split wrote the output itself
   const int64_t R = HD + 2;
   const float* base = a.ws + (int64_t)bh * a.num_splits * R;
   // Lane s holds split s's (m, l) for the first 64 splits; more splits are read in further passes.
   float m0 = kNegBig, l0 = 0.f;
   if (lane < nact) {
-    m0 = base[lane * R];
-    l0 = base[lane * R + 1];
+    m0 = rec_load<COH>(base + lane * R);
+    l0 = rec_load<COH>(base + lane * R + 1);
   }
   float M = m0;
-  for (int s = lane + kWave; s < nact; s += kWave) M = fmaxf(M, base[s * R]);
+  for (int s = lane + kWave; s < nact; s += kWave) M = fmaxf(M, rec_load<COH>(base + s * R));
   M = wave_max(M);
   const float f0 = lane < nact ? fast_exp2(m0 - M) : 0.f;  // weight of split `lane`, 0 past the splits
   float lsum = l0 * f0;
-  for (int s = lane + kWave; s < nact; s += kWave) lsum = fmaf(base[s * R + 1], fast_exp2(base[s * R] - M), lsum);
+  for (int s = lane + kWave; s < nact; s += kWave) lsum = fmaf(rec_load<COH>(base + s * R + 1), fast_exp2(rec_load<COH>(base + s * R) - M), lsum);
   lsum = wave_sum(lsum);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
@@ -334,14 +363,14 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
     float A = 0.f;
     for (int s0 = 0; s0 < nact; s0 += kWave) {
       const int n = nact - s0 < kWave ? nact - s0 : kWave;
-      const float f = s0 == 0 ? f0 : (lane < n ? fast_exp2(base[(s0 + lane) * R] - M) : 0.f);
+      const float f = s0 == 0 ? f0 : (lane < n ? fast_exp2(rec_load<COH>(base + (s0 + lane) * R) - M) : 0.f);
       const float* rec = base + s0 * R + 2 + dd;
       // 8 loads in flight: indices past the last split are clamped to it (a valid record) and
       // get weight 0 (lane j0 + jj <= 63 since j0 <= n - 1 rounded down to a multiple of 8).
       for (int j0 = 0; j0 < n; j0 += 8) {
         float x[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) x[jj] = rec[(j0 + jj < n ? j0 + jj : n - 1) * R];
+        for (int jj = 0; jj < 8; ++jj) x[jj] = rec_load<COH>(rec + (j0 + jj < n ? j0 + jj : n - 1) * R);
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
           A = fmaf(x[jj], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), j0 + jj)), A);
@@ -349,6 +378,17 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
     }
     if (d < HD) Elem<IO>::store(op + d, A * inv);
   }
+}
+
+template <typename IO>
+__global__ __launch_bounds__(kWave) void decode_merge_kernel(const AttnArgs a) {
+  const int bh = blockIdx.x;
+  const int b = bh / a.H;
+  int nb = (valid_keys(a.seq_lens[b], a.cur_lens[b], 0) + 15) / 16;
+  nb = nb < a.max_pages ? nb : a.max_pages;
+  const int nact = nb > 0 ? (nb + a.split_blocks - 1) / a.split_blocks : 1;
+  if (nact == 1) return;  // the split wrote the output itself
+  merge_pair<IO, false>(a, bh, nact, threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -474,11 +514,21 @@ static int num_splits_for(int32_t max_pages, int32_t split_blocks) {
 
 using namespace pa;
 
+// Split workspace layout: arrival counters (one int32 per (request, head), at most
+// kDecodeCounterBytes / 4 pairs) at the start, zero between calls, then the split records. The
+// counters region has one fixed size whatever the call's shape, so calls of any shapes can share
+// a workspace and always find their counters at zero.
+constexpr size_t kDecodeCounterBytes = PA_DECODE_COUNTER_BYTES;
+// Splits per (request, head) up to which the last split to finish merges the records in the same
+// launch; more splits are merged by a second launch (its merge reads them faster than one
+// workgroup's device-scope loads).
+constexpr int kSameLaunchMaxSplits = 8;
+
 extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                            int32_t max_pages, int32_t split_blocks) {
   const int s = num_splits_for(max_pages, split_blocks);
   if (s <= 1 || batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  return (size_t)batch * num_heads * s * (head_dim + 2) * sizeof(float);
+  return kDecodeCounterBytes + (size_t)batch * num_heads * s * (head_dim + 2) * sizeof(float);
 }
 
 // Shared body of pa_decode and pa_decode_noalloc. `ws_limit_is_scratch` only changes the error
@@ -532,7 +582,9 @@ static int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h,
       PA_FAIL(PA_ERR_WORKSPACE, "decode workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
     a.num_splits = nsplit;
     a.split_blocks = split_blocks;
-    a.ws = static_cast<float*>(workspace);
+    a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kDecodeCounterBytes);
+    if (nsplit <= kSameLaunchMaxSplits && (size_t)batch * num_heads * sizeof(int32_t) <= kDecodeCounterBytes)
+      a.counters = static_cast<int32_t*>(workspace);
   }
   if (((int64_t)batch + kXcds) * num_heads * nsplit > 0x7fffffffLL)
     PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
@@ -541,7 +593,7 @@ static int decode_entry(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                            : dispatch_decode_fast_io<uint16_t>(a, kv_dtype, stream);
   if (!ok) PA_FAIL(PA_ERR_UNSUPPORTED, "no decode kernel for head_dim %d", head_dim);
   PA_CHECK_LAUNCH("decode kernel");
-  if (nsplit > 1) {
+  if (nsplit > 1 && a.counters == nullptr) {
     const dim3 grid((unsigned)((int64_t)batch * num_heads)), block(kWave);
     if (io_dtype == PA_DTYPE_F32)
       decode_merge_kernel<float><<<grid, block, 0, stream>>>(a);

@@ -20,7 +20,7 @@ import torch
 
 from src.kernels import _lib
 
-_workspaces: dict[int, torch.Tensor] = {}
+_workspaces: dict[tuple[int, str], torch.Tensor] = {}
 _cu_counts: dict[int, int] = {}
 
 
@@ -46,28 +46,34 @@ def cu_count(device: torch.device) -> int:
     return _cu_counts[idx]
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The device's split-K partial-result workspace, at least `nbytes` long."""
+def _workspace(device: torch.device, nbytes: int, kind: str) -> torch.Tensor:
+    """The device's split-K workspace for `kind` ("decode" or "prefill"), at least `nbytes` long.
+    Decode workspaces start with the arrival counters of the in-launch merge, which must be zero
+    before first use and stay zero between calls: they are zero-filled when allocated and never
+    shared with prefill calls, whose records would overwrite them."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _workspaces.get(idx)
+    ws = _workspaces.get((idx, kind))
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[idx] = ws
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[(idx, kind)] = ws
     return ws
 
 
 def default_split_blocks(batch: int, num_heads: int, max_pages: int, device: torch.device) -> int:
     """KV blocks per decode split: 0 (no split) when (request, head) pairs alone fill the GPU or
-    the context is at most 1024 tokens (64 blocks: the merge launch costs about what it saves;
-    8 requests x 8 heads fp32 up to 1024 tokens, six layers: 52.7 us unsplit, 55.1 us in 16-block
-    splits, HIP-graph replay), otherwise enough splits for about two workgroups per compute unit,
-    16 to 32 blocks each when there are at most 128 pairs, at least 16 blocks above that.
-    Measured (graph replay, MI355X): 1-4 requests x 32 heads x 128 bf16 at 8k tokens
-    26 / 36 / 64 us with 32-block splits against 74 / 75 / 83 us unsplit."""
+    the context is at most 256 tokens; 16 blocks when contexts are at most 1024 tokens and the
+    pairs fill at most one workgroup per compute unit (at most 4 splits, merged inside the launch:
+    8 requests x 8 heads fp32 at 128-1024 tokens, graph replay, 10.4-11.7 us per layer unsplit,
+    7.8-8.1 us split); otherwise enough splits for about two workgroups per compute unit, 16 to
+    32 blocks each when there are at most 128 pairs, at least 16 blocks above that. Measured
+    (graph replay, MI355X): 1-4 requests x 32 heads x 128 bf16 at 8k tokens 26 / 36 / 64 us with
+    32-block splits against 74 / 75 / 83 us unsplit."""
     units = batch * num_heads
     target = 2 * cu_count(device)
-    if units == 0 or units >= target or max_pages <= 64:
+    if units == 0 or units >= target or max_pages <= 16:
         return 0
+    if max_pages <= 64:
+        return 16 if units <= cu_count(device) else 0
     splits = math.ceil(target / units)
     blocks = max(16, math.ceil(max_pages / splits))
     if units <= 128:
@@ -140,7 +146,7 @@ def paged_attention_decode_hip(
         split_blocks = default_split_blocks(B, H, max_pages, q.device)
     lib = _lib.load()
     ws_bytes = lib.pa_decode_workspace_size(B, H, Hd, max_pages, split_blocks)
-    ws_ptr = _workspace(q.device, ws_bytes).data_ptr() if ws_bytes else None
+    ws_ptr = _workspace(q.device, ws_bytes, "decode").data_ptr() if ws_bytes else None
     status = lib.pa_decode(
         q.data_ptr(), q.stride(0), q.stride(1),
         out.data_ptr(), out.stride(0), out.stride(1), _lib.dtype_code(q.dtype),
@@ -188,7 +194,7 @@ def paged_attention_prefill_hip(
         split_blocks = default_prefill_split_blocks(B, H, T, max_pages, q.device)
     lib = _lib.load()
     ws_bytes = lib.pa_prefill_workspace_size(B, H, T, Hd, max_pages, split_blocks) if bs == 16 else 0
-    ws_ptr = _workspace(q.device, ws_bytes).data_ptr() if ws_bytes else None
+    ws_ptr = _workspace(q.device, ws_bytes, "prefill").data_ptr() if ws_bytes else None
     status = lib.pa_prefill(
         q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _lib.dtype_code(q.dtype),

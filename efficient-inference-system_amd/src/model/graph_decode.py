@@ -327,7 +327,7 @@ class _Captured:
             ws_bytes = lib.pa_prefill_workspace_size(B, H, Tb, Hd, pages, self.split_blocks)
         # Allocated outside the capture and referenced here, so the address the graph records
         # stays valid for the graph's lifetime.
-        self.ws = _workspace(device, ws_bytes) if ws_bytes else None
+        self.ws = _workspace(device, ws_bytes, "decode" if Tb == 1 else "prefill") if ws_bytes else None
         self.fused = B * Tb <= FUSED_STEP_ROWS and fused_decode_enabled() and hip_linear.model_supported(model)
         # Steps of at most 16 rows of an fp32 model (every decode step at batch <= 16): per layer
         # four launches, the MLP in one (fc1 column tiles adding their fc2 shares with atomic adds).

@@ -66,9 +66,13 @@ const char* pa_last_error_message(void);
  * One workgroup of wavefronts per (request, head, split); the wavefronts split the request's KV
  * blocks between them and merge their online-softmax states in LDS. When split_blocks > 0 and a
  * request has more than split_blocks KV blocks, its blocks are also divided among several
- * workgroups whose partial results are merged by a second kernel; that path needs a workspace of
- * pa_decode_workspace_size() bytes (no initialisation needed). split_blocks <= 0 means one
- * workgroup per (request, head) and no workspace.
+ * workgroups whose partial results are merged: with at most 8 splits per request (and at most
+ * PA_DECODE_COUNTER_BYTES / 4 (request, head) pairs) by the split that finishes last, in the same
+ * launch, otherwise by a second kernel. That path needs a workspace of pa_decode_workspace_size()
+ * bytes whose first PA_DECODE_COUNTER_BYTES hold per-(request, head) arrival counters: they must
+ * be zero before the workspace is first used, and every call leaves them zero, so one zeroing at
+ * allocation serves all later calls of any shape; other calls (pa_prefill) must not write into
+ * that region. split_blocks <= 0 means one workgroup per (request, head) and no workspace.
  *
  * order: optional int32 [B] permutation giving the processing order of requests (e.g. longest
  * first, for load balance); NULL means 0..B-1. Results do not depend on it.
@@ -83,12 +87,17 @@ int pa_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
               void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of workspace pa_decode needs for these sizes (0 when split_blocks <= 0 or no request can
- * need more than one split). No reference counterpart: the Triton decode path has no split-K.
+ * need more than one split; otherwise PA_DECODE_COUNTER_BYTES + 4 * batch * num_heads * splits *
+ * (head_dim + 2)). No reference counterpart: the Triton decode path has no split-K.
  * Calls that share a workspace must not run concurrently (e.g. on different streams). */
 size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                 int32_t max_pages, int32_t split_blocks);
 
-/* Size of the fixed per-device scratch array that pa_decode_noalloc keeps its split records in. */
+/* Bytes at the start of a decode split workspace that hold the arrival counters (see pa_decode). */
+#define PA_DECODE_COUNTER_BYTES ((size_t)256 << 10)
+
+/* Size of the fixed per-device scratch array that pa_decode_noalloc keeps its arrival counters
+ * and split records in (the same layout as a pa_decode workspace). */
 #define PA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
 
 /*
@@ -97,9 +106,10 @@ size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_d
  * splits a request) go to a fixed device array of PA_DECODE_NOALLOC_SCRATCH_BYTES inside the
  * library, one per device, resolved on the first call on that device. No counterpart in the
  * reference: this is for callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc). A call whose records
- * (pa_decode_workspace_size) exceed the array fails with PA_ERR_INVALID_ARGUMENT before any
- * launch. The records need no initialisation, but every call on a device shares that device's
+ * capture, tight serving loops, harnesses that forbid hipMalloc). A call whose workspace size
+ * (pa_decode_workspace_size: the counters and the records) exceeds the array fails with
+ * PA_ERR_INVALID_ARGUMENT before any launch. The array starts at zero when the library is loaded
+ * and every call leaves its counters zero, but every call on a device shares that device's
  * array: calls that overlap on one device (e.g. on two streams) race and must be serialised.
  */
 int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -42,6 +42,7 @@ def test_header_declares_the_expected_entry_points():
 def test_noalloc_scratch_size_is_stated_in_the_header():
     text = HEADER.read_text()
     assert re.search(r"#define PA_DECODE_NOALLOC_SCRATCH_BYTES \(\(size_t\)16 << 20\)", text)
+    assert re.search(r"#define PA_DECODE_COUNTER_BYTES \(\(size_t\)256 << 10\)", text)
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -57,7 +58,8 @@ def test_host_only_entry_points(lib):
     assert lib.pa_version() == 100
     # no split -> no workspace; a split of 16 blocks over 64 pages -> 4 partial records per (b, h)
     assert lib.pa_decode_workspace_size(8, 8, 64, 64, 0) == 0
-    assert lib.pa_decode_workspace_size(8, 8, 64, 64, 16) == 8 * 8 * 4 * (64 + 2) * 4
+    # (arrival counters first: a fixed 256 KiB region; then the records)
+    assert lib.pa_decode_workspace_size(8, 8, 64, 64, 16) == (256 << 10) + 8 * 8 * 4 * (64 + 2) * 4
     assert lib.pa_decode_workspace_size(8, 8, 64, 16, 16) == 0
     # prefill: 4 requests x 8 heads x 16 tiles of 16 rows, 58 pages in splits of 16 -> 4 splits
     assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 58, 0) == 0

@@ -83,7 +83,7 @@ def test_bf16_kv_against_unrounded_fp32(device):
     assert max_err(got, want) <= 2e-2
 
 
-@pytest.mark.parametrize("split_blocks", [1, 3, 16])
+@pytest.mark.parametrize("split_blocks", [1, 3, 16, 32, 129])
 def test_split_path_matches_oracle_and_unsplit(device, split_blocks):
     lens = [5, 64, 200, 1000, 2049]
     b = make_batch(device, 5, lens, [1] * 5, H=3, Hd=64)
@@ -237,3 +237,48 @@ def test_large_ragged_decode_bf16_against_unrounded_fp32(device):
     assert float(e16.max()) <= 1e-4
     del b, kb, vb
     torch.cuda.empty_cache()
+
+
+def test_in_launch_split_merge_shares_one_workspace_across_shapes_and_graph_replays(device):
+    """Splits of at most 8 per (request, head) are merged in the launch by the split that arrives
+    last, counted in the workspace's leading arrival counters. Calls of different shapes (and
+    merge modes: more than 8 splits take the merge launch) share the decode workspace; each must
+    match the oracle and leave every counter at zero, also when replayed from a graph with eager
+    calls of other shapes in between."""
+    from src.kernels.hip_paged_attention import _workspaces
+
+    cases = [
+        (make_batch(device, 31, [130, 1000, 17, 600, 257, 990, 1, 700], [1] * 8, H=8, Hd=64), 16),  # <= 4 splits
+        (make_batch(device, 32, [3000, 40, 2049], [1] * 3, H=4, Hd=128, kv_dtype=torch.bfloat16), 32),  # <= 6
+        (make_batch(device, 33, [1500, 900], [1] * 2, H=3, Hd=64), 8),  # 12 splits: merge launch
+    ]
+    wants = [oracle_out(b) for b, _ in cases]
+
+    def counters_zero():
+        ws = _workspaces.get((device.index if device.index is not None else 0, "decode"))
+        return ws is None or int(ws[:256 << 10].view(torch.int32).abs().sum()) == 0
+
+    for rep in range(2):
+        for (b, split), want in zip(cases, wants):
+            print(f"in-launch merge rep {rep}: lens {b.seq_lens} split {split}", flush=True)
+            assert max_err(run(b, split_blocks=split), want) <= 1e-4
+            torch.cuda.synchronize()
+            assert counters_zero()
+    b, split = cases[0]
+    out = torch.empty_like(b.q)
+    call = lambda: run(b, split_blocks=split, out=out)
+    call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert max_err(out, wants[0]) <= 1e-4, rep
+        assert counters_zero()
+        b2, split2 = cases[1 + rep % 2]
+        assert max_err(run(b2, split_blocks=split2), wants[1 + rep % 2]) <= 1e-4
+        torch.cuda.synchronize()
+        assert counters_zero()

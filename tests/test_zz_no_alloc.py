@@ -1,6 +1,6 @@
-"""pa_decode_noalloc (split-K records in the library's fixed per-device scratch array) against
-pa_decode with a caller workspace, called through the C ABI: same kernels, so the outputs must be
-bit-identical. Two calls in a row, the second with a smaller batch, so the second reads records
+"""pa_decode_noalloc (arrival counters and split-K records in the library's fixed per-device
+scratch array) against pa_decode with a caller workspace, called through the C ABI: same kernels,
+so the outputs must be bit-identical. Two calls in a row, the second with a smaller batch, so the second reads records
 the first left behind in the shared array only if it were wrong. Also checked against the
 oracle (fp32 within 1e-4, bf16 KV within 1e-4 of the oracle on the same bf16 values)."""
 import math
@@ -55,7 +55,7 @@ def call(lb, b, split_blocks, noalloc):
         st = lb.pa_decode_noalloc(*common, stream)
     else:
         need = lb.pa_decode_workspace_size(B, H, Hd, max_pages, split_blocks)
-        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=b.q.device)
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=b.q.device)  # arrival counters start at zero
         st = lb.pa_decode(*common, ws.data_ptr(), need, stream)
         torch.cuda.synchronize()
         del ws
