@@ -123,6 +123,12 @@ template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Wait until this wavefront's LDS reads have returned. The compiler waits for an LDS read only
+// where its value is used, which may be after a later LDS-direct load was issued; a ring stage is
+// refilled only after this wait, so the refill cannot overwrite bytes a pending read still takes.
+__device__ __forceinline__ void lds_read_wait() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
 
 // Number of keys query row i may attend (src/kernels/reference_paged_attention.py:33-42):
 // t <= (L - C) + i and t < L.

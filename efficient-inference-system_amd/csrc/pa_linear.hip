@@ -26,6 +26,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "pa_attention.h"
 
 namespace pa {
@@ -141,6 +143,29 @@ __device__ __forceinline__ void load_words(uint32_t (&dst)[NWD], const void* p, 
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Output element (m, n) of segment seg, bias and activation applied: the K/V segments of a
+// q/k/v launch go to the row's pool slot (skipped for slot < 0 or outside the pool); otherwise
+// v + residual is stored (and, with out_copy, stored a second time).
+template <typename T>
+__device__ __forceinline__ void lin_store(const LinArgs& a, int seg, int m, int n, float v, float res_v) {
+  if (a.k_pool != nullptr && seg > 0) {
+    const int slot = a.slots[m];
+    const int64_t blk = slot >= 0 ? slot / a.bs : -1;
+    if (blk < 0 || blk >= a.num_blocks) return;
+    const int h = n / a.Hd, dd = n - h * a.Hd;
+    const int64_t off = ((blk * a.H + h) * a.bs + (slot - blk * a.bs)) * a.Hd + dd;
+    void* pool = seg == 1 ? a.k_pool : a.v_pool;
+    if (a.pool_bf16)
+      static_cast<uint16_t*>(pool)[off] = f32_to_bf16(v);
+    else
+      static_cast<float*>(pool)[off] = v;
+    return;
+  }
+  Elem<T>::store(static_cast<T*>(a.out) + (int64_t)m * a.out_stride + seg * a.seg_n + n, v + res_v);
+  if (a.out_copy != nullptr)
+    Elem<T>::store(static_cast<T*>(a.out_copy) + (int64_t)m * a.out_copy_stride + seg * a.seg_n + n, v + res_v);
+}
 
 // STG: the weight rows of the tile and, where LDS allows (at most 128 KB for both), the
 // activation rows go through LDS. Loaded straight into the operand registers, lane (G, c) reads
@@ -420,22 +445,322 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
     if (cc == 0 && m < a.M) __hip_atomic_fetch_min(a.token_keys + m, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!live) return;
   }
-  if (a.k_pool != nullptr && seg > 0) {
-    const int slot = a.slots[m];
-    const int64_t blk = slot >= 0 ? slot / a.bs : -1;
-    if (blk < 0 || blk >= a.num_blocks) return;
-    const int h = n / a.Hd, dd = n - h * a.Hd;
-    const int64_t off = ((blk * a.H + h) * a.bs + (slot - blk * a.bs)) * a.Hd + dd;
-    void* pool = seg == 1 ? a.k_pool : a.v_pool;
-    if (a.pool_bf16)
-      static_cast<uint16_t*>(pool)[off] = f32_to_bf16(v);
-    else
-      static_cast<float*>(pool)[off] = v;
-    return;
+  lin_store<T>(a, seg, m, n, v, res_v);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Tiled kernel for steps of more than 16 rows. One workgroup of 4 wavefronts owns a 32-row x
+// (16 * NT)-column output tile, so each weight column slice is read once per 32 rows (the
+// 16-row kernel reads it once per 16 and, beyond a few hundred rows, runs in several rounds of
+// workgroups). The wavefronts split K; each copies its K range, in chunks of one 128-byte row
+// slice (32 fp32 or 64 bf16 values), into a private LDS ring with LDS-direct loads (one
+// instruction copies 8 row slices, 16 bytes per lane): the whole range at once when that leaves
+// room for two workgroups per compute unit, else through a two-stage ring, so no wavefront waits
+// for another inside the loop. Row slices are stored with their
+// 16-byte chunks XOR-swizzled by row, so the 16 rows of an operand read hit every bank group
+// once. Operands and MFMAs follow the 16-row kernel (the same contiguous k-slot map; 16x16x4
+// fp32 or 16x16x16 bf16, fp32 accumulation), two row tiles by NT column tiles per wavefront.
+// LayerNorm: with the whole K range staged the row statistics come from the staged rows, each
+// wavefront summing its K range of all 32 rows, combined in LDS; otherwise from a pass over the
+// rows in memory that overlaps the ring's first loads. Either way the mean first, then the biased
+// variance from the squared deviations (two passes, as torch does); every A value is then
+// normalised (and, for bf16, rounded to bf16) as it is read. The wavefronts' partial tiles are summed in
+// LDS and the epilogue (bias, GELU, residual, K/V scatter) runs one thread per output element.
+// ---------------------------------------------------------------------------------------------
+constexpr int kTileRows = 32;
+constexpr int kTileWaves = 4;
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
   }
-  Elem<T>::store(static_cast<T*>(a.out) + (int64_t)m * a.out_stride + seg * a.seg_n + n, v + res_v);
-  if (a.out_copy != nullptr)
-    Elem<T>::store(static_cast<T*>(a.out_copy) + (int64_t)m * a.out_copy_stride + seg * a.seg_n + n, v + res_v);
+}
+
+template <typename T, int K, int NT>
+struct TileShape {
+  static constexpr int BK = 128 / (int)sizeof(T);           // K per chunk
+  static constexpr int NCH = K / kTileWaves / BK;           // chunks per wavefront
+  static constexpr int STAGE = (kTileRows + 16 * NT) * 128; // bytes per chunk (A and B slices)
+  // The whole K range staged when that leaves room for two workgroups per compute unit, else a
+  // two-stage ring (the loads of the next chunk in flight while one is folded).
+  static constexpr bool FULL = NCH * STAGE * kTileWaves <= 80 * 1024;
+  static constexpr int STAGES = FULL ? NCH : 2;
+};
+
+template <typename T, int K, bool LN, int NT>
+__global__ __launch_bounds__(kTileWaves * kWave) void tile_linear_kernel(const LinArgs a) {
+  using Sh = TileShape<T, K, NT>;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int EPW = LinT<T>::EPW;                 // values per 32-bit word
+  constexpr int BK = Sh::BK;
+  constexpr int KL = BK / 4;                        // contiguous k per lane per chunk
+  constexpr int NWD = KL / EPW;                     // 8 words
+  constexpr int KW = K / kTileWaves;                // K range of one wavefront
+  constexpr int NCH = Sh::NCH;
+  constexpr int STAGES = Sh::STAGES;
+  constexpr int BN = 16 * NT;
+  constexpr int A_BYTES = kTileRows * 128;
+  constexpr int STAGE = Sh::STAGE;
+  constexpr int RING = STAGES * STAGE;
+  constexpr int EPT = kTileRows * BN / (kTileWaves * kWave);  // epilogue elements per thread
+  constexpr int LOADS = (kTileRows + BN) / 8;                 // LDS-direct loads per chunk
+  static_assert(KW % BK == 0 && NCH >= 1, "K must be a multiple of 4 row slices");
+  static_assert(!LN || K <= 1024, "LayerNorm tiles take K <= 1024");
+  static_assert(kTileWaves * RING >= kTileWaves * kTileRows * (BN + 1) * 4, "reduction buffer");
+
+  __shared__ __attribute__((aligned(16))) unsigned char sm[kTileWaves * RING];
+  __shared__ float sm_part[kTileWaves][kTileRows];
+  __shared__ float sm_stat[kTileRows][2];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int G = lane >> 4;
+  const int c = lane & 15;
+
+  int segn = a.seg_n;
+  const void *w0 = a.w[0], *w1 = a.w[1], *w2 = a.w[2];
+  asm volatile("" : "+s"(segn), "+s"(w0), "+s"(w1), "+s"(w2)
+               : "s"(a.x), "s"(a.x_stride), "s"(a.M), "s"(a.ln_w), "s"(a.ln_b), "s"(a.res), "s"(a.res_stride),
+                 "s"(a.b[0]), "s"(a.b[1]), "s"(a.b[2]));
+  const int tiles_per_seg = segn / BN;
+  const int seg = blockIdx.x / tiles_per_seg;
+  const int n0 = (blockIdx.x - seg * tiles_per_seg) * BN;
+  const T* W = static_cast<const T*>(seg == 0 ? w0 : (seg == 1 ? w1 : w2));
+  const T* X = static_cast<const T*>(a.x);
+  const int r0 = blockIdx.y * kTileRows;
+  const int kw0 = w * KW;
+  auto sw = [](int r) { return (r >> 1) & 7; };  // chunk swizzle of row slice r
+
+  unsigned char* ring = sm + w * RING;
+  auto issue = [&](int ch) {
+    unsigned char* st = ring + (ch % STAGES) * STAGE;
+    const uint32_t kb = (uint32_t)(kw0 + ch * BK) * (uint32_t)sizeof(T);
+    const int r = lane >> 3, pc = lane & 7;
+#pragma unroll
+    for (int j = 0; j < kTileRows / 8; ++j) {
+      const int rr = 8 * j + r;
+      const int xr = r0 + rr < a.M ? r0 + rr : a.M - 1;
+      stage_load16(X, (uint32_t)(xr * a.x_stride * (int64_t)sizeof(T)) + kb + 16 * (pc ^ sw(rr)), st + 1024 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < BN / 8; ++j) {
+      const int rr = 8 * j + r;
+      stage_load16(W, (uint32_t)((n0 + rr) * K * (int)sizeof(T)) + kb + 16 * (pc ^ sw(rr)), st + A_BYTES + 1024 * j);
+    }
+  };
+  // The ring's first chunks go out first; everything else overlaps them.
+#pragma unroll
+  for (int ch = 0; ch < STAGES; ++ch) issue(ch);
+
+  // ---- loads that do not depend on the loop: LayerNorm parameters of this lane's k values,
+  // and the epilogue's bias and residual values -------------------------------------------------
+  uint32_t gw[LN ? NCH * NWD : 1], bw[LN ? NCH * NWD : 1];
+  if constexpr (LN) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      const int kk = kw0 + ch * BK + G * KL;
+      load_words(*reinterpret_cast<uint32_t(*)[NWD]>(gw + ch * NWD), static_cast<const T*>(a.ln_w) + kk, true);
+      load_words(*reinterpret_cast<uint32_t(*)[NWD]>(bw + ch * NWD), static_cast<const T*>(a.ln_b) + kk, true);
+    }
+  }
+  float bias_e[EPT], res_e[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + i * kTileWaves * kWave;
+    const int m = r0 + e / BN, n = n0 + e % BN;
+    bias_e[i] = a.b[seg] != nullptr ? Elem<T>::load(static_cast<const T*>(a.b[seg]) + n) : 0.f;
+    res_e[i] = (a.res != nullptr && m < a.M)
+                   ? Elem<T>::load(static_cast<const T*>(a.res) + (int64_t)m * a.res_stride + seg * segn + n) : 0.f;
+  }
+
+  // ---- LayerNorm statistics. Whole K staged: from the staged rows, lane l summing row l / 2,
+  // half h = l % 2 of every chunk's 128-byte slice (4 of its 8 16-byte pieces), over this
+  // wavefront's K range. Otherwise: a pass over the rows in memory (wavefront w takes rows
+  // 8w .. 8w + 7, all 64 lanes along each row), while the ring's first chunks are in flight. ----
+  float mu[2] = {0.f, 0.f}, rs[2] = {0.f, 0.f};
+  if constexpr (LN && !Sh::FULL) {
+    constexpr int EL = K / kWave;  // values per lane of one row
+    constexpr int LW = EL / EPW;   // words per lane of one row
+    static_assert(LW == 2 || LW % 4 == 0, "row slice per lane");
+    uint32_t xr[8][LW];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = r0 + 8 * w + i;
+      const int rr = r < a.M ? r : a.M - 1;
+      load_words(xr[i], X + (int64_t)rr * a.x_stride + lane * EL, true);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < EL; ++e) sum += LinT<T>::get(xr[i], e);
+      const float mean = wave_sum(sum) / K;
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < EL; ++e) {
+        const float d = LinT<T>::get(xr[i], e) - mean;
+        q = fmaf(d, d, q);
+      }
+      const float var = wave_sum(q) / K;
+      if (lane == 0) {
+        sm_stat[8 * w + i][0] = mean;
+        sm_stat[8 * w + i][1] = 1.f / sqrtf(var + a.ln_eps);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      mu[rt] = sm_stat[16 * rt + c][0];
+      rs[rt] = sm_stat[16 * rt + c][1];
+    }
+  }
+  if constexpr (LN && Sh::FULL) {
+    vm_wait<0>();
+    const int sr = lane >> 1, sh = lane & 1;
+    auto row_pass = [&](float center, bool square) {
+      float acc_s = 0.f;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) {
+        const unsigned char* st = ring + ch * STAGE + sr * 128;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 q = *reinterpret_cast<const u32x4*>(st + 16 * ((4 * sh + t) ^ sw(sr)));
+          const uint32_t qw[4] = {q[0], q[1], q[2], q[3]};
+#pragma unroll
+          for (int e = 0; e < 4 * EPW; ++e) {
+            const float d = LinT<T>::get(qw, e) - center;
+            acc_s = square ? fmaf(d, d, acc_s) : acc_s + d;
+          }
+        }
+      }
+      return acc_s + __shfl_xor(acc_s, 1);
+    };
+    float part = row_pass(0.f, false);
+    if (sh == 0) sm_part[w][sr] = part;
+    __syncthreads();
+    float mean = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kTileWaves; ++ww) mean += sm_part[ww][sr];
+    mean /= K;
+    __syncthreads();
+    part = row_pass(mean, true);
+    if (sh == 0) sm_part[w][sr] = part;
+    __syncthreads();
+    if (w == 0 && sh == 0) {
+      float var = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kTileWaves; ++ww) var += sm_part[ww][sr];
+      sm_stat[sr][0] = mean;
+      sm_stat[sr][1] = 1.f / sqrtf(var / K + a.ln_eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      mu[rt] = sm_stat[16 * rt + c][0];
+      rs[rt] = sm_stat[16 * rt + c][1];
+    }
+  }
+  bool row_ok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) row_ok[rt] = r0 + 16 * rt + c < a.M;
+
+  f32x4 acc[2][NT];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  static_for<0, NCH>([&](auto chc) {
+    constexpr int ch = decltype(chc)::value;
+    // chunk ch has landed once at most the loads of the chunks issued after it are outstanding
+    constexpr int last_issued = (ch + STAGES - 1) < (NCH - 1) ? (ch + STAGES - 1) : (NCH - 1);
+    if constexpr (!(LN && Sh::FULL)) vm_wait<(last_issued - ch) * LOADS>();
+    const unsigned char* st = ring + (ch % STAGES) * STAGE;
+    uint32_t av[2][NWD], bv[NT][NWD];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int rr = 16 * rt + c;
+#pragma unroll
+      for (int t = 0; t < NWD / 4; ++t) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(st + rr * 128 + 16 * ((2 * G + t) ^ sw(rr)));
+        av[rt][4 * t] = q[0]; av[rt][4 * t + 1] = q[1]; av[rt][4 * t + 2] = q[2]; av[rt][4 * t + 3] = q[3];
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) {
+      const int rr = 16 * ct + c;
+#pragma unroll
+      for (int t = 0; t < NWD / 4; ++t) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(st + A_BYTES + rr * 128 + 16 * ((2 * G + t) ^ sw(rr)));
+        bv[ct][4 * t] = q[0]; bv[ct][4 * t + 1] = q[1]; bv[ct][4 * t + 2] = q[2]; bv[ct][4 * t + 3] = q[3];
+      }
+    }
+    if constexpr (LN) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        float xf[KL];
+#pragma unroll
+        for (int e = 0; e < KL; ++e)
+          xf[e] = row_ok[rt] ? fmaf((LinT<T>::get(av[rt], e) - mu[rt]) * rs[rt], LinT<T>::get(gw + ch * NWD, e),
+                                    LinT<T>::get(bw + ch * NWD, e))
+                             : 0.f;
+#pragma unroll
+        for (int i = 0; i < NWD; ++i) {
+          if constexpr (BF) av[rt][i] = (uint32_t)f32_to_bf16(xf[2 * i]) | ((uint32_t)f32_to_bf16(xf[2 * i + 1]) << 16);
+          else av[rt][i] = __float_as_uint(xf[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) {
+        if constexpr (BF) {
+#pragma unroll
+          for (int s4 = 0; s4 < KL / 4; ++s4) {
+            const s16x4 x4 = __builtin_bit_cast(s16x4, (u32x2{av[rt][2 * s4], av[rt][2 * s4 + 1]}));
+            const s16x4 w4 = __builtin_bit_cast(s16x4, (u32x2{bv[ct][2 * s4], bv[ct][2 * s4 + 1]}));
+            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(x4, w4, acc[rt][ct], 0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int s1 = 0; s1 < KL; ++s1)
+            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(av[rt][s1]), __uint_as_float(bv[ct][s1]),
+                                                               acc[rt][ct], 0, 0, 0);
+        }
+      }
+    // refill this chunk's stage with chunk ch + STAGES once its reads have returned
+    if constexpr (ch + STAGES < NCH) {
+      lds_read_wait();
+      issue(ch + STAGES);
+    }
+  });
+
+  // ---- sum the wavefronts' partial tiles in LDS (the rings are free once every wavefront is
+  // past its loop), then one thread per output element -----------------------------------------
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(sm);
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(w * kTileRows + 16 * rt + 4 * G + i) * (BN + 1) + 16 * ct + c] = acc[rt][ct][i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + i * kTileWaves * kWave;
+    const int ml = e / BN, col = e % BN;
+    const int m = r0 + ml;
+    if (m >= a.M) continue;
+    float v = bias_e[i];
+#pragma unroll
+    for (int ww = 0; ww < kTileWaves; ++ww) v += red[(ww * kTileRows + ml) * (BN + 1) + col];
+    if (a.act == 1) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+    lin_store<T>(a, seg, m, n0 + col, v, res_e[i]);
+  }
 }
 
 static bool small_linear_k_supported(int32_t K) {
@@ -467,7 +792,57 @@ static bool lin_stage_in_lds() {
   return !(env != nullptr && strcmp(env, "regs") == 0);
 }
 
+// Kernel for a call: the tiled kernel above 16 rows where it applies (PAGED_HIP_LINEAR_KERNEL =
+// small / tiled forces one of them where both apply; tests use it to cover both).
+static bool tile_linear_applies(const LinArgs& a) {
+  if (a.row_sel != nullptr || a.token_keys != nullptr) return false;
+  if (!(a.K == 256 || a.K == 512 || a.K == 1024 || a.K == 2048)) return false;
+  if (a.ln_w != nullptr && a.K > 1024) return false;
+  if (a.seg_n % 16 != 0) return false;
+  return (int64_t)a.M * a.x_stride * (a.bf16 ? 2 : 4) < (1LL << 31);
+}
+
+// Measured in graph replay on MI355X (d_model 512, d_ff 2048; 16-row / tiled kernel, us): fc2
+// (K 2048) fp32 7.9 / 7.6 at 32 rows, 16.1 / 8.0 at 256; bf16 3.7 / 4.3 at 64, 4.4 / 4.4 at 128,
+// 7.0 / 4.6 at 256. K 512: LayerNorm + q/k/v fp32 9.7 / 11.6 at 128 rows, 13.5 / 14.3 at 192,
+// 15.7 / 14.5 at 256, 27.6 / 22.2 at 512; out_proj 3.7 / 3.9 at 128, 4.4 / 3.9 at 192; LayerNorm
+// + fc1 + GELU fp32 11.0 / 10.7 at 128, 15.3 / 14.0 at 192, bf16 11.1 / 9.2 at 192.
+static bool use_tile_linear(const LinArgs& a) {
+  if (!tile_linear_applies(a)) return false;
+  const char* env = getenv("PAGED_HIP_LINEAR_KERNEL");
+  if (env != nullptr && strcmp(env, "small") == 0) return false;
+  if (env != nullptr && strcmp(env, "tiled") == 0) return true;
+  if (a.K >= 1024) return a.M >= (a.bf16 ? 128 : 32);
+  return a.M >= 192;
+}
+
+static int launch_tile_linear(const LinArgs& a, hipStream_t stream) {
+  const int64_t row_tiles = (a.M + kTileRows - 1) / kTileRows;
+  // 32 columns per workgroup when that still gives a workgroup per compute unit, else 16
+  const bool nt2 = a.seg_n % 32 == 0 && (int64_t)a.nseg * (a.seg_n / 32) * row_tiles >= pa_host::device_cu_count();
+  const int bn = nt2 ? 32 : 16;
+  const dim3 grid((unsigned)(a.nseg * (a.seg_n / bn)), (unsigned)row_tiles);
+  const dim3 block(kTileWaves * kWave);
+  const bool ln = a.ln_w != nullptr;
+#define PA_TILE_LAUNCH(TT, KK, LNF)                                                   \
+  if (nt2) tile_linear_kernel<TT, KK, LNF, 2><<<grid, block, 0, stream>>>(a);         \
+  else tile_linear_kernel<TT, KK, LNF, 1><<<grid, block, 0, stream>>>(a);
+#define PA_TILE_K(TT)                                                                 \
+  switch (a.K) {                                                                      \
+    case 256: if (ln) { PA_TILE_LAUNCH(TT, 256, true) } else { PA_TILE_LAUNCH(TT, 256, false) } break; \
+    case 512: if (ln) { PA_TILE_LAUNCH(TT, 512, true) } else { PA_TILE_LAUNCH(TT, 512, false) } break; \
+    case 1024: if (ln) { PA_TILE_LAUNCH(TT, 1024, true) } else { PA_TILE_LAUNCH(TT, 1024, false) } break; \
+    case 2048: PA_TILE_LAUNCH(TT, 2048, false) break;                                 \
+  }
+  if (a.bf16) { PA_TILE_K(uint16_t) } else { PA_TILE_K(float) }
+#undef PA_TILE_K
+#undef PA_TILE_LAUNCH
+  PA_CHECK_LAUNCH("tiled linear kernel");
+  return PA_OK;
+}
+
 static int launch_small_linear(LinArgs a, hipStream_t stream) {
+  if (use_tile_linear(a)) return launch_tile_linear(a, stream);
   a.cw_log2 = lin_cw_log2(a);
   const int64_t tiles = (int64_t)a.nseg * ((a.seg_n + (1 << a.cw_log2) - 1) >> a.cw_log2);
   if (tiles > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");

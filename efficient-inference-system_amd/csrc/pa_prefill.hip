@@ -411,6 +411,7 @@ void prefill_mfma_kernel(const AttnArgs a) {
       for (int k = 0; k < cnt; ++k) {
         const int st = k & 1;
         if (k + 1 < cnt) {
+          lds_read_wait();  // the stage refilled now was read in step k - 1
           stage_issue(st ^ 1, k + 1);
           vm_wait<2 * NI>();
         } else {

@@ -837,6 +837,7 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void prefill_split_kernel(cons
     issue(0, 0);
     for (int k = 0; k < cnt; ++k) {
       if (k + 1 < cnt) {
+        lds_read_wait();  // the stage refilled now was read in step k - 1
         issue((k + 1) & 1, k + 1);
         vm_wait<2 * NDMA>();
       } else {

@@ -39,7 +39,7 @@ layer; PAGED_HIP_DECODE_FOLD=0 keeps five). A fused launch reads its weight tile
 once per 16 rows, so above a per-layer row count (FUSED_ROWS) that layer runs through torch
 instead. Set PAGED_HIP_FUSED_DECODE=0 to use the torch layers throughout.
 
-Query lengths T > 1 are padded up to a bucket (16, 32, 64, 128, 256) with token id 0 and the
+Query lengths T > 1 are padded up to a bucket (16, 32, 64, then every 32 to 256) with token id 0 and the
 logits of the real rows are returned. Padded rows are never appended to the cache (their slots
 are -1) and no real row reads them, so real rows are computed exactly as in eager mode; padded
 rows' positions are clamped to the position table.
@@ -71,23 +71,24 @@ try:  # native host bookkeeping (csrc/host/paged_host.cpp): same results as the 
 except ImportError:  # not built: the Python versions run
     _host = None
 
-T_BUCKETS = (16, 32, 64, 128, 256)
+# Query-length buckets of captured prefill steps: padded rows cost as much as real ones, so above
+# 64 rows the buckets are 32 rows apart.
+T_BUCKETS = (16, 32, 64, 96, 128, 160, 192, 224, 256)
 
 # Largest step (rows = B * bucketed T) for which each fused launch beats torch's layers, per
 # dtype. Measured in HIP-graph replay on MI355X (fused vs torch, us), d_model 512, d_ff 2048,
-# vocab 5000, the fused kernels staging their weight and activation slices through LDS:
-#   LayerNorm + q/k/v + append  fp32 6.4 vs 28.7 at 64 rows, 14.7 vs 26.4 at 256, 26.6 vs 28.0 at 512;
-#                               bf16 19.4 vs 23.2 at 512
-#   out_proj + residual         fp32 7.0 vs 8.7 at 512; bf16 4.5 vs 7.3 at 512
-#   LayerNorm + fc1 + GELU      fp32 10.6 vs 13.9 at 128, 15.2 vs 14.8 at 192; bf16 10.8 vs 13.3 at
-#                               192, 13.6 vs 13.7 at 256
-#   fc2 + residual              fp32 8.5 vs 9.0 at 96, 9.2 vs 9.1 at 128; bf16 6.8 vs 8.2 at 256,
-#                               9.3 vs 8.9 at 384
+# vocab 5000, with the library's choice between its 16-row and tiled kernels:
+#   LayerNorm + q/k/v + append  fp32 14.5 at 256 rows, 22.2 at 512 (torch's LayerNorm and three
+#                               GEMMs with the append: 26-28); bf16 16.8 at 512
+#   out_proj + residual         fp32 5.3 vs 8.2 at 512; bf16 4.2 vs 7.2 at 512
+#   LayerNorm + fc1 + GELU      fp32 14.1 vs 14.9 at 256, 21.3 vs 17.7 at 384; bf16 9.5 vs 13.7 at
+#                               256, 15.1 vs 14.1 at 384
+#   fc2 + residual              fp32 8.0 vs 10.7 at 256, 12.8 vs 14.9 at 512; bf16 6.1 vs 8.9 at 512
 #   LayerNorm + lm_head         fp32 10.7 vs 11.8 at 48, 15.8 vs 11.8 at 64; bf16 9.1 vs 10.4 at 64,
 #                               13.6 vs 11.2 at 96
 FUSED_ROWS = {
-    torch.float32: {"qkv": 512, "out_proj": 512, "fc1": 128, "fc2": 96, "lm_head": 48},
-    torch.bfloat16: {"qkv": 512, "out_proj": 512, "fc1": 192, "fc2": 256, "lm_head": 64},
+    torch.float32: {"qkv": 512, "out_proj": 512, "fc1": 256, "fc2": 512, "lm_head": 48},
+    torch.bfloat16: {"qkv": 512, "out_proj": 512, "fc1": 256, "fc2": 512, "lm_head": 64},
 }
 FUSED_STEP_ROWS = 512  # steps above this run the torch layers (q/k/v and out_proj limits)
 

@@ -127,28 +127,36 @@ class TinyTransformerLM(nn.Module):
         runner = self._graph_runner()
         before = runner.captures
         for B in range(1, max_batch + 1):
-            per_request = self.create_request_kv_caches(B)
             pools = self._ensure_layer_block_pools()
-
-            def stacked():
-                return [BatchedPagedKVCache([per_request[r][l] for r in range(B)], pools[l])
-                        for l in range(len(self.blocks))]
-
-            pos = 0
+            per_request, pos = None, 0
             for T in (16,) + tuple(T_BUCKETS) + (1,):
+                if per_request is None or pos + T > self.max_seq_len:
+                    # fresh requests once the current ones would outgrow the position table (the
+                    # first step of new requests runs eagerly and initialises nothing new)
+                    if per_request is not None:
+                        for r in range(B):
+                            self.release_request_caches(per_request[r])
+                    per_request, pos = self.create_request_kv_caches(B), 0
+                    if T > 16 and pos + 16 <= self.max_seq_len:
+                        self._prepare_step(per_request, pools, B, 16, pos, device, want_logits)
+                        pos += 16
                 if pos + T > self.max_seq_len:
                     continue
-                ids = torch.zeros((B, T), dtype=torch.long, device=device)
-                if want_logits:
-                    self(ids, kv_caches=stacked(), use_cache=True, position_offset=pos, current_lengths=T)
-                else:
-                    self.greedy_step(ids, stacked(), position_offset=pos, current_lengths=[T] * B)
+                self._prepare_step(per_request, pools, B, T, pos, device, want_logits)
                 pos += T
             for r in range(B):
                 self.release_request_caches(per_request[r])
         torch.cuda.synchronize(device)
         self.reset_paged_cache_pools()
         return runner.captures - before
+
+    def _prepare_step(self, per_request, pools, B, T, pos, device, want_logits) -> None:
+        caches = [BatchedPagedKVCache([per_request[r][l] for r in range(B)], pools[l]) for l in range(len(self.blocks))]
+        ids = torch.zeros((B, T), dtype=torch.long, device=device)
+        if want_logits:
+            self(ids, kv_caches=caches, use_cache=True, position_offset=pos, current_lengths=T)
+        else:
+            self.greedy_step(ids, caches, position_offset=pos, current_lengths=[T] * B)
 
     def create_request_kv_caches(self, batch_size: int) -> list[list[PagedKVCacheState]]:
         pools = self._ensure_layer_block_pools()
