@@ -508,6 +508,52 @@ def _chunked_prefill(res, device, steps, with_cpu):
             res[f"chunked_prefill_{tag}"]["cpu"] = cpu_call_times(
                 w["q"], w["k_pool"], w["v_pool"], lists, w["seq_lens"], w["chunk_lens"], loop_request=0)
         del w
+        res[f"chunked_prefill_{tag}"]["mixed_chunks"] = _chunked_prefill_mix(device, kv_dtype, steps, peak)
+
+
+def _chunked_prefill_mix(device, kv_dtype, steps, peak):
+    """The same configuration at seed 2, whose chunks are a 128/256 mix (seed 0 draws four
+    256-token chunks): attention time, eager and in graph replay."""
+    from src import workloads
+    from src.kernels.hip_paged_attention import kv_append_hip, paged_attention_prefill_hip
+
+    w = workloads.chunked_prefill(seed=2, device=device, kv_dtype=kv_dtype)
+    lists = w["block_lists"]
+    pt, s32, cur, slots = _prefill_metadata(device, lists, w["prev_lens"], w["chunk_lens"], w["q"].shape[2])
+    kv_append_hip(w["k_new"], w["v_new"], w["k_pool"], w["v_pool"], slots)
+    attn = lambda: paged_attention_prefill_hip(w["q"], w["k_pool"], w["v_pool"], pt, s32, cur)
+    attn_ms = time_call(attn, steps)
+    graph_ms = time_graph_call(attn)
+    flops = workloads.prefill_flops(w["prev_lens"], w["chunk_lens"], 8, 64)
+    padded = workloads.prefill_flops_with_padding(w["prev_lens"], w["chunk_lens"], w["q"].shape[2], 8, 64)
+    return {
+        "workload": f"seed 2: context {w['prev_lens']} + chunk {w['chunk_lens']}",
+        "attention_us": round(1e3 * attn_ms, 2), "attention_us_graph": round(1e3 * graph_ms, 2),
+        "useful_gflop": round(flops / 1e9, 4),
+        "gflop_with_padded_rows": round(padded / 1e9, 4),
+        "padded_rows": "rows past a 128-token chunk in the 256-row batch attend to all of their request's keys, "
+                       "as in the reference, so the kernel computes them; useful_gflop counts real rows only",
+        "TFLOPs_graph": round(flops / (graph_ms * 1e-3) / 1e12, 2),
+        "mfma_frac_graph": round(flops / (graph_ms * 1e-3) / 1e12 / peak, 4),
+        "mfma_frac_graph_with_padded_rows": round(padded / (graph_ms * 1e-3) / 1e12 / peak, 4),
+    }
+
+
+def _prefill_metadata(device, lists, prev_lens, chunk_lens, T):
+    """Page table, sequence lengths, chunk lengths and append slots of a chunked-prefill batch,
+    packed on the device (the chunk's blocks already in the lists)."""
+    import torch
+
+    from src.kernels.hip_paged_attention import pack_metadata_hip
+
+    flat = [i for x in lists for i in x]
+    offs = [0]
+    for x in lists:
+        offs.append(offs[-1] + len(x))
+    i32 = lambda a: torch.tensor(a, dtype=torch.int32, device=device)
+    pt, s32, _, slots = pack_metadata_hip(i32(flat), i32(offs), i32(prev_lens), i32(chunk_lens),
+                                          query_len=T, block_size=16, max_pages=max(len(x) for x in lists))
+    return pt, s32, i32(chunk_lens), slots
 
 
 def _large_prefill(res, device, steps):

@@ -191,6 +191,18 @@ def prefill_flops(prev_lens: list[int], chunk_lens: list[int], heads: int, head_
     return sum(4 * heads * head_dim * (c * c0 + c * (c + 1) // 2) for c0, c in zip(prev_lens, chunk_lens))
 
 
+def prefill_flops_with_padding(prev_lens: list[int], chunk_lens: list[int], query_len: int, heads: int,
+                               head_dim: int) -> int:
+    """FLOPs over every row of a [B, H, query_len] batch, the padded rows past a shorter chunk
+    included: padded row i of request b attends to all of its seq_len keys, as in the reference
+    (src/kernels/reference_paged_attention.py:33-42), so a kernel computes them too."""
+    total = 0
+    for c0, c in zip(prev_lens, chunk_lens):
+        L = c0 + c
+        total += c * c0 + c * (c + 1) // 2 + (query_len - c) * L
+    return 4 * heads * head_dim * total
+
+
 def large_prefill(seed: int = 0, device="cpu", batch: int = 8, heads: int = 32, head_dim: int = 128,
                   chunk: int = 512, ctx_lo: int = 1024, ctx_hi: int = 4096,
                   kv_dtype: torch.dtype = torch.bfloat16) -> PagedBatch:

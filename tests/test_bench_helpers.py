@@ -70,3 +70,15 @@ def test_token_agreement_counts():
     assert bench.token_agreement(a, a)["requests_identical"] == 3
     # a request missing from the second run counts as different from its first token
     assert bench.token_agreement({3: [1, 2]}, {})["first_difference_positions"] == [0]
+
+
+@pytest.mark.parametrize("prev,chunks,T", [([704, 384, 736, 480], [128, 256, 128, 256], 256),
+                                          ([0, 16], [5, 32], 32), ([176, 608], [256, 256], 256)])
+def test_prefill_flops_with_padding(prev, chunks, T):
+    """4 * H * Hd FLOPs per attended (row, key) pair over every row of the padded batch: the
+    brute-force count of the reference loop's visited pairs; equal to the useful count when no
+    row is padded."""
+    want = 4 * 8 * 64 * _brute_pairs([p + c for p, c in zip(prev, chunks)], chunks, T)
+    assert workloads.prefill_flops_with_padding(prev, chunks, T, 8, 64) == want
+    if all(c == T for c in chunks):
+        assert want == workloads.prefill_flops(prev, chunks, 8, 64)

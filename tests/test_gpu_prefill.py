@@ -93,7 +93,8 @@ def test_chunked_prefill_config(device, seed, kv_dtype, tol):
 def test_kv_staging_lds_and_registers_agree(device, monkeypatch, seed, kv_dtype, tol):
     """The 16-row kernel's two KV stagings (LDS-direct copies into a per-wavefront ring, or loads
     straight into the operand registers) run the same products in the same order: bit-identical
-    outputs on the chunked-prefill workload, unsplit and split, and within tolerance of the oracle."""
+    outputs on the chunked-prefill workload, unsplit and split (down to one block per split), and
+    within tolerance of the oracle."""
     w = workloads.chunked_prefill(seed=seed, device=device, kv_dtype=kv_dtype)
     lists = w["block_lists"]
     b = workloads._batch(w["q"], w["k_pool"], w["v_pool"], lists, w["seq_lens"], w["chunk_lens"], device)
@@ -101,11 +102,29 @@ def test_kv_staging_lds_and_registers_agree(device, monkeypatch, seed, kv_dtype,
     outs = {}
     for staging in ("lds", "regs"):
         monkeypatch.setenv("PAGED_HIP_PREFILL_STAGING", staging)
-        for split in (0, 3):
+        for split in (0, 1, 3):
             outs[staging, split] = run(b, split_blocks=split)
-    for split in (0, 3):
+    for split in (0, 1, 3):
         assert torch.equal(outs["lds", split], outs["regs", split]), split
     err = max_err(outs["lds", 0], oracle_out(b))
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= tol
+
+
+@pytest.mark.parametrize("kv_dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_kv_staging_over_several_page_table_chunks(device, monkeypatch, kv_dtype, tol):
+    """Contexts of 4.4k and 5.1k tokens, unsplit: each wavefront walks 69-80 blocks, so the walk
+    restarts at a second 64-entry page-table chunk of 5-16 blocks. Both stagings bit-identical
+    and within tolerance of the oracle."""
+    b = make_prefill(device, 5, [4400, 5090], [32, 21], 32, 2, 64, kv_dtype=kv_dtype)
+    print(f"kv staging long contexts kv={kv_dtype}", flush=True)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", "tile")
+    outs = {}
+    for staging in ("lds", "regs"):
+        monkeypatch.setenv("PAGED_HIP_PREFILL_STAGING", staging)
+        outs[staging] = run(b, split_blocks=0)
+    assert torch.equal(outs["lds"], outs["regs"])
+    err = max_err(outs["lds"], oracle_out(b))
     print(f"  max err {err:.2e}", flush=True)
     assert err <= tol
 
