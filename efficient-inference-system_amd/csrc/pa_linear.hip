@@ -367,7 +367,7 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
     }
 #pragma unroll
     for (int i = 0; i < NWD; ++i) {
-      if constexpr (BF) xv[i] = (uint32_t)f32_to_bf16(xf[2 * i]) | ((uint32_t)f32_to_bf16(xf[2 * i + 1]) << 16);
+      if constexpr (BF) xv[i] = pack_bf16x2(xf[2 * i], xf[2 * i + 1]);
       else xv[i] = __float_as_uint(xf[i]);
     }
   }
@@ -581,33 +581,51 @@ __global__ __launch_bounds__(kTileWaves * kWave) void tile_linear_kernel(const L
   // 8w .. 8w + 7, all 64 lanes along each row), while the ring's first chunks are in flight. ----
   float mu[2] = {0.f, 0.f}, rs[2] = {0.f, 0.f};
   if constexpr (LN && !Sh::FULL) {
-    constexpr int EL = K / kWave;  // values per lane of one row
-    constexpr int LW = EL / EPW;   // words per lane of one row
-    static_assert(LW == 2 || LW % 4 == 0, "row slice per lane");
-    uint32_t xr[8][LW];
+    // wavefront w takes rows 8w .. 8w + 7 with 8 lanes per row (lane 8i + j: row i, 16-byte
+    // pieces 8t + j of it), so every load instruction reads 128 contiguous bytes per row and a
+    // row's sums close with three DPP steps instead of a wavefront-wide reduction per row
+    constexpr int PL = K * (int)sizeof(T) / 128;  // 16-byte pieces per lane
+    constexpr int PH = PL < 16 ? PL : 16;          // pieces held at once (fp32 K 1024 reads twice)
+    constexpr int NH = PL / PH;
+    const int ri = lane >> 3, pj = lane & 7;
+    const int r = r0 + 8 * w + ri;
+    const u32x4* xp = reinterpret_cast<const u32x4*>(X + (int64_t)(r < a.M ? r : a.M - 1) * a.x_stride);
+    u32x4 xr[PH];
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = r0 + 8 * w + i;
-      const int rr = r < a.M ? r : a.M - 1;
-      load_words(xr[i], X + (int64_t)rr * a.x_stride + lane * EL, true);
+    for (int hh = 0; hh < NH; ++hh) {
+#pragma unroll
+      for (int t = 0; t < PH; ++t) xr[t] = xp[8 * (hh * PH + t) + pj];
+#pragma unroll
+      for (int t = 0; t < PH; ++t) {
+        const uint32_t qw[4] = {xr[t][0], xr[t][1], xr[t][2], xr[t][3]};
+#pragma unroll
+        for (int e = 0; e < 4 * EPW; ++e) part[e & 3] += LinT<T>::get(qw, e);
+      }
     }
+    const float mean = group_sum<8>((part[0] + part[1]) + (part[2] + part[3])) / K;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float sum = 0.f;
+    for (int e = 0; e < 4; ++e) part[e] = 0.f;
 #pragma unroll
-      for (int e = 0; e < EL; ++e) sum += LinT<T>::get(xr[i], e);
-      const float mean = wave_sum(sum) / K;
-      float q = 0.f;
+    for (int hh = 0; hh < NH; ++hh) {
+      if (NH > 1) {
 #pragma unroll
-      for (int e = 0; e < EL; ++e) {
-        const float d = LinT<T>::get(xr[i], e) - mean;
-        q = fmaf(d, d, q);
+        for (int t = 0; t < PH; ++t) xr[t] = xp[8 * (hh * PH + t) + pj];
       }
-      const float var = wave_sum(q) / K;
-      if (lane == 0) {
-        sm_stat[8 * w + i][0] = mean;
-        sm_stat[8 * w + i][1] = 1.f / sqrtf(var + a.ln_eps);
+#pragma unroll
+      for (int t = 0; t < PH; ++t) {
+        const uint32_t qw[4] = {xr[t][0], xr[t][1], xr[t][2], xr[t][3]};
+#pragma unroll
+        for (int e = 0; e < 4 * EPW; ++e) {
+          const float d = LinT<T>::get(qw, e) - mean;
+          part[e & 3] = fmaf(d, d, part[e & 3]);
+        }
       }
+    }
+    const float var = group_sum<8>((part[0] + part[1]) + (part[2] + part[3])) / K;
+    if (pj == 0) {
+      sm_stat[8 * w + ri][0] = mean;
+      sm_stat[8 * w + ri][1] = 1.f / sqrtf(var + a.ln_eps);
     }
     __syncthreads();
 #pragma unroll
@@ -662,9 +680,6 @@ __global__ __launch_bounds__(kTileWaves * kWave) void tile_linear_kernel(const L
       rs[rt] = sm_stat[16 * rt + c][1];
     }
   }
-  bool row_ok[2];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) row_ok[rt] = r0 + 16 * rt + c < a.M;
 
   f32x4 acc[2][NT];
 #pragma unroll
@@ -702,13 +717,12 @@ __global__ __launch_bounds__(kTileWaves * kWave) void tile_linear_kernel(const L
       for (int rt = 0; rt < 2; ++rt) {
         float xf[KL];
 #pragma unroll
-        for (int e = 0; e < KL; ++e)
-          xf[e] = row_ok[rt] ? fmaf((LinT<T>::get(av[rt], e) - mu[rt]) * rs[rt], LinT<T>::get(gw + ch * NWD, e),
-                                    LinT<T>::get(bw + ch * NWD, e))
-                             : 0.f;
+        for (int e = 0; e < KL; ++e)  // (rows past M hold row M - 1 and are never stored)
+          xf[e] = fmaf((LinT<T>::get(av[rt], e) - mu[rt]) * rs[rt], LinT<T>::get(gw + ch * NWD, e),
+                       LinT<T>::get(bw + ch * NWD, e));
 #pragma unroll
         for (int i = 0; i < NWD; ++i) {
-          if constexpr (BF) av[rt][i] = (uint32_t)f32_to_bf16(xf[2 * i]) | ((uint32_t)f32_to_bf16(xf[2 * i + 1]) << 16);
+          if constexpr (BF) av[rt][i] = pack_bf16x2(xf[2 * i], xf[2 * i + 1]);
           else av[rt][i] = __float_as_uint(xf[i]);
         }
       }
@@ -803,17 +817,18 @@ static bool tile_linear_applies(const LinArgs& a) {
 }
 
 // Measured in graph replay on MI355X (d_model 512, d_ff 2048; 16-row / tiled kernel, us): fc2
-// (K 2048) fp32 7.9 / 7.6 at 32 rows, 16.1 / 8.0 at 256; bf16 3.7 / 4.3 at 64, 4.4 / 4.4 at 128,
-// 7.0 / 4.6 at 256. K 512: LayerNorm + q/k/v fp32 9.7 / 11.6 at 128 rows, 13.5 / 14.3 at 192,
-// 15.7 / 14.5 at 256, 27.6 / 22.2 at 512; out_proj 3.7 / 3.9 at 128, 4.4 / 3.9 at 192; LayerNorm
-// + fc1 + GELU fp32 11.0 / 10.7 at 128, 15.3 / 14.0 at 192, bf16 11.1 / 9.2 at 192.
+// (K 2048) fp32 8.0 / 7.6 at 32 rows, 16.1 / 8.1 at 256; bf16 3.8 / 4.3 at 64, 4.5 / 4.4 at 128,
+// 7.2 / 4.7 at 256. K 512 with LayerNorm: q/k/v fp32 6.7 / 6.8 at 64 rows, 9.3 / 9.2 at 128, 13.4 /
+// 11.8 at 192; fc1 + GELU fp32 6.5 / 6.5 at 64, 11.1 / 8.1 at 128, bf16 7.5 / 6.4 at 128 (q/k/v
+// bf16 6.3 / 6.8 at 128, 8.6 / 8.0 at 192). K 512 without: out_proj 3.7 / 3.8 at 128 rows, 4.4 /
+// 3.9 at 192.
 static bool use_tile_linear(const LinArgs& a) {
   if (!tile_linear_applies(a)) return false;
   const char* env = getenv("PAGED_HIP_LINEAR_KERNEL");
   if (env != nullptr && strcmp(env, "small") == 0) return false;
   if (env != nullptr && strcmp(env, "tiled") == 0) return true;
   if (a.K >= 1024) return a.M >= (a.bf16 ? 128 : 32);
-  return a.M >= 192;
+  return a.M >= (a.ln_w != nullptr ? 96 : 192);
 }
 
 static int launch_tile_linear(const LinArgs& a, hipStream_t stream) {

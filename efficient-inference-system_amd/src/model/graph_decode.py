@@ -78,17 +78,17 @@ T_BUCKETS = (16, 32, 64, 96, 128, 160, 192, 224, 256)
 # Largest step (rows = B * bucketed T) for which each fused launch beats torch's layers, per
 # dtype. Measured in HIP-graph replay on MI355X (fused vs torch, us), d_model 512, d_ff 2048,
 # vocab 5000, with the library's choice between its 16-row and tiled kernels:
-#   LayerNorm + q/k/v + append  fp32 14.5 at 256 rows, 22.2 at 512 (torch's LayerNorm and three
-#                               GEMMs with the append: 26-28); bf16 16.8 at 512
-#   out_proj + residual         fp32 5.3 vs 8.2 at 512; bf16 4.2 vs 7.2 at 512
-#   LayerNorm + fc1 + GELU      fp32 14.1 vs 14.9 at 256, 21.3 vs 17.7 at 384; bf16 9.5 vs 13.7 at
-#                               256, 15.1 vs 14.1 at 384
-#   fc2 + residual              fp32 8.0 vs 10.7 at 256, 12.8 vs 14.9 at 512; bf16 6.1 vs 8.9 at 512
+#   LayerNorm + q/k/v + append  fp32 11.8 at 256 rows, 17.3 at 512 (torch's LayerNorm and three
+#                               GEMMs with the append: 26-28); bf16 13.9 at 512
+#   out_proj + residual         fp32 5.4 vs 8.4 at 512; bf16 4.3 vs 7.3 at 512
+#   LayerNorm + fc1 + GELU      fp32 16.3 vs 17.8 at 384, 20.0 vs 20.2 at 512; bf16 11.9 vs 14.1 at
+#                               384, 13.5 vs 14.5 at 512
+#   fc2 + residual              fp32 8.1 vs 10.9 at 256, 13.0 vs 14.9 at 512; bf16 6.1 vs 9.0 at 512
 #   LayerNorm + lm_head         fp32 10.7 vs 11.8 at 48, 15.8 vs 11.8 at 64; bf16 9.1 vs 10.4 at 64,
 #                               13.6 vs 11.2 at 96
 FUSED_ROWS = {
-    torch.float32: {"qkv": 512, "out_proj": 512, "fc1": 256, "fc2": 512, "lm_head": 48},
-    torch.bfloat16: {"qkv": 512, "out_proj": 512, "fc1": 256, "fc2": 512, "lm_head": 64},
+    torch.float32: {"qkv": 512, "out_proj": 512, "fc1": 512, "fc2": 512, "lm_head": 48},
+    torch.bfloat16: {"qkv": 512, "out_proj": 512, "fc1": 512, "fc2": 512, "lm_head": 64},
 }
 FUSED_STEP_ROWS = 512  # steps above this run the torch layers (q/k/v and out_proj limits)
 
