@@ -67,6 +67,7 @@ struct LinArgs {
   int32_t sel_group;       // (a negative entry counts from the group's end; clamped into the group)
   unsigned long long* token_keys;  // when set: per row, the running minimum of token_key over the
                                    // row's outputs (the row's greedy token in the low 32 bits)
+  int64_t keys_stride;             // elements between rows' keys
   // Second layer folded into the first (small_linear_kernel with F2; fp32, one 16-row tile, 16
   // columns per workgroup): with h = this workgroup's 16 output columns n0.. of the first layer
   // (after bias and activation), out2[m][j] += sum_c h[m][c] * w2[j][n0 + c] for j < n2, by
@@ -442,7 +443,8 @@ __global__ __launch_bounds__(lin_waves<K>() * kWave) void small_linear_kernel(co
       const unsigned long long o = __shfl_xor(key, off);
       key = o < key ? o : key;
     }
-    if (cc == 0 && m < a.M) __hip_atomic_fetch_min(a.token_keys + m, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cc == 0 && m < a.M)
+      __hip_atomic_fetch_min(a.token_keys + m * a.keys_stride, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!live) return;
   }
   lin_store<T>(a, seg, m, n, v, res_v);
@@ -993,7 +995,8 @@ extern "C" int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t gr
                                      const int32_t* row_index, int32_t in_features, const void* weight,
                                      const void* bias, int32_t out_features, const void* ln_weight,
                                      const void* ln_bias, float ln_eps, int32_t activation, void* out,
-                                     int64_t out_stride, uint64_t* token_keys, int dtype, void* stream) {
+                                     int64_t out_stride, uint64_t* token_keys, int64_t token_keys_stride,
+                                     int dtype, void* stream) {
   pa_host::clear_error();
   PA_CHECK_ARG(groups >= 0 && groups <= kLinMaxRows, "groups must be in [0, %d], got %d", kLinMaxRows, groups);
   PA_CHECK_ARG(group_rows > 0, "group_rows must be positive, got %d", group_rows);
@@ -1015,7 +1018,10 @@ extern "C" int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t gr
   a.out = out; a.out_stride = out_stride; a.bf16 = dtype == PA_DTYPE_BF16;
   a.row_sel = row_index; a.sel_group = group_rows;
   PA_CHECK_ARG((reinterpret_cast<uintptr_t>(token_keys) & 7) == 0, "token_keys must be 8-byte aligned");
+  PA_CHECK_ARG(token_keys == nullptr || token_keys_stride >= 1, "token_keys_stride must be >= 1, got %lld",
+               (long long)token_keys_stride);
   a.token_keys = reinterpret_cast<unsigned long long*>(token_keys);
+  a.keys_stride = token_keys_stride;
   return launch_small_linear(a, static_cast<hipStream_t>(stream));
 }
 

@@ -106,7 +106,8 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _i64, _i32, _i32, _c_void_p,  # x, stride, groups, group rows, row index
          _i32, _c_void_p, _c_void_p, _i32,  # in_features, weight, bias, out_features
          _c_void_p, _c_void_p, _f32,  # LayerNorm weight, bias, eps
-         _i32, _c_void_p, _i64, _c_void_p, _int, _c_void_p],  # activation, out, stride, token keys, dtype, stream
+         _i32, _c_void_p, _i64, _c_void_p, _i64,  # activation, out, stride, token keys, key stride
+         _int, _c_void_p],  # dtype, stream
     ),
     "pa_qkv_append": (
         _int,

@@ -100,9 +100,11 @@ def linear_select_rows_hip(x: torch.Tensor, group_rows: int, row_index: torch.Te
     count from the group's end; clamped into the group), for the len(row_index) groups of rows of
     x; x, the layer's parameters and out share one dtype (float32 or bfloat16).
 
-    token_keys (int64 [groups] device tensor holding -1, i.e. all bits set): the same launch folds
-    in each group's greedy token; afterwards token_keys.view(torch.int32)[0::2] holds
-    torch.argmax(out[g]) per group (see token_keys_to_tokens)."""
+    token_keys (int64 [groups] device tensor, any positive stride, holding -1, i.e. all bits set):
+    the same launch folds in each group's greedy token; afterwards the low 32-bit word of
+    token_keys[g] holds torch.argmax(out[g]) (see token_keys_to_tokens). Every workgroup sends one
+    atomic per group, so keys one 128-byte line apart (a stride of KEY_STRIDE) are faster for
+    several groups."""
     _rows(x, "x")
     dt = x.dtype
     M, K = x.shape
@@ -123,23 +125,29 @@ def linear_select_rows_hip(x: torch.Tensor, group_rows: int, row_index: torch.Te
     if out.shape[0] < groups or out.shape[1] != N:
         raise ValueError(f"out must hold {groups} rows of {N} features")
     if token_keys is not None and (token_keys.dtype != torch.int64 or token_keys.dim() != 1 or token_keys.numel() < groups
-                                   or token_keys.stride(0) != 1 or token_keys.device != x.device):
-        raise ValueError("token_keys must be a unit-stride int64 [groups] tensor on x's device")
+                                   or token_keys.stride(0) < 1 or token_keys.device != x.device):
+        raise ValueError("token_keys must be a positively strided int64 [groups] tensor on x's device")
     status = _lib.load().pa_linear_select_rows(
         x.data_ptr(), x.stride(0), groups, group_rows, row_index.data_ptr(), K,
         linear.weight.data_ptr(), _ptr(linear.bias), N,
         _ptr(ln.weight if ln is not None else None), _ptr(ln.bias if ln is not None else None),
         float(ln.eps) if ln is not None else 0.0,
-        1 if gelu else 0, out.data_ptr(), out.stride(0), _ptr(token_keys), _lib.dtype_code(dt), _stream(x.device),
+        1 if gelu else 0, out.data_ptr(), out.stride(0), _ptr(token_keys),
+        token_keys.stride(0) if token_keys is not None else 1, _lib.dtype_code(dt), _stream(x.device),
     )
     _lib.check(status, "pa_linear_select_rows")
     return out
 
 
+KEY_STRIDE = 16  # int64 elements: one 128-byte line per group's token key
+
+
 def token_keys_to_tokens(token_keys: torch.Tensor) -> torch.Tensor:
     """The greedy tokens folded into token_keys by linear_select_rows_hip: the low 32-bit word of
-    each key (a strided int32 view, no copy)."""
-    return token_keys.view(torch.int32)[0::2]
+    each key (a strided int32 view of the same memory, no copy)."""
+    words = torch.empty(0, dtype=torch.int32, device=token_keys.device)
+    return words.set_(token_keys.untyped_storage(), 2 * token_keys.storage_offset(), (token_keys.numel(),),
+                      (2 * token_keys.stride(0),))
 
 
 def qkv_append_hip(x: torch.Tensor, ln: nn.LayerNorm, attn, k_pool: torch.Tensor, v_pool: torch.Tensor,

@@ -282,16 +282,17 @@ class _Captured:
         # that launch (token keys, reset to all ones by the staging copy of every step).
         self.select_head = tokens_only and hip_linear.model_supported(model)
         # Step descriptor (int32 words of pinned host memory the device reads):
-        #   [ids int64 B*Tb | first positions int64 B | current lengths B | greedy rows B |
-        #    token keys int64 B, all ones (select_head only)]
+        #   [ids int64 B*Tb | first positions int64 B | current lengths B | greedy rows B | padding |
+        #    token keys, one 128-byte line per request, all ones (select_head only)]
         #     staged into the device buffer `stage` by the metadata launch;
         #   [mirror rows B | first changed page B | list lengths B | lengths before B | appended B |
         #    update ids, mirror width words per request]  read by that launch in place.
         o_pos = 2 * B * Tb
         o_cur = o_pos + 2 * B
         o_sel = o_cur + B
-        o_key = o_sel + B  # even: the keys are 8-byte aligned in `stage`
-        self.stage_words = o_key + (2 * B if self.select_head else 0)
+        ks = hip_linear.KEY_STRIDE
+        o_key = -(-(o_sel + B) // (2 * ks)) * (2 * ks)  # each request's key on its own 128-byte line
+        self.stage_words = o_key + (2 * B * ks if self.select_head else 0)
         o_mrow = self.stage_words
         o_first, o_npages = o_mrow + B, o_mrow + 2 * B
         o_prev = o_npages + B
@@ -313,7 +314,7 @@ class _Captured:
         self.cur = self.stage[o_cur:o_sel]
         self.rows = self.stage[o_sel:o_sel + B]
         if self.select_head:
-            self.keys = self.stage[o_key:self.stage_words].view(torch.int64)
+            self.keys = self.stage[o_key:self.stage_words].view(torch.int64).view(B, ks)[:, 0]
             self.tokens = hip_linear.token_keys_to_tokens(self.keys)
         else:
             self.keys = None

@@ -251,19 +251,23 @@ int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int32_t in_fea
  * ln_f + lm_head (src/model/transformer.py:176-177) only for the row of each request whose greedy
  * token the executors take (src/serving/continuous_generate.py:145,238), instead of every row
  * of a prefill chunk.
- * token_keys (device uint64 [groups], 8-byte aligned, or NULL): when set, each group's greedy
- * token is folded in as well, the argmax the executors take (continuous_generate.py:145,238)
- * without a separate launch: token_keys[g] is lowered (atomic minimum) to the least key over the
- * group's out_features columns, key = ((uint64)~ord(v) << 32) | column, v the column's output as
- * stored (rounded to dtype) and ord the order-preserving bits of v (NaN highest, -0.0 = +0.0). The
- * caller sets token_keys to all ones before the call; afterwards the low 32 bits of token_keys[g]
- * are torch.argmax of out[g, :] (the first index of the maximum; the first NaN if any).
+ * token_keys (device uint64, 8-byte aligned, or NULL; group g's key at token_keys[g *
+ * token_keys_stride], token_keys_stride >= 1): when set, each group's greedy token is folded in
+ * as well, the argmax the executors take (continuous_generate.py:145,238) without a separate
+ * launch: group g's key is lowered (atomic minimum) to the least key over the group's
+ * out_features columns, key = ((uint64)~ord(v) << 32) | column, v the column's output as stored
+ * (rounded to dtype) and ord the order-preserving bits of v (NaN highest, -0.0 = +0.0). The
+ * caller sets the keys to all ones before the call; afterwards the low 32 bits of group g's key
+ * are torch.argmax of out[g, :] (the first index of the maximum; the first NaN if any). Every
+ * workgroup of the launch sends one atomic per group, so keys 128 bytes apart (stride 16) keep
+ * the groups' atomics off one cache line.
  */
 int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t groups, int32_t group_rows,
                           const int32_t* row_index, int32_t in_features, const void* weight,
                           const void* bias, int32_t out_features, const void* ln_weight,
                           const void* ln_bias, float ln_eps, int32_t activation, void* out,
-                          int64_t out_stride, uint64_t* token_keys, int dtype, void* stream);
+                          int64_t out_stride, uint64_t* token_keys, int64_t token_keys_stride,
+                          int dtype, void* stream);
 
 /*
  * pa_qkv_append: the three projections of a cached attention layer in one launch, with the

@@ -114,16 +114,20 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     assert lin(None, 0, 0, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 0, None, 0, BF16, None) == _lib.PA_OK
     # the row-selecting form: group_rows must be positive, row_index present, at most 1024 groups
     sel = lib.pa_linear_select_rows
-    assert sel(A, 512, 2, 0, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert sel(A, 512, 2, 0, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, 1, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"group_rows" in lib.pa_last_error_message()
-    assert sel(A, 512, 2, 4, None, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert sel(A, 512, 1025, 4, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert sel(A, 96, 2, 4, A, 96, A, None, 32, None, None, 0.0, 0, A, 32, None, F32, None) == _lib.PA_ERR_UNSUPPORTED
-    assert sel(None, 0, 0, 4, None, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, F32, None) == _lib.PA_OK
+    assert sel(A, 512, 2, 4, None, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, 1, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert sel(A, 512, 1025, 4, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, 1, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert sel(A, 96, 2, 4, A, 96, A, None, 32, None, None, 0.0, 0, A, 32, None, 1, F32, None) == _lib.PA_ERR_UNSUPPORTED
+    assert sel(None, 0, 0, 4, None, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 1, F32, None) == _lib.PA_OK
     # greedy-token keys must be 8-byte aligned
-    assert sel(A, 512, 2, 4, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, A + 4, F32, None) \
+    assert sel(A, 512, 2, 4, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, A + 4, 1, F32, None) \
         == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"token_keys" in lib.pa_last_error_message()
+    # and their stride positive
+    assert sel(A, 512, 2, 4, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, A, 0, F32, None) \
+        == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"token_keys_stride" in lib.pa_last_error_message()
     # q/k/v: d_model must be heads x head_dim
     qkv = lib.pa_qkv_append
     assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 32, 16,

@@ -339,12 +339,14 @@ def test_linear_lds_staging_matches_registers(device, monkeypatch, dtype, K, M, 
     assert err <= (2e-5 if dtype == torch.float32 else 0.1)
 
 
+@pytest.mark.parametrize("key_stride", [1, hip_linear.KEY_STRIDE])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("case", ["plain", "ties", "zeros", "nan"])
-def test_linear_select_rows_folds_the_argmax(device, dtype, case):
+def test_linear_select_rows_folds_the_argmax(device, dtype, case, key_stride):
     """pa_linear_select_rows with token_keys: the low word of each group's key is torch.argmax of
     the group's output row as stored (first index of the maximum; -0.0 == +0.0; the first NaN
-    wins), the outputs themselves unchanged; exact ties planted by duplicated weight rows."""
+    wins), the outputs themselves unchanged; exact ties planted by duplicated weight rows. Keys
+    packed or one 128-byte line apart; the words between strided keys stay untouched."""
     torch.manual_seed(11)
     K, N, groups, rows = 512, 5000, 6, 9
     lin = nn.Linear(K, N).to(device, dtype)
@@ -367,14 +369,17 @@ def test_linear_select_rows_folds_the_argmax(device, dtype, case):
             lin.bias[4100] = float("nan")  # the first NaN column wins
     x = torch.randn(groups * rows, K, device=device, dtype=dtype)
     idx = torch.tensor([r % rows - (r % 2) * rows for r in range(groups)], dtype=torch.int32, device=device)
-    keys = torch.full((groups,), -1, dtype=torch.int64, device=device)
-    print(f"folded argmax dtype={dtype} case={case}", flush=True)
+    key_buf = torch.full((groups, key_stride), -1, dtype=torch.int64, device=device)
+    key_buf[:, 1:] = 7
+    keys = key_buf[:, 0]
+    print(f"folded argmax dtype={dtype} case={case} key stride={key_stride}", flush=True)
     out = hip_linear.linear_select_rows_hip(x, rows, idx, lin, ln=ln, token_keys=keys)
     plain = hip_linear.linear_select_rows_hip(x, rows, idx, lin, ln=ln)
     assert torch.equal(out, plain) if case != "nan" else torch.equal(out.isnan(), plain.isnan())
     tokens = hip_linear.token_keys_to_tokens(keys).tolist()
     want = torch.argmax(plain.float().cpu(), dim=1).tolist()
     assert tokens == want
+    assert bool((key_buf[:, 1:] == 7).all())
     if case == "ties":
         assert want == [17] * groups
     if case == "zeros":
