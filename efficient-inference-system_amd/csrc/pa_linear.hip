@@ -36,7 +36,7 @@ constexpr int kLinRows = 16;     // activation rows per workgroup (MFMA tile hei
 // Rows per call, in 16-row tiles along grid y. A workgroup reads its weight tile once per 16-row
 // tile, so these kernels are for small row counts; against torch's LayerNorm / GEMM / epilogue
 // sequence they win up to 32-512 rows depending on the layer (the graph runner picks per layer).
-constexpr int kLinMaxRows = 1024;
+constexpr int kLinMaxRows = 2048;
 
 struct LinArgs {
   const void* x;      // [M, K] rows of type T

@@ -1,4 +1,4 @@
-"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32 or bf16, <= 1024 rows).
+"""torch-facing wrappers of the decode-step linear kernels of libpaged_hip (fp32 or bf16, <= 2048 rows).
 
   linear_rows_hip  act(LayerNorm(x) W^T + b) + residual in one launch     (pa_linear_rows)
   linear_select_rows_hip  the same without residual for one selected row per group of rows
@@ -22,7 +22,7 @@ import torch.nn as nn
 
 from src.kernels import _lib
 
-MAX_ROWS = 1024  # rows per call accepted by the library (16-row tiles)
+MAX_ROWS = 2048  # rows per call accepted by the library
 SUPPORTED_FEATURES = (128, 256, 512, 1024, 2048)
 
 
@@ -60,7 +60,7 @@ def supported(linear: nn.Linear) -> bool:
 def linear_rows_hip(x: torch.Tensor, linear: nn.Linear, *, ln: nn.LayerNorm | None = None, gelu: bool = False,
                     residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
                     copy_to: torch.Tensor | None = None) -> torch.Tensor:
-    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 1024); x, the layer's
+    """out[m] = act(LN(x[m]) W^T + b) + residual[m] for the rows of x (at most 2048); x, the layer's
     parameters, residual and out share one dtype (float32 or bfloat16). copy_to: the same rows are
     also written there (it may be residual itself)."""
     _rows(x, "x")

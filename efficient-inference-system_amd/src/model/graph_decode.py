@@ -28,7 +28,7 @@ list when that state is garbage collected, and the least recently used row is ta
 none is free.
 
 Steps of at most FUSED_STEP_ROWS rows (B * bucketed T: every decode step, and prefill chunks up
-to 512 rows) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
+to 1024 rows) run the layers through the fused kernels (src/kernels/hip_linear.py) when the model's
 shapes allow: per layer one launch for LayerNorm + q/k/v projections + KV append, the attention
 (decode or chunked prefill kernel), one for the output projection + residual, one for LayerNorm +
 fc1 + GELU, one for fc2 + residual; then LayerNorm + lm_head. Steps of at most 16 rows of an fp32
@@ -78,19 +78,20 @@ T_BUCKETS = (16, 32, 64, 96, 128, 160, 192, 224, 256)
 # Largest step (rows = B * bucketed T) for which each fused launch beats torch's layers, per
 # dtype. Measured in HIP-graph replay on MI355X (fused vs torch, us), d_model 512, d_ff 2048,
 # vocab 5000, with the library's choice between its 16-row and tiled kernels:
-#   LayerNorm + q/k/v + append  fp32 11.8 at 256 rows, 17.3 at 512 (torch's LayerNorm and three
-#                               GEMMs with the append: 26-28); bf16 13.9 at 512
-#   out_proj + residual         fp32 5.4 vs 8.4 at 512; bf16 4.3 vs 7.3 at 512
-#   LayerNorm + fc1 + GELU      fp32 16.3 vs 17.8 at 384, 20.0 vs 20.2 at 512; bf16 11.9 vs 14.1 at
-#                               384, 13.5 vs 14.5 at 512
-#   fc2 + residual              fp32 8.1 vs 10.9 at 256, 13.0 vs 14.9 at 512; bf16 6.1 vs 9.0 at 512
+#   LayerNorm + q/k/v + append  fp32 11.8 at 256 rows, 32.5 vs 40.4 at 1024, 47.2 vs 46.4 at 1536
+#                               (torch without the append); bf16 22.1 vs 33.4 at 1024
+#   out_proj + residual         fp32 8.6 vs 11.0 at 1024, 12.6 vs 13.0 at 1536; bf16 5.0 vs 8.0 at 1024
+#   LayerNorm + fc1 + GELU      fp32 29.4 vs 31.4 at 768, 39.0 vs 33.6 at 1024; bf16 13.5 vs 14.5
+#                               at 512, 19.4 vs 16.7 at 768
+#   fc2 + residual              fp32 23.7 vs 24.0 at 1024, 34.3 vs 31.9 at 1536; bf16 10.6 vs 11.0
+#                               at 1024, 15.5 vs 12.7 at 1536
 #   LayerNorm + lm_head         fp32 10.7 vs 11.8 at 48, 15.8 vs 11.8 at 64; bf16 9.1 vs 10.4 at 64,
 #                               13.6 vs 11.2 at 96
 FUSED_ROWS = {
-    torch.float32: {"qkv": 512, "out_proj": 512, "fc1": 512, "fc2": 512, "lm_head": 48},
-    torch.bfloat16: {"qkv": 512, "out_proj": 512, "fc1": 512, "fc2": 512, "lm_head": 64},
+    torch.float32: {"qkv": 1024, "out_proj": 1024, "fc1": 768, "fc2": 1024, "lm_head": 48},
+    torch.bfloat16: {"qkv": 1024, "out_proj": 1024, "fc1": 512, "fc2": 1024, "lm_head": 64},
 }
-FUSED_STEP_ROWS = 512  # steps above this run the torch layers (q/k/v and out_proj limits)
+FUSED_STEP_ROWS = 1024  # steps above this run the torch layers throughout
 
 
 def graphs_enabled() -> bool:

@@ -214,12 +214,13 @@ int pa_zero_blocks(void* k_pool, void* v_pool, int pool_dtype, int64_t num_block
                    const int32_t* block_ids, int32_t n_ids, void* stream);
 
 /*
- * Decode-step linear layers of the model around the paged attention (fp32, at most 64 token rows).
- * No reference counterpart as entry points: they replace the torch nn.Linear / nn.LayerNorm /
- * nn.GELU calls of the reference's cached forward (src/model/transformer.py:30-35,
- * src/model/attention.py:46-48,64) on one-token steps and prefill chunks, where a step is a
- * few rows against every weight matrix. A workgroup reads its weight tile once per 16 rows, so
- * they pay off up to 32-512 rows depending on the layer; rows is at most 1024.
+ * Step linear layers of the model around the paged attention (fp32 or bf16). No reference
+ * counterpart as entry points: they replace the torch nn.Linear / nn.LayerNorm / nn.GELU calls of
+ * the reference's cached forward (src/model/transformer.py:30-35, src/model/attention.py:46-48,64)
+ * on one-token steps and prefill chunks, where a step is a few rows against every weight matrix.
+ * Up to a few dozen rows a workgroup reads its weight tile once per 16 rows; above that a tiled
+ * kernel reads it once per 32 rows. They pay off up to 48-1536 rows depending on the layer; rows is
+ * at most 2048.
  *
  * pa_linear_rows: out[m, :] = act(LN(x[m, :]) W^T + bias) + residual[m, :] for m < rows.
  *   dtype (PA_DTYPE_F32 or PA_DTYPE_BF16) is the element type of x, weight, bias, LayerNorm
@@ -247,7 +248,7 @@ int pa_linear_rows(const void* x, int64_t x_stride, int32_t rows, int32_t in_fea
  * out[g, :] = act(LN(x[g * group_rows + r_g, :]) W^T + bias) for g < groups, where r_g =
  * row_index[g] (device int32; a negative value counts from the group's end, as Python indexing
  * does, and the result is clamped into [0, group_rows)). Same dtypes, shapes and alignment as
- * pa_linear_rows; groups is at most 1024. No reference counterpart as an entry point: it computes
+ * pa_linear_rows; groups is at most 2048. No reference counterpart as an entry point: it computes
  * ln_f + lm_head (src/model/transformer.py:176-177) only for the row of each request whose greedy
  * token the executors take (src/serving/continuous_generate.py:145,238), instead of every row
  * of a prefill chunk.
@@ -276,7 +277,7 @@ int pa_linear_select_rows(const void* x, int64_t x_stride, int32_t groups, int32
  * vectors of head_dim, into pool slot slot_mapping[m] of the K and V pools (converted to the pool
  * dtype; slot < 0 or a block outside [0, num_blocks) skips the row). dtype is the element type of
  * x, the weights, biases, LayerNorm parameters and q_out (as pa_linear_rows). Replaces
- * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 1024 and
+ * src/model/attention.py:46-56 (q/k/v projections, then append_batch) for rows <= 2048 and
  * d_model in {128, 256, 512, 1024, 2048}.
  */
 int pa_qkv_append(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,

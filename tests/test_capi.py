@@ -93,8 +93,8 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     F32, BF16 = _lib.PA_DTYPE_F32, _lib.PA_DTYPE_BF16
     lin = lib.pa_linear_rows
     # more than 1024 rows
-    assert lin(A, 512, 1025, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None, 0, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert b"rows must be in [0, 1024]" in lib.pa_last_error_message()
+    assert lin(A, 512, 2049, 512, A, None, 512, None, None, 0.0, 0, None, 0, A, 512, None, 0, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"rows must be in [0, 2048]" in lib.pa_last_error_message()
     # unknown activation
     assert lin(A, 512, 4, 512, A, None, 512, None, None, 0.0, 2, None, 0, A, 512, None, 0, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # unknown element type
@@ -112,12 +112,12 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     assert b"in_features" in lib.pa_last_error_message()
     # no rows: nothing to do
     assert lin(None, 0, 0, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 0, None, 0, BF16, None) == _lib.PA_OK
-    # the row-selecting form: group_rows must be positive, row_index present, at most 1024 groups
+    # the row-selecting form: group_rows must be positive, row_index present, at most 2048 groups
     sel = lib.pa_linear_select_rows
     assert sel(A, 512, 2, 0, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, 1, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"group_rows" in lib.pa_last_error_message()
     assert sel(A, 512, 2, 4, None, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, 1, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert sel(A, 512, 1025, 4, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, 1, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert sel(A, 512, 2049, 4, A, 512, A, None, 512, None, None, 0.0, 0, A, 512, None, 1, F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert sel(A, 96, 2, 4, A, 96, A, None, 32, None, None, 0.0, 0, A, 32, None, 1, F32, None) == _lib.PA_ERR_UNSUPPORTED
     assert sel(None, 0, 0, 4, None, 512, None, None, 512, None, None, 0.0, 0, None, 0, None, 1, F32, None) == _lib.PA_OK
     # greedy-token keys must be 8-byte aligned
@@ -133,9 +133,9 @@ def test_decode_step_layer_entry_points_check_arguments_on_the_host(lib):
     assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 32, 16,
                F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"d_model" in lib.pa_last_error_message()
-    assert qkv(A, 512, 1025, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 64, 16,
+    assert qkv(A, 512, 2049, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 64, 16,
                F32, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert b"rows must be in [0, 1024]" in lib.pa_last_error_message()
+    assert b"rows must be in [0, 2048]" in lib.pa_last_error_message()
     assert qkv(A, 512, 2, 512, None, None, 0.0, A, None, A, None, A, None, A, 512, A, A, 0, 8, A, 8, 64, 16,
                5, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # embedding rows must be whole 16-byte vectors: 4 fp32 or 8 bf16 values

@@ -1,6 +1,6 @@
 """Decode-step linear kernels (pa_linear_rows, pa_qkv_append) against float64 torch on the CPU:
 LayerNorm prologue, bias / GELU / residual epilogues, every supported in_features, ragged
-out_features, 1..1024 rows (1-64 row tiles), and the K/V scatter into fp32 and bf16 pools (bit-exact placement,
+out_features, 1..2048 rows, and the K/V scatter into fp32 and bf16 pools (bit-exact placement,
 skipped slots untouched)."""
 import pytest
 import torch
@@ -26,7 +26,7 @@ def ref_linear(x, lin, ln=None, gelu=False, residual=None):
 
 
 @pytest.mark.parametrize("K", [128, 256, 512, 1024, 2048])
-@pytest.mark.parametrize("M", [1, 3, 16, 17, 40, 64, 200, 1024])
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 40, 64, 200, 1024, 2048])
 def test_linear_rows_shapes(device, K, M):
     torch.manual_seed(K + M)
     N = 300 if K != 512 else 5000  # out_features not a multiple of 16 (partial last tile)
@@ -72,7 +72,7 @@ def test_linear_rows_rejects_bad_shapes(device):
         hip_linear.linear_rows_hip(torch.randn(2, 96, device=device), lin)  # in_features 96 unsupported
     lin = nn.Linear(128, 32).to(device)
     with pytest.raises(ValueError):
-        hip_linear.linear_rows_hip(torch.randn(1025, 128, device=device), lin)  # more than 1024 rows
+        hip_linear.linear_rows_hip(torch.randn(2049, 128, device=device), lin)  # more than 2048 rows
 
 
 class _Attn(nn.Module):
