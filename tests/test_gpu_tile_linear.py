@@ -29,21 +29,24 @@ def test_tiled_linear_fp32(device, K, M, N):
     lin, ln = _layer(device, K, N, K + M + N)
     x = torch.randn(M, K, device=device) * 2 + 0.3
     r = torch.randn(M, N, device=device)
-    use_ln = K <= 512
+    use_ln = K <= 1024  # (fp32 at 1024: the statistics pass reads each row in two halves)
     print(f"tiled fp32 K={K} M={M} N={N} ln={use_ln}", flush=True)
     got = hip_linear.linear_rows_hip(x, lin, ln=ln if use_ln else None, gelu=use_ln, residual=r)
     err = (got.double().cpu() - ref_linear(x, lin, ln if use_ln else None, use_ln, r)).abs().max().item()
     assert err <= 5e-5, err
 
 
-@pytest.mark.parametrize("K", [256, 512, 2048])
+@pytest.mark.parametrize("kernel", ["auto", "tiled"])
+@pytest.mark.parametrize("K", [256, 512, 1024, 2048])
 @pytest.mark.parametrize("M,N", [(20, 512), (64, 2048), (300, 512)])
-def test_tiled_linear_bf16(device, K, M, N):
+def test_tiled_linear_bf16(device, monkeypatch, K, M, N, kernel):
+    if kernel == "tiled":
+        monkeypatch.setenv("PAGED_HIP_LINEAR_KERNEL", "tiled")
     lin, ln = _layer(device, K, N, 50 + K + M, torch.bfloat16)
     x = (torch.randn(M, K, device=device) * 2 + 0.3).to(torch.bfloat16)
     r = torch.randn(M, N, device=device).to(torch.bfloat16)
-    use_ln = K <= 512
-    print(f"tiled bf16 K={K} M={M} N={N} ln={use_ln}", flush=True)
+    use_ln = K <= 1024
+    print(f"tiled bf16 K={K} M={M} N={N} ln={use_ln} kernel={kernel}", flush=True)
     got = hip_linear.linear_rows_hip(x, lin, ln=ln if use_ln else None, gelu=use_ln, residual=r)
     assert_bf16_close(got, ref_linear_bf16(x, lin, ln if use_ln else None, use_ln, r))
 
