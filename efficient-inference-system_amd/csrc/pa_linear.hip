@@ -833,10 +833,20 @@ static bool use_tile_linear(const LinArgs& a) {
   return a.M >= (a.ln_w != nullptr ? 96 : 192);
 }
 
+// Column tile width. 32 columns with a LayerNorm prologue, which each workgroup runs for its
+// rows and then spreads over twice the columns; without one, 32 only when that still gives two
+// workgroups per compute unit. Graph replay on MI355X, d_model 512, 16 / 32 columns, us: LayerNorm
+// + q/k/v fp32 9.1 / 8.4 at 128 rows, 11.5 / 11.9 at 256, 19.2 / 17.2 at 512; LayerNorm + fc1 fp32
+// 14.2 / 11.5 at 256, bf16 10.3 / 7.6; out_proj fp32 3.9 / 5.3 at 256, 5.1 / 5.4 at 512; fc2 (K
+// 2048) fp32 8.1 / 11.9 at 256, 12.3 / 12.9 at 512. PAGED_HIP_TILE_COLUMNS=16 / 32 forces a width.
 static int launch_tile_linear(const LinArgs& a, hipStream_t stream) {
   const int64_t row_tiles = (a.M + kTileRows - 1) / kTileRows;
-  // 32 columns per workgroup when that still gives a workgroup per compute unit, else 16
-  const bool nt2 = a.seg_n % 32 == 0 && (int64_t)a.nseg * (a.seg_n / 32) * row_tiles >= pa_host::device_cu_count();
+  const int64_t tiles32 = (int64_t)a.nseg * (a.seg_n / 32) * row_tiles;
+  bool nt2 = a.seg_n % 32 == 0 && (a.ln_w != nullptr || tiles32 >= 2 * (int64_t)pa_host::device_cu_count());
+  if (const char* env = getenv("PAGED_HIP_TILE_COLUMNS")) {
+    if (strcmp(env, "16") == 0) nt2 = false;
+    if (strcmp(env, "32") == 0) nt2 = a.seg_n % 32 == 0;
+  }
   const int bn = nt2 ? 32 : 16;
   const dim3 grid((unsigned)(a.nseg * (a.seg_n / bn)), (unsigned)row_tiles);
   const dim3 block(kTileWaves * kWave);

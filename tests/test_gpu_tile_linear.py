@@ -63,6 +63,21 @@ def test_tiled_and_16row_kernels_agree(device, monkeypatch, dtype):
     assert (outs["tiled"] - outs["small"]).abs().max().item() <= tol
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ln_on", [True, False])
+def test_tiled_column_widths_agree(device, monkeypatch, dtype, ln_on):
+    """16- and 32-column tiles run the same per-column products in the same order: bit-identical
+    outputs (q/k/v-sized layer with LayerNorm, and without)."""
+    lin, ln = _layer(device, 512, 1536, 79, dtype)
+    x = torch.randn(160, 512, device=device).to(dtype)
+    monkeypatch.setenv("PAGED_HIP_LINEAR_KERNEL", "tiled")
+    outs = {}
+    for cols in ("16", "32"):
+        monkeypatch.setenv("PAGED_HIP_TILE_COLUMNS", cols)
+        outs[cols] = hip_linear.linear_rows_hip(x, lin, ln=ln if ln_on else None, gelu=ln_on)
+    assert torch.equal(outs["16"], outs["32"])
+
+
 def test_tiled_strided_rows_and_copy(device):
     lin, _ = _layer(device, 512, 512, 78)
     big = torch.randn(70, 600, device=device)
