@@ -779,10 +779,6 @@ __global__ __launch_bounds__(kTileWaves * kWave) void tile_linear_kernel(const L
   }
 }
 
-static bool small_linear_k_supported(int32_t K) {
-  return K == 128 || K == 256 || K == 512 || K == 1024 || K == 2048;
-}
-
 #ifndef PA_LIN_FORCE_CW_LOG2
 #define PA_LIN_FORCE_CW_LOG2 0
 #endif
