@@ -21,13 +21,14 @@ import torch
 import torch.nn as nn
 
 from src.kernels import _lib
+from src.kernels.hip_paged_attention import _stream_ptr
 
 MAX_ROWS = 2048  # rows per call accepted by the library
 SUPPORTED_FEATURES = (128, 256, 512, 1024, 2048)
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    return _stream_ptr(device)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:

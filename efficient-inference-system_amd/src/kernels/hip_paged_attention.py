@@ -24,7 +24,15 @@ _workspaces: dict[tuple[int, str], torch.Tensor] = {}
 _cu_counts: dict[int, int] = {}
 
 
+# torch's raw current-stream lookup (one C call, ~0.1 us) where this build of torch has it; the
+# public torch.cuda.current_stream(device).cuda_stream builds a Stream object per call (~2 us).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(device: torch.device) -> int:
+    """The current HIP stream of `device` as a raw pointer."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

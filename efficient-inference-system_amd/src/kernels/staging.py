@@ -20,6 +20,8 @@ import weakref
 import numpy as np
 import torch
 
+from src.kernels.hip_paged_attention import _stream_ptr
+
 _SLOT_BYTES = 256 * 1024
 _SLOTS = 32
 _H2D = 1  # hipMemcpyHostToDevice
@@ -96,7 +98,7 @@ class _PinnedRing:
             src = torch.from_numpy(arr.view(np.uint8).reshape(-1)).pin_memory()
             dst.view(-1).view(torch.uint8)[:nbytes].copy_(src, non_blocking=True)
             return
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = _stream_ptr(self.device)
         i = self.next
         self.next = (i + 1) % _SLOTS
         ev = self.events[i]
