@@ -25,7 +25,9 @@ struct AttnArgs {
   int32_t num_splits;    // workgroups per work unit along the KV axis, >= 1
   int32_t split_blocks;  // KV blocks per split when num_splits > 1
   float* ws;             // partial (m, l, acc[head_dim]) records of the splits
-  int32_t* counters;     // decode, same-launch merge: per (request, head) arrivals (zero between calls)
+  int32_t* counters;     // same-launch merge: arrival counters (zero between calls); decode per
+                         // (request, head), balanced wide prefill per (request, head, tile)
+  int32_t die_cus;       // balanced wide prefill: compute units per die
 };
 
 // Wave-wide partner exchange on gfx950 without an LDS round trip: v_permlane16_swap /
@@ -54,6 +56,11 @@ __device__ __forceinline__ float sum_xor32(float x) {
 bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size);
 int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len);
 int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream);
+// Balanced launch of the head_dim 128 bf16 wide kernel: its grid (0 when it does not apply) and
+// the bytes of its split records. launch_prefill_wide takes it when a.counters is set.
+int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
+                              int32_t max_pages);
+size_t prefill_balanced_record_bytes(int64_t grid);
 
 // Split-step prefill (32 query rows per workgroup, 8 wavefronts splitting the KV steps; bf16 KV
 // at head_dim 64). Defined in pa_prefill_wide.hip.

@@ -687,10 +687,14 @@ using namespace pa;
 extern "C" size_t pa_prefill_workspace_size(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                                             int32_t max_pages, int32_t split_blocks) {
   if (batch <= 0 || num_heads <= 0 || query_len <= 0 || !prefill_fast_shape(head_dim, 16)) return 0;
+  if (split_blocks < 0) {
+    const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages);
+    return grid > 0 ? PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid) : 0;
+  }
   const int s = prefill_num_splits(max_pages, split_blocks);
   if (s <= 1) return 0;
   const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);
-  return (size_t)units * s * 16 * (head_dim + 2) * sizeof(float);
+  return PA_PREFILL_COUNTER_BYTES + (size_t)units * s * 16 * (head_dim + 2) * sizeof(float);
 }
 
 extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
@@ -729,8 +733,19 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 
   if (!prefill_fast_shape(head_dim, block_size)) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
   if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
-      use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len))
+      use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len)) {
+    if (split_blocks < 0 && kv_dtype == PA_DTYPE_BF16) {
+      const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages);
+      if (grid > 0) {
+        const size_t need = PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid);
+        if (workspace == nullptr || workspace_bytes < need)
+          PA_FAIL(PA_ERR_WORKSPACE, "prefill workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
+        a.counters = static_cast<int32_t*>(workspace);
+        a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + PA_PREFILL_COUNTER_BYTES);
+      }
+    }
     return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
+  }
   if (split_blocks <= 0 && prefill_split_supported(kv_dtype, head_dim, block_size) &&
       use_split_prefill(batch, num_heads, query_len))
     return launch_prefill_split(a, io_dtype, stream);
@@ -743,7 +758,7 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
       PA_FAIL(PA_ERR_WORKSPACE, "prefill workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
     a.num_splits = nsplit;
     a.split_blocks = split_blocks;
-    a.ws = static_cast<float*>(workspace);
+    a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + PA_PREFILL_COUNTER_BYTES);
   }
   if (units * nsplit > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
   const dim3 grid((unsigned)(units * nsplit));

@@ -141,8 +141,85 @@ constexpr int kWideStages64 = WIDE_NST64;
 // round of workgroups needs the CU slots it holds.
 static bool wide128_pair(int64_t units) { return units <= 2 * (int64_t)pa_host::device_cu_count(); }
 
-template <typename IO, int HD, int NSUB, int NST>
-__global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const AttnArgs a) {
+// Balanced launch (BAL; head_dim 128 bf16 KV, one 32-key sub-tile per step, 2 stages): the grid
+// is the workgroups the compute units hold at once (three per CU), and the KV steps of all tiles are
+// dealt out evenly instead of one workgroup per tile. Die k (workgroups x = k mod 8) takes the
+// (request, head) pairs with head = k mod 8, listed by request, then head; a pair's work is the
+// step count of its last (longest) tile, at least 1. The die's workgroups form gangs of ntiles
+// members (x = 8 (g ntiles + t) + k is member t of gang g); gang g takes the share
+// [lo_g, lo_g+1) of the die's list (its W steps split over the NG gangs in proportion to
+// share_weight, which favours the gangs dispatched first), and member t walks tile t of each
+// pair in that share over the same key steps as its mates, so a pair's tiles still read each KV
+// step at about the same time (from the die's L2). A tile whose steps fall into several
+// gangs' shares is cut into pieces: each leaves an (m, l, O) record (two slots per workgroup: its
+// share's first and last pair; pairs inside a share are never cut), and the piece that arrives
+// last (per-tile arrival counter, reset to zero by that piece) merges them in gang order.
+// Workspace: a.counters holds one arrival counter per (request, head, tile), zero between calls;
+// a.ws the records, slot s of workgroup x at a.ws + (2 x + s) * kWideRecFloats. A wavefront's
+// part is 17 groups of 16 bytes per lane, lane-minor (group j of lane L at float 4 (64 j + L), so
+// each group is one coalesced 1 KB block): group 0 holds m and l, group 1 + 4d + q the
+// accumulators oacc[d][4q .. 4q + 3].
+constexpr int kWideRecGroups = 17;
+// Share weight of the gangs whose workgroups are the s-th to reach their compute units (s = 0, 1, 2
+// at three workgroups per CU). Measured on MI355X with equal shares (8 x 32 heads x 128, chunk
+// 512 over 1.8-3.7k contexts): the first, second and third workgroup of each CU finished at 197,
+// 207 and 218 us (medians), i.e. progressed at relative rates 1.10 : 1.05 : 1.
+__device__ __forceinline__ int share_weight(int s) { return s < 2 ? 22 - s : 20; }
+
+template <int HD>
+constexpr int kWideRecFloats = kWideWaves * kWideRecGroups * kWave * 4;
+static_assert(kWideRecGroups == 1 + 128 / 32 * 16 / 4, "record groups at head_dim 128");
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Groups 0-8 and 9-16 of a record (p: the lane's group 0; groups 1 KB apart), read with the
+// device-scope coherence bit (sc1) that relaxed agent-scope atomic loads use, nine and eight
+// loads in flight, each batch waited for inside its assembly block. (As atomic loads the compiler
+// issues them one at a time, waiting for each: 66 memory round trips per record.)
+__device__ __forceinline__ void load_record_lo(const float* p, f32x4 (&v)[9]) {
+  const float* p4 = p + 4 * 256;
+  const float* p8 = p + 8 * 256;
+  asm volatile(
+      "global_load_dwordx4 %0, %9, off offset:-4096 sc1\n\t"
+      "global_load_dwordx4 %1, %9, off offset:-3072 sc1\n\t"
+      "global_load_dwordx4 %2, %9, off offset:-2048 sc1\n\t"
+      "global_load_dwordx4 %3, %9, off offset:-1024 sc1\n\t"
+      "global_load_dwordx4 %4, %9, off sc1\n\t"
+      "global_load_dwordx4 %5, %9, off offset:1024 sc1\n\t"
+      "global_load_dwordx4 %6, %9, off offset:2048 sc1\n\t"
+      "global_load_dwordx4 %7, %9, off offset:3072 sc1\n\t"
+      "global_load_dwordx4 %8, %10, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+        "=&v"(v[7]), "=&v"(v[8])
+      : "v"(p4), "v"(p8)
+      : "memory");
+}
+// One 16-byte record group store with the device-scope coherence bit (sc1) that relaxed
+// agent-scope atomic stores use; the caller waits for its stores (s_waitcnt vmcnt(0)) before
+// counting itself in.
+__device__ __forceinline__ void store_record_group(float* p, f32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void load_record_hi(const float* p, f32x4 (&v)[8]) {
+  const float* p13 = p + 13 * 256;
+  asm volatile(
+      "global_load_dwordx4 %0, %8, off offset:-4096 sc1\n\t"
+      "global_load_dwordx4 %1, %8, off offset:-3072 sc1\n\t"
+      "global_load_dwordx4 %2, %8, off offset:-2048 sc1\n\t"
+      "global_load_dwordx4 %3, %8, off offset:-1024 sc1\n\t"
+      "global_load_dwordx4 %4, %8, off sc1\n\t"
+      "global_load_dwordx4 %5, %8, off offset:1024 sc1\n\t"
+      "global_load_dwordx4 %6, %8, off offset:2048 sc1\n\t"
+      "global_load_dwordx4 %7, %8, off offset:3072 sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+        "=&v"(v[7])
+      : "v"(p13)
+      : "memory");
+}
+
+template <typename IO, int HD, int NSUB, int NST, bool BAL>
+__device__ __forceinline__ void prefill_wide_body(const AttnArgs& a) {
   constexpr int NW = kWideWaves;
   constexpr int KS = 32 * NSUB;          // keys per step
   constexpr int NBS = KS / 16;           // KV blocks per step
@@ -157,6 +234,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   constexpr int TILE = KS * HD;          // elements per K (or V) tile
 
   static_assert(NST == 2 || NST == 3, "stages");
+  static_assert(!BAL || (HD == 128 && NSUB == 1 && NST == 2), "balanced launch shape");
   // Stage s: K tile at sbuf + 2 * s * TILE, V tile right after it (one array addressed through
   // per-stage pointers takes fewer registers than one array per tile).
   __shared__ __attribute__((aligned(16))) uint16_t sbuf[NST * 2 * TILE];
@@ -173,251 +251,458 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const 
   uint16_t* const sv2 = sbuf + (NST > 2 ? 5 : 1) * TILE;
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
-  int bh, qt;
-  static_assert(sizeof(sbuf) >= (kOrderMax + 1) * sizeof(int), "order scratch");
-  if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(sbuf), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
-  const int h = bh % a.H;
-  const int b = bh / a.H;
-  const int i0 = qt * kWideRows;
-  const int iw = i0 + 32 * w;
-  const int i = iw + c;
-
-  const int L = a.seq_lens[b];
-  const int C = a.cur_lens[b];
-  const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
-  const int last_wg = (i0 + kWideRows - 1) < (a.T - 1) ? (i0 + kWideRows - 1) : (a.T - 1);
-  const int n_wg = valid_keys(L, C, last_wg);  // nondecreasing in the row index
-  int nb = (n_wg + 15) / 16;
-  nb = nb < a.max_pages ? nb : a.max_pages;
-  const int nsteps = (nb + NBS - 1) / NBS;
-  int wsteps = 0;  // steps this wavefront computes (its rows need no keys beyond them)
-  if (iw < a.T) {
-    const int last_w = (iw + 31) < (a.T - 1) ? (iw + 31) : (a.T - 1);
-    wsteps = (valid_keys(L, C, last_w) + KS - 1) / KS;
-    wsteps = wsteps < nsteps ? wsteps : nsteps;
-  }
-
-  // B operand of S^T = K Q^T: q[i][G2*QH + 8s + e] for MFMA s, pre-scaled, rounded to bf16.
-  bf16x8 qb[NQ];
-  {
-    const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
-                   (int64_t)(i < a.T ? i : 0) * a.q_st + G2 * QH;
-    const float qs = i < a.T ? a.scale_log2 : 0.f;
-#pragma unroll
-    for (int s = 0; s < NQ; ++s) {
-      uint32_t wd[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        wd[e] = pack_bf16x2(Elem<IO>::load(qp + 8 * s + 2 * e) * qs, Elem<IO>::load(qp + 8 * s + 2 * e + 1) * qs);
-      qb[s] = __builtin_bit_cast(bf16x8, (u32x4{wd[0], wd[1], wd[2], wd[3]}));
-    }
-  }
-
-  f32x16 oacc[DU];
-#pragma unroll
-  for (int u = 0; u < DU; ++u)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) oacc[u][e] = 0.f;
-  float m = kNegBig, l = 0.f;
-
-  const uint16_t* kpool = static_cast<const uint16_t*>(a.k_pool);
-  const uint16_t* vpool = static_cast<const uint16_t*>(a.v_pool);
-  const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
-  // Page-table entries are int32: one unsigned 32-bit compare checks 0 <= e < num_blocks.
-  const uint32_t nblk = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
-  auto ok_blk = [&](int e) { return (uint32_t)e < nblk; };
-  auto block_base = [&](const uint16_t* pool, int e) {
-    const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
-    return pool + ((int64_t)blk * a.H + h) * (16 * HD);
+  // Steps of 32 * NSUB keys that tile qt of request b walks (the valid keys of its last row).
+  auto tile_steps = [&](int rb, int rqt) {
+    const int last = (rqt * kWideRows + kWideRows - 1) < (a.T - 1) ? (rqt * kWideRows + kWideRows - 1) : (a.T - 1);
+    int nbb = (valid_keys(a.seq_lens[rb], a.cur_lens[rb], last) + 15) / 16;  // nondecreasing in the row
+    nbb = nbb < a.max_pages ? nbb : a.max_pages;
+    return (nbb + NBS - 1) / NBS;
   };
-
-  // LDS tiles hold key rows of HD values unpadded; 16-byte chunk p of key row r holds head_dim
-  // chunk p ^ kswz(r) (K) or p ^ vswz(r) (V). The swizzles make the operand reads below hit all
-  // LDS banks once per pass: the 16 rows of a K read cover 16 distinct chunk positions, and the
-  // 4 key rows x 4 head_dim chunks of a transposing V read cover 16 distinct chunks.
-  auto kswz = [](int r) { return (r / RPB) & (CPR - 1); };
-  auto vswz = [](int r) { return (4 * ((r / RPB) & 3)) & (CPR - 1); };
-
-  // LDS-direct loads (global_load_lds_dwordx4): lane L of a wavefront's instruction writes the 16
-  // bytes at LDS address dst + 16L. Instruction n of wavefront w fills key rows RPI*(w*NDMA + n)
-  // ..+RPI-1 of the step tile, all in one KV block; the lane's source offset in the block is
-  // fixed (kdo / vdo), only the block base changes per step.
-  uint32_t kdo[NDMA], vdo[NDMA];
-#pragma unroll
-  for (int n = 0; n < NDMA; ++n) {
-    const int r = (w * NDMA + n) * RPI + lane / CPR;
-    const int p = lane % CPR;
-    kdo[n] = (uint32_t)((r & 15) * HD + 8 * (p ^ kswz(r)));
-    vdo[n] = (uint32_t)((r & 15) * HD + 8 * (p ^ vswz(r)));
-  }
-  // Page-table entries come from a per-wavefront copy of 64 consecutive entries (lane i holds
-  // entry ptb + i), refreshed when a step's blocks leave it (64 is a multiple of NBS): one
-  // vector load per 64 blocks instead of one scalar load and wait per step.
-  int ptc = 0, ptb = -64;
-  auto issue_loads = [&](int st, int (&ent)[NBS], uint16_t* skx, uint16_t* svx) {
-    const int j0 = NBS * st;
-    if (j0 - ptb >= 64) {
-      ptb = j0;
-      const int idx = j0 + lane;
-      ptc = load_now(pt + (idx < nb ? idx : 0));
+  int bh = 0, qt = 0;
+  // BAL: this workgroup's share [lo, hi) of its die's pair list (see above), the pair it
+  // has reached (request pb, head index hh: head k + 8 hh) and that pair's list position Sb and
+  // work P per head.
+  // The host keeps W below 2^31 / 64, so list positions fit in int.
+  int k = 0, gang = 0, NG = 1, HP = 1, pb = 0, hh = 0, P = 1;
+  int W = 1, lo = 0, hi = 0, Sb = 0;
+  __shared__ int sm_last;                     // BAL: this piece arrived last
+  __shared__ int sP[kWideWaves * kWave];      // BAL: pair work per request
+  __shared__ int sS[kWideWaves * kWave];      // BAL: its prefix sums
+  __shared__ int sCw[kWideWaves * kWave];     // BAL: prefix sums of the gangs' share weights
+  __shared__ int sLo[kWideWaves * kWave];     // BAL: the gangs' shares: [sLo[g], sLo[g + 1])
+  // BAL: the gang whose share holds list position pos (the last g with sLo[g] <= pos).
+  auto gang_of = [&](int pos) {
+    int lg = 0, ug = NG - 1;
+    while (lg < ug) {
+      const int mid = (lg + ug + 1) / 2;
+      if (__builtin_amdgcn_readfirstlane(sLo[mid]) <= pos) lg = mid;
+      else ug = mid - 1;
     }
+    return lg;
+  };
+  if constexpr (!BAL) {
+    static_assert(sizeof(sbuf) >= (kOrderMax + 1) * sizeof(int), "order scratch");
+    if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(sbuf), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
+  } else {
+    k = blockIdx.x % kXcds;
+    const int jx = blockIdx.x / kXcds;
+    gang = jx / ntiles;
+    qt = jx - gang * ntiles;
+    NG = gridDim.x / (kXcds * ntiles);
+    HP = a.H / kXcds;
+    // S[r] = work of requests 0 .. r - 1 per head (at most 255 requests: one thread per entry).
+    if (threadIdx.x < a.B) {
+      const int p = tile_steps(threadIdx.x, ntiles - 1);
+      sP[threadIdx.x] = p > 1 ? p : 1;
+    }
+    __syncthreads();
+    if (threadIdx.x <= a.B) {
+      int s = 0;
+      for (int r = 0; r < (int)threadIdx.x; ++r) s += sP[r];
+      sS[threadIdx.x] = s;
+    }
+    // Share weights: gang g's workgroups are the (g ntiles / die_cus)-th to reach their compute
+    // units (the dispatcher deals a die's workgroups round-robin over its CUs), and the ones that
+    // arrive later progress more slowly (the instruction arbiter favours older wavefronts), so
+    // earlier gangs take proportionally more steps.
+    if (threadIdx.x <= NG) {
+      int s = 0;
+      for (int gg = 0; gg < (int)threadIdx.x; ++gg) s += share_weight(gg * ntiles / a.die_cus);
+      sCw[threadIdx.x] = s;
+    }
+    __syncthreads();
+    W = HP * __builtin_amdgcn_readfirstlane(sS[a.B]);
+    if (threadIdx.x <= NG) sLo[threadIdx.x] = (int)((int64_t)W * sCw[threadIdx.x] / sCw[NG]);
+    __syncthreads();
+    lo = __builtin_amdgcn_readfirstlane(sLo[gang]);
+    hi = __builtin_amdgcn_readfirstlane(sLo[gang + 1]);
+    // First pair of the share: request pb = the last with HP * S[pb] <= lo (S[0] = 0).
+    int lb = 0, ub = a.B - 1;
+    while (lb < ub) {
+      const int mid = (lb + ub + 1) / 2;
+      if (HP * __builtin_amdgcn_readfirstlane(sS[mid]) <= lo) lb = mid;
+      else ub = mid - 1;
+    }
+    pb = lb;
+    Sb = __builtin_amdgcn_readfirstlane(sS[pb]);
+    P = __builtin_amdgcn_readfirstlane(sS[pb + 1]) - Sb;
+    hh = (int)((lo - HP * Sb) / P);
+  }
+  for (bool first = true;; first = false) {
+    int b, h, s_hi = 0x7fffffff;
+    // BAL: the piece's step range starts at s_lo; the tile has np pieces (gangs g0 .. g0 + np - 1),
+    // this one in record slot rec_slot; tile_start: the tile's list position.
+    int s_lo = 0, np = 1, g0 = 0, rec_slot = 0;
+    int tile_start = 0;
+    if constexpr (!BAL) {
+      h = bh % a.H;
+      b = bh / a.H;
+    } else {
+      // Every member walks the share's part of every pair in it, its mates' steps included (their
+      // loads and barriers, without the products past its own tile's steps), so that the gang's
+      // workgroups keep reading the same KV steps at the same time.
+      tile_start = HP * Sb + hh * P;
+      if (lo >= hi || pb >= a.B || tile_start >= hi) break;
+      s_lo = lo > tile_start ? lo - tile_start : 0;
+      s_hi = hi - tile_start < P ? hi - tile_start : P;
+      const int nt = tile_steps(pb, qt);
+      const int ntp = nt > 1 ? nt : 1;
+      np = 0;  // no piece of this tile when the share starts past its steps
+      if (lo < tile_start + ntp) {
+        g0 = gang_of(tile_start);
+        np = gang_of(tile_start + ntp - 1) - g0 + 1;
+        rec_slot = lo >= tile_start ? 0 : 1;
+      }
+      b = pb;
+      h = k + kXcds * hh;
+      if (!first) __syncthreads();  // every wavefront is done with the previous piece's LDS tiles
+    }
+    const int i0 = qt * kWideRows;
+    const int iw = i0 + 32 * w;
+    const int i = iw + c;
+
+    const int L = a.seq_lens[b];
+    const int C = a.cur_lens[b];
+    const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
+    // Blocks the walk loads: up to the last row of the tile (BAL: of the pair's last tile).
+    const int last_row = BAL ? ntiles * kWideRows - 1 : i0 + kWideRows - 1;
+    const int last_wg = last_row < (a.T - 1) ? last_row : (a.T - 1);
+    const int n_wg = valid_keys(L, C, last_wg);  // nondecreasing in the row index
+    int nb = (n_wg + 15) / 16;
+    nb = nb < a.max_pages ? nb : a.max_pages;
+    int nsteps = (nb + NBS - 1) / NBS;
+    nsteps = nsteps < s_hi ? nsteps : s_hi;
+    int wsteps = 0;  // steps this wavefront computes (its rows need no keys beyond them)
+    if (iw < a.T) {
+      const int last_w = (iw + 31) < (a.T - 1) ? (iw + 31) : (a.T - 1);
+      wsteps = (valid_keys(L, C, last_w) + KS - 1) / KS;
+      wsteps = wsteps < nsteps ? wsteps : nsteps;
+    }
+
+    // B operand of S^T = K Q^T: q[i][G2*QH + 8s + e] for MFMA s, pre-scaled, rounded to bf16.
+    bf16x8 qb[NQ];
+    {
+      const IO* qp = static_cast<const IO*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
+                     (int64_t)(i < a.T ? i : 0) * a.q_st + G2 * QH;
+      const float qs = i < a.T ? a.scale_log2 : 0.f;
 #pragma unroll
-    for (int j = 0; j < NBS; ++j) ent[j] = j0 + j < nb ? __builtin_amdgcn_readlane(ptc, j0 - ptb + j) : -1;
+      for (int s = 0; s < NQ; ++s) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          wd[e] = pack_bf16x2(Elem<IO>::load(qp + 8 * s + 2 * e) * qs, Elem<IO>::load(qp + 8 * s + 2 * e + 1) * qs);
+        qb[s] = __builtin_bit_cast(bf16x8, (u32x4{wd[0], wd[1], wd[2], wd[3]}));
+      }
+    }
+
+    f32x16 oacc[DU];
+#pragma unroll
+    for (int u = 0; u < DU; ++u)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) oacc[u][e] = 0.f;
+    float m = kNegBig, l = 0.f;
+
+    const uint16_t* kpool = static_cast<const uint16_t*>(a.k_pool);
+    const uint16_t* vpool = static_cast<const uint16_t*>(a.v_pool);
+    const int32_t* pt = a.page_table + (int64_t)b * a.pt_stride;
+    // Page-table entries are int32: one unsigned 32-bit compare checks 0 <= e < num_blocks.
+    const uint32_t nblk = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
+    auto ok_blk = [&](int e) { return (uint32_t)e < nblk; };
+    auto block_base = [&](const uint16_t* pool, int e) {
+      const int blk = ok_blk(e) ? e : 0;  // masked in the softmax when invalid
+      return pool + ((int64_t)blk * a.H + h) * (16 * HD);
+    };
+
+    // LDS tiles hold key rows of HD values unpadded; 16-byte chunk p of key row r holds head_dim
+    // chunk p ^ kswz(r) (K) or p ^ vswz(r) (V). The swizzles make the operand reads below hit all
+    // LDS banks once per pass: the 16 rows of a K read cover 16 distinct chunk positions, and the
+    // 4 key rows x 4 head_dim chunks of a transposing V read cover 16 distinct chunks.
+    auto kswz = [](int r) { return (r / RPB) & (CPR - 1); };
+    auto vswz = [](int r) { return (4 * ((r / RPB) & 3)) & (CPR - 1); };
+
+    // LDS-direct loads (global_load_lds_dwordx4): lane L of a wavefront's instruction writes the 16
+    // bytes at LDS address dst + 16L. Instruction n of wavefront w fills key rows RPI*(w*NDMA + n)
+    // ..+RPI-1 of the step tile, all in one KV block; the lane's source offset in the block is
+    // fixed (kdo / vdo), only the block base changes per step.
+    uint32_t kdo[NDMA], vdo[NDMA];
 #pragma unroll
     for (int n = 0; n < NDMA; ++n) {
-      const int r0 = (w * NDMA + n) * RPI;
-      const int e = ent[r0 >> 4];
-      lds_direct_load16(block_base(kpool, e), 2 * kdo[n], skx + r0 * HD);
-      lds_direct_load16(block_base(vpool, e), 2 * vdo[n], svx + r0 * HD);
+      const int r = (w * NDMA + n) * RPI + lane / CPR;
+      const int p = lane % CPR;
+      kdo[n] = (uint32_t)((r & 15) * HD + 8 * (p ^ kswz(r)));
+      vdo[n] = (uint32_t)((r & 15) * HD + 8 * (p ^ vswz(r)));
     }
-  };
-
-  // Per-lane LDS element offsets of the operand reads (fixed for the whole walk).
-  //   K (A of S^T = K Q^T, MFMA s, sub-tile u): key row c + 32u, head_dim chunk G2*CPR/2 + s.
-  //   V (A of O^T += V^T P^T, tile d): ds_read_b64_tr_b16 gives lane j of each 16-lane group
-  //   element r = the value at row r' = r, column j of the 4 x 16 block its group addresses
-  //   (lanes 4r' + a' supply the addresses of row r', columns 4a'..4a'+3). Lane (G2, c) reads,
-  //   for 4 keys K0 + r (r = (c mod 16) / 4), head_dim 32d + 16(c / 16) + 4(c mod 4): it then
-  //   holds V[K0 + r][32d + c], r = 0..3 — four k slots of row c of V^T.
-  const int kx = kswz(c);
-  const int vr4 = (c & 15) >> 2;
-  const int vx = vswz(4 * G2 + vr4);
-  auto v_off = [&](int d) {
-    const int hd = 32 * d + 16 * (c >> 4) + 4 * (c & 3);
-    return (4 * G2 + vr4) * HD + 8 * ((hd >> 3) ^ vx) + (hd & 4);
-  };
-
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  auto compute = [&](const uint16_t* skx, const uint16_t* svx, int st, const int (&ent)[NBS]) {
-    // ---- S^T = K Q^T for each 32-key sub-tile ------------------------------------------------
-    f32x16 sacc[NSUB];
-#pragma unroll
-    for (int u = 0; u < NSUB; ++u)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[u][e] = 0.f;
-#pragma unroll
-    for (int s = 0; s < NQ; ++s)
-#pragma unroll
-      for (int u = 0; u < NSUB; ++u) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(skx + (c + 32 * u) * HD + 8 * ((G2 * (CPR / 2) + s) ^ kx));
-        sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s], sacc[u], 0, 0, 0);
+    // Page-table entries come from a per-wavefront copy of 64 consecutive entries (lane i holds
+    // entry ptb + i), refreshed when a step's blocks leave it (64 is a multiple of NBS): one
+    // vector load per 64 blocks instead of one scalar load and wait per step.
+    int ptc = 0, ptb = -64;
+    auto issue_loads = [&](int st, int (&ent)[NBS], uint16_t* skx, uint16_t* svx) {
+      const int j0 = NBS * st;
+      if (j0 - ptb >= 64) {
+        ptb = j0;
+        const int idx = j0 + lane;
+        ptc = load_now(pt + (idx < nb ? idx : 0));
       }
-    // ---- online softmax (sub-tile u, keys 32u + 8j + 4*G2 + r of this step), in place --------
-    bool all_ok = true;
 #pragma unroll
-    for (int j = 0; j < NBS; ++j) all_ok = all_ok && ok_blk(ent[j]);
-    // Interior steps (every block valid, every key below every row's limit) need no mask.
-    const bool full = all_ok && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
-    if (!full) {
-      const int t0 = st * KS + 4 * G2;
+      for (int j = 0; j < NBS; ++j) ent[j] = j0 + j < nb ? __builtin_amdgcn_readlane(ptc, j0 - ptb + j) : -1;
+#pragma unroll
+      for (int n = 0; n < NDMA; ++n) {
+        const int r0 = (w * NDMA + n) * RPI;
+        const int e = ent[r0 >> 4];
+        lds_direct_load16(block_base(kpool, e), 2 * kdo[n], skx + r0 * HD);
+        lds_direct_load16(block_base(vpool, e), 2 * vdo[n], svx + r0 * HD);
+      }
+    };
+
+    // Per-lane LDS element offsets of the operand reads (fixed for the whole walk).
+    //   K (A of S^T = K Q^T, MFMA s, sub-tile u): key row c + 32u, head_dim chunk G2*CPR/2 + s.
+    //   V (A of O^T += V^T P^T, tile d): ds_read_b64_tr_b16 gives lane j of each 16-lane group
+    //   element r = the value at row r' = r, column j of the 4 x 16 block its group addresses
+    //   (lanes 4r' + a' supply the addresses of row r', columns 4a'..4a'+3). Lane (G2, c) reads,
+    //   for 4 keys K0 + r (r = (c mod 16) / 4), head_dim 32d + 16(c / 16) + 4(c mod 4): it then
+    //   holds V[K0 + r][32d + c], r = 0..3 — four k slots of row c of V^T.
+    const int kx = kswz(c);
+    const int vr4 = (c & 15) >> 2;
+    const int vx = vswz(4 * G2 + vr4);
+    auto v_off = [&](int d) {
+      const int hd = 32 * d + 16 * (c >> 4) + 4 * (c & 3);
+      return (4 * G2 + vr4) * HD + 8 * ((hd >> 3) ^ vx) + (hd & 4);
+    };
+
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    auto compute = [&](const uint16_t* skx, const uint16_t* svx, int st, const int (&ent)[NBS]) {
+      // ---- S^T = K Q^T for each 32-key sub-tile ------------------------------------------------
+      f32x16 sacc[NSUB];
 #pragma unroll
       for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool okb = ok_blk(ent[2 * u + (j >> 1)]);
+        for (int e = 0; e < 16; ++e) sacc[u][e] = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = t0 + 32 * u + 8 * j + r;
-            sacc[u][4 * j + r] = (okb && t < n_c) ? sacc[u][4 * j + r] : -INFINITY;
+      for (int s = 0; s < NQ; ++s)
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) {
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(skx + (c + 32 * u) * HD + 8 * ((G2 * (CPR / 2) + s) ^ kx));
+          sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qb[s], sacc[u], 0, 0, 0);
+        }
+      // ---- online softmax (sub-tile u, keys 32u + 8j + 4*G2 + r of this step), in place --------
+      bool all_ok = true;
+#pragma unroll
+      for (int j = 0; j < NBS; ++j) all_ok = all_ok && ok_blk(ent[j]);
+      // Interior steps (every block valid, every key below every row's limit) need no mask.
+      const bool full = all_ok && __builtin_amdgcn_ballot_w64(n_c < (st + 1) * KS) == 0;
+      if (!full) {
+        const int t0 = st * KS + 4 * G2;
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool okb = ok_blk(ent[2 * u + (j >> 1)]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = t0 + 32 * u + 8 * j + r;
+              sacc[u][4 * j + r] = (okb && t < n_c) ? sacc[u][4 * j + r] : -INFINITY;
+            }
+          }
+      }
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sacc[u][e]);
+      mloc = max_xor32(mloc);
+      const bool grow = mloc > m + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float mnew = grow ? mloc : m;
+        const float alpha = fast_exp2(m - mnew);
+        l *= alpha;
+#pragma unroll
+        for (int u = 0; u < DU; ++u) oacc[u] *= alpha;
+        m = mnew;
+      }
+      float ps = 0.f;
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          sacc[u][e] = fast_exp2(sacc[u][e] - m);
+          ps += sacc[u][e];
+        }
+      l += sum_xor32(ps);
+      // ---- O^T += V^T P^T: MFMA (u2, mm, d) contracts keys 32u2 + 16mm + 8jj + 4*G2 + r at slot
+      // (G2, 4jj + r), i.e. the lane's registers 8mm + 4jj + r ----------------------------------
+      // The PV MFMAs run at raised wavefront priority, so a wavefront that reaches them issues
+      // ahead of co-resident wavefronts still in their softmax and the matrix pipe stays fed (the
+      // same around the QK^T MFMAs costs 20 registers and a wavefront per SIMD).
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int u2 = 0; u2 < NSUB; ++u2)
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+          uint32_t pw[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(sacc[u2][8 * mm + 2 * q], sacc[u2][8 * mm + 2 * q + 1]);
+          const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
+#pragma unroll
+          for (int d = 0; d < DU; ++d) {
+            const uint16_t* vp = svx + v_off(d) + (32 * u2 + 16 * mm) * HD;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(vp));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(vp + 8 * HD));
+            const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[d], 0, 0, 0);
           }
         }
-    }
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < NSUB; ++u)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sacc[u][e]);
-    mloc = max_xor32(mloc);
-    const bool grow = mloc > m + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float mnew = grow ? mloc : m;
-      const float alpha = fast_exp2(m - mnew);
-      l *= alpha;
-#pragma unroll
-      for (int u = 0; u < DU; ++u) oacc[u] *= alpha;
-      m = mnew;
-    }
-    float ps = 0.f;
-#pragma unroll
-    for (int u = 0; u < NSUB; ++u)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        sacc[u][e] = fast_exp2(sacc[u][e] - m);
-        ps += sacc[u][e];
-      }
-    l += sum_xor32(ps);
-    // ---- O^T += V^T P^T: MFMA (u2, mm, d) contracts keys 32u2 + 16mm + 8jj + 4*G2 + r at slot
-    // (G2, 4jj + r), i.e. the lane's registers 8mm + 4jj + r ----------------------------------
-    // The PV MFMAs run at raised wavefront priority, so a wavefront that reaches them issues
-    // ahead of co-resident wavefronts still in their softmax and the matrix pipe stays fed (the
-    // same around the QK^T MFMAs costs 20 registers and a wavefront per SIMD).
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int u2 = 0; u2 < NSUB; ++u2)
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        uint32_t pw[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) pw[q] = pack_bf16x2(sacc[u2][8 * mm + 2 * q], sacc[u2][8 * mm + 2 * q + 1]);
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[0], pw[1], pw[2], pw[3]}));
-#pragma unroll
-        for (int d = 0; d < DU; ++d) {
-          const uint16_t* vp = svx + v_off(d) + (32 * u2 + 16 * mm) * HD;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(vp));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(vp + 8 * HD));
-          const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[d], 0, 0, 0);
+      __builtin_amdgcn_s_setprio(0);
+    };
+
+    // NST-stage pipeline: the loads of step st + NST - 1 are issued once every wavefront is past
+    // step st - 1 (whose stage they reuse), NST - 1 steps ahead of their use. Before computing step
+    // st a wavefront waits for its own loads of step st (vmcnt: those of the later steps may still
+    // be in flight) and the barrier makes every wavefront's loads of step st visible.
+    if (s_lo < nsteps) {
+      int e0[NBS], e1[NBS], e2[NBS];  // page-table entries of the steps in stages 0, 1, 2
+      issue_loads(s_lo, e0, sk0, sv0);
+      if (NST > 2 && s_lo + 1 < nsteps) issue_loads(s_lo + 1, e1, sk1, sv1);
+      auto iteration = [&](int st, const int (&ec)[NBS], int (&en)[NBS], const uint16_t* skc, const uint16_t* svc,
+                           uint16_t* skn, uint16_t* svn) {
+        if (NST > 2 && st + 1 < nsteps) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NDMA));  // vmcnt(2 * NDMA)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                                           // vmcnt(0)
+        __syncthreads();
+        // The next stage's loads are issued at raised priority too, so they start right after
+        // the barrier.
+        __builtin_amdgcn_s_setprio(1);
+        if (st + NST - 1 < nsteps) issue_loads(st + NST - 1, en, skn, svn);
+        __builtin_amdgcn_s_setprio(0);
+        if (st < wsteps) compute(skc, svc, st, ec);
+      };
+      if constexpr (NST == 3) {
+        for (int st = s_lo; st < nsteps; st += 3) {
+          iteration(st, e0, e2, sk0, sv0, sk2, sv2);
+          if (st + 1 < nsteps) iteration(st + 1, e1, e0, sk1, sv1, sk0, sv0);
+          if (st + 2 < nsteps) iteration(st + 2, e2, e1, sk2, sv2, sk1, sv1);
+        }
+      } else {
+        for (int st = s_lo; st < nsteps; st += 2) {
+          iteration(st, e0, e1, sk0, sv0, sk1, sv1);
+          if (st + 1 < nsteps) iteration(st + 1, e1, e0, sk1, sv1, sk0, sv0);
         }
       }
-    __builtin_amdgcn_s_setprio(0);
-  };
+    }
 
-  // NST-stage pipeline: the loads of step st + NST - 1 are issued once every wavefront is past
-  // step st - 1 (whose stage they reuse), NST - 1 steps ahead of their use. Before computing step
-  // st a wavefront waits for its own loads of step st (vmcnt: those of the later steps may still
-  // be in flight) and the barrier makes every wavefront's loads of step st visible.
-  if (nsteps > 0) {
-    int e0[NBS], e1[NBS], e2[NBS];  // page-table entries of the steps in stages 0, 1, 2
-    issue_loads(0, e0, sk0, sv0);
-    if (NST > 2 && nsteps > 1) issue_loads(1, e1, sk1, sv1);
-    auto iteration = [&](int st, const int (&ec)[NBS], int (&en)[NBS], const uint16_t* skc, const uint16_t* svc,
-                         uint16_t* skn, uint16_t* svn) {
-      if (NST > 2 && st + 1 < nsteps) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NDMA));  // vmcnt(2 * NDMA)
-      else __builtin_amdgcn_s_waitcnt(0x0F70);                                           // vmcnt(0)
-      __syncthreads();
-      // The next stage's loads are issued at raised priority too, so they start right after
-      // the barrier.
-      __builtin_amdgcn_s_setprio(1);
-      if (st + NST - 1 < nsteps) issue_loads(st + NST - 1, en, skn, svn);
-      __builtin_amdgcn_s_setprio(0);
-      if (st < wsteps) compute(skc, svc, st, ec);
-    };
-    if constexpr (NST == 3) {
-      for (int st = 0; st < nsteps; st += 3) {
-        iteration(st, e0, e2, sk0, sv0, sk2, sv2);
-        if (st + 1 < nsteps) iteration(st + 1, e1, e0, sk1, sv1, sk0, sv0);
-        if (st + 2 < nsteps) iteration(st + 2, e2, e1, sk2, sv2, sk1, sv1);
-      }
-    } else {
-      for (int st = 0; st < nsteps; st += 2) {
-        iteration(st, e0, e1, sk0, sv0, sk1, sv1);
-        if (st + 1 < nsteps) iteration(st + 1, e1, e0, sk1, sv1, sk0, sv0);
+    bool store = true;
+    if constexpr (BAL) {
+      if (np == 0) {
+        store = false;
+      } else if (np > 1) {
+        // Cut tile, pieces in gangs g0 .. g0 + np - 1. A piece writes its record (device-scope
+        // stores), waits for them and counts itself in; the piece that arrives last resets the
+        // counter and merges the pieces in gang order. Gang g0's piece ends its share, so it
+        // usually arrives last: it first looks whether all the others have arrived, and then
+        // writes no record. Merging starts from gang g0's state, taken from the registers when this
+        // is gang g0 (the values its record would hold), so the result does not depend on which
+        // piece arrives last.
+        int32_t* cnt = a.counters + ((int64_t)b * a.H + h) * ntiles + qt;
+        constexpr int WREC = kWideRecGroups * kWave * 4;  // a wavefront's floats in a record
+        bool last = false;
+        if (gang == g0) {
+          if (threadIdx.x == 0) sm_last = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
+          __syncthreads();
+          last = __builtin_amdgcn_readfirstlane(sm_last);
+        }
+        if (!last) {
+          float* rp = a.ws + ((int64_t)blockIdx.x * 2 + rec_slot) * kWideRecFloats<HD> + w * WREC + 4 * lane;
+          store_record_group(rp, f32x4{m, l, 0.f, 0.f});
+#pragma unroll
+          for (int d = 0; d < DU; ++d)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+              store_record_group(rp + (1 + 4 * d + q4) * 4 * kWave,
+                                 f32x4{oacc[d][4 * q4], oacc[d][4 * q4 + 1], oacc[d][4 * q4 + 2], oacc[d][4 * q4 + 3]});
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();
+          if (threadIdx.x == 0)
+            sm_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
+          __syncthreads();
+          last = __builtin_amdgcn_readfirstlane(sm_last);
+        }
+        store = last;
+        if (last) {
+          if (threadIdx.x == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          // Gang gg's record is in its slot 0, except gang g0's when its share starts before the
+          // tile (the tile is then its share's last pair: slot 1).
+          if (gang != g0) {
+            m = kNegBig;
+            l = 0.f;
+          }
+          for (int gg = gang == g0 ? g0 + 1 : g0; gg < g0 + np; ++gg) {
+            const int slot = __builtin_amdgcn_readfirstlane(sLo[gg]) >= tile_start ? 0 : 1;
+            const int64_t x = (int64_t)kXcds * ((int64_t)gg * ntiles + qt) + k;
+            const float* rq = a.ws + (x * 2 + slot) * kWideRecFloats<HD> + w * WREC + 4 * lane;
+            f32x4 lo[9];
+            load_record_lo(rq, lo);
+            const float mr = lo[0][0], lr = lo[0][1];
+            const float mn = fmaxf(m, mr);
+            const float fa = gg == g0 ? 0.f : fast_exp2(m - mn), fr = fast_exp2(mr - mn);
+            l = l * fa + lr * fr;
+            m = mn;
+#pragma unroll
+            for (int gi = 1; gi < 9; ++gi)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
+                oacc[d][r] = oacc[d][r] * fa + lo[gi][e] * fr;
+              }
+            f32x4 hi[8];
+            load_record_hi(rq, hi);
+#pragma unroll
+            for (int gi = 9; gi < 17; ++gi)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
+                oacc[d][r] = oacc[d][r] * fa + hi[gi - 9][e] * fr;
+              }
+          }
+        }
       }
     }
-  }
 
-  // ---- write: lane holds O^T rows 8j + 4*G2 + r (head_dim 32d + row) of query column c -------
-  if (i >= a.T) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_st;
+    // ---- write: lane holds O^T rows 8j + 4*G2 + r (head_dim 32d + row) of query column c -------
+    if (store && i < a.T) {
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_st;
 #pragma unroll
-  for (int d = 0; d < DU; ++d)
+      for (int d = 0; d < DU; ++d)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Elem<IO>::store(op + 32 * d + 8 * j + 4 * G2 + r, oacc[d][4 * j + r] * inv);
+          for (int r = 0; r < 4; ++r) Elem<IO>::store(op + 32 * d + 8 * j + 4 * G2 + r, oacc[d][4 * j + r] * inv);
+    }
+    if constexpr (!BAL) {
+      break;
+    } else {
+      if (++hh == HP) {
+        hh = 0;
+        if (++pb < a.B) {
+          Sb = __builtin_amdgcn_readfirstlane(sS[pb]);
+          P = __builtin_amdgcn_readfirstlane(sS[pb + 1]) - Sb;
+        }
+      }
+    }
+  }  // pieces
+}
+
+template <typename IO, int HD, int NSUB, int NST>
+__global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const AttnArgs a) {
+  prefill_wide_body<IO, HD, NSUB, NST, false>(a);
+}
+
+// The balanced launch needs three workgroups per compute unit (its grid is the slots the CUs
+// hold at once): at most 168 registers per lane.
+template <typename IO>
+__global__ __launch_bounds__(kWideWaves * kWave) __attribute__((amdgpu_waves_per_eu(3)))
+void prefill_balanced_kernel(const AttnArgs a) {
+  prefill_wide_body<IO, 128, 1, 2, true>(a);
 }
 
 // fp32 KV: the same workgroup layout, LDS staging and online softmax, on v_mfma_f32_32x32x2_f32
@@ -980,10 +1265,63 @@ int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len) 
   return (int64_t)batch * num_heads * ((query_len + kWideRows - 1) / kWideRows);
 }
 
+// Workgroups of the balanced kernel one compute unit holds at once (the smaller of its two
+// output types), per device.
+static int balanced_slots_per_cu() {
+  constexpr int kMaxDevices = 64;
+  static int cached[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (cached[dev] == 0) {
+    int nf = 0, nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_balanced_kernel<float>,
+                                                     kWideWaves * kWave, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_balanced_kernel<uint16_t>,
+                                                     kWideWaves * kWave, 0) != hipSuccess)
+      nf = nb = 0;
+    cached[dev] = (nf < nb ? nf : nb) > 0 ? (nf < nb ? nf : nb) : -1;
+  }
+  return cached[dev] > 0 ? cached[dev] : 0;
+}
+
+int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
+                              int32_t max_pages) {
+  if (head_dim != 128 || batch < 1 || batch > 255 || num_heads < kXcds || num_heads % kXcds != 0 ||
+      query_len < 1 || max_pages < 0)
+    return 0;
+  const int64_t ntiles = (query_len + kWideRows - 1) / kWideRows;
+  const int64_t units = (int64_t)batch * num_heads * ntiles;
+  if (wide128_pair(units) || units * (int64_t)sizeof(int32_t) > (int64_t)PA_PREFILL_COUNTER_BYTES) return 0;
+  const int64_t gangs = (int64_t)balanced_slots_per_cu() * pa_host::device_cu_count() / (kXcds * ntiles);
+  if (gangs < 1) return 0;
+  // The kernel's list positions are int: a die's work W (steps of at most max_pages / 2 + 1 per
+  // pair, at least 1) stays below 2^31 / 64; its share table holds gangs + 1 entries.
+  const int64_t w = (int64_t)(num_heads / kXcds) * batch * ((int64_t)max_pages / 2 + 1);
+  if (w >= (0x7fffffffLL >> 6) || gangs + 1 > kWideWaves * kWave) return 0;
+  return gangs * kXcds * ntiles;
+}
+
+size_t prefill_balanced_record_bytes(int64_t grid) {
+  return (size_t)grid * 2 * kWideRecFloats<128> * sizeof(float);
+}
+
 int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream) {
   const int64_t units = prefill_wide_units(a.B, a.H, a.T);
   if (units > 0x7fffffffLL) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "grid too large");
-  const dim3 grid((unsigned)units), block(kWideWaves * kWave);
+  const dim3 block(kWideWaves * kWave);
+  if (a.counters != nullptr) {
+    // Balanced launch: the caller checked prefill_balanced_grid > 0 and sized the workspace.
+    const int64_t g = prefill_balanced_grid(a.B, a.H, a.T, a.head_dim, a.max_pages);
+    if (g <= 0 || kv_dtype != PA_DTYPE_BF16) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "balanced prefill does not apply");
+    const dim3 grid((unsigned)g);
+    AttnArgs ab = a;
+    ab.die_cus = pa_host::device_cu_count() / kXcds > 0 ? pa_host::device_cu_count() / kXcds : 1;
+    if (io_dtype == PA_DTYPE_F32) prefill_balanced_kernel<float><<<grid, block, 0, stream>>>(ab);
+    else prefill_balanced_kernel<uint16_t><<<grid, block, 0, stream>>>(ab);
+    PA_CHECK_LAUNCH("balanced wide prefill kernel");
+    return PA_OK;
+  }
+  const dim3 grid((unsigned)units);
   if (kv_dtype == PA_DTYPE_F32) {
     if (io_dtype == PA_DTYPE_F32) {
       if (a.head_dim == 64) prefill_wide_f32_kernel<float, 64><<<grid, block, 0, stream>>>(a);

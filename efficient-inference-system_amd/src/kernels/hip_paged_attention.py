@@ -89,6 +89,11 @@ def default_split_blocks(batch: int, num_heads: int, max_pages: int, device: tor
     return 0 if blocks >= max_pages else blocks
 
 
+# split_blocks value asking pa_prefill for its balanced launch (bf16 KV, head_dim 128, more than
+# two (request, head, 128-row tile) units per compute unit; other calls run unsplit).
+PREFILL_BALANCED = -1
+
+
 def default_prefill_split_blocks(batch: int, num_heads: int, query_len: int, max_pages: int,
                                  device: torch.device) -> int:
     """KV blocks per prefill split-K workgroup. Always 0: measured on MI355X, the second (merge)
@@ -181,7 +186,8 @@ def paged_attention_prefill_hip(
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Chunked causal prefill attention for q [B, H, T, Hd]; returns a tensor shaped like q.
-    split_blocks: KV blocks per split-K workgroup (0: none; None: default_prefill_split_blocks)."""
+    split_blocks: KV blocks per split-K workgroup (0: none; PREFILL_BALANCED: the balanced launch
+    where it applies; None: default_prefill_split_blocks)."""
     _require_gpu("paged_attention_prefill_hip", q, k_pool, v_pool, page_table, seq_lens, current_lengths)
     _check_pool("paged_attention_prefill_hip", k_pool, v_pool)
     B, H, T, Hd = q.shape

@@ -128,8 +128,14 @@ int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * MFMA with fp32 accumulation (q and the softmax weights are rounded to bf16 for the products).
  * Work is one workgroup per (request, head, 16-row query tile); with split_blocks > 0 each tile's
  * KV blocks are also cut into ranges of split_blocks blocks, one workgroup each, whose partial
- * results a second kernel merges through a workspace of pa_prefill_workspace_size() bytes (no
- * initialisation needed). split_blocks <= 0 means no split and no workspace.
+ * results a second kernel merges through a workspace of pa_prefill_workspace_size() bytes.
+ * split_blocks == 0 means no split and no workspace. split_blocks < 0 (PA_PREFILL_BALANCED) asks
+ * for the balanced launch where it applies (bf16 KV, head_dim 128, more than two (request, head,
+ * 128-row tile) units per compute unit, num_heads a multiple of 8, batch <= 255): one workgroup
+ * per slot the compute units hold at once, the tiles' KV steps dealt out evenly among them, and
+ * a tile cut between workgroups merged by the one that finishes it last, in the same launch;
+ * other calls run as with 0. Every prefill workspace starts with PA_PREFILL_COUNTER_BYTES of
+ * arrival counters that must be zero before its first use; every call leaves them zero.
  */
 int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
@@ -141,10 +147,14 @@ int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_
                int32_t block_size, float scale, int32_t split_blocks,
                void* workspace, size_t workspace_bytes, void* stream);
 
-/* Bytes of workspace pa_prefill needs for these sizes (0 when no split applies). No reference
- * counterpart: the Triton prefill path has no split-K. */
+/* Bytes of workspace pa_prefill needs for these sizes (0 when neither a split nor the balanced
+ * launch applies; the balanced launch's size is given whatever the KV dtype, and fp32 KV calls
+ * leave that workspace unused). No reference counterpart: the Triton prefill path has no split-K. */
 size_t pa_prefill_workspace_size(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                                  int32_t max_pages, int32_t split_blocks);
+
+#define PA_PREFILL_BALANCED (-1)
+#define PA_PREFILL_COUNTER_BYTES ((size_t)64 << 10)
 
 /*
  * KV append / scatter: writes k_new[b, :, j, :] and v_new[b, :, j, :] into pool slot

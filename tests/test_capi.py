@@ -62,10 +62,14 @@ def test_host_only_entry_points(lib):
     assert lib.pa_decode_workspace_size(8, 8, 64, 64, 16) == (256 << 10) + 8 * 8 * 4 * (64 + 2) * 4
     assert lib.pa_decode_workspace_size(8, 8, 64, 16, 16) == 0
     # prefill: 4 requests x 8 heads x 16 tiles of 16 rows, 58 pages in splits of 16 -> 4 splits
+    # (arrival counters first: a fixed 64 KiB region; then the records)
     assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 58, 0) == 0
-    assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 58, 16) == 4 * 8 * 16 * 4 * 16 * (64 + 2) * 4
+    assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 58, 16) == (64 << 10) + 4 * 8 * 16 * 4 * 16 * (64 + 2) * 4
     assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 16, 16) == 0
     assert lib.pa_prefill_workspace_size(4, 8, 256, 96, 58, 16) == 0  # no tuned kernel: no split
+    # the balanced launch applies to head_dim 128 only (and needs a device to size its grid)
+    assert lib.pa_prefill_workspace_size(8, 32, 512, 64, 300, -1) == 0
+    assert lib.pa_prefill_workspace_size(8, 12, 512, 128, 300, -1) == 0  # heads not a multiple of 8
 
 
 def test_argument_errors_are_reported_without_a_device(lib):

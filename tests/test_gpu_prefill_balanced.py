@@ -1,0 +1,124 @@
+"""The balanced launch of the wide bf16 prefill kernel (head_dim 128; split_blocks < 0): the
+tiles' KV steps dealt out evenly over the workgroups the GPU holds at once, tiles cut between
+workgroups merged in the same launch by the piece that finishes last. Checked against the oracle
+on the same bf16 KV values (2e-2, the bf16 tolerance) and against the unbalanced wide kernel,
+on repeated calls (the arrival counters must be left at zero) and ragged shapes whose tiles are
+cut into many pieces."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from src import workloads
+from src.kernels import _lib
+from src.kernels.hip_paged_attention import PREFILL_BALANCED, cu_count, paged_attention_prefill_hip
+from test_gpu_prefill import _check_large_request, make_prefill, max_err
+
+pytestmark = pytest.mark.gpu
+NTHREADS = min(16, os.cpu_count() or 1)
+
+
+def _prefill(b, q=None, page_table=None, **kw):
+    q = b.q if q is None else q
+    pt = b.page_table if page_table is None else page_table
+    return paged_attention_prefill_hip(q, b.k_pool, b.v_pool, pt, b.seq_lens_t, b.cur_lens_t, **kw)
+
+
+def _balanced_applies(b):
+    B, H, T, Hd = b.q.shape
+    return _lib.load().pa_prefill_workspace_size(B, H, T, Hd, b.page_table.shape[1], PREFILL_BALANCED) > 0
+
+
+def test_balanced_large_prefill(device):
+    """The large-prefill workload (8 x 32 heads x 128, chunk 512 over 1-4k contexts): three calls
+    in a row agree with each other up to the pieces' summation order and with the unbalanced
+    launch; requests 0 (shortest) and 6 (longest, its tiles cut between workgroups) against the
+    oracle on every head."""
+    b = workloads.large_prefill(seed=0, device=device)
+    assert _balanced_applies(b)
+    print(f"balanced large prefill ctx={b.extra['prev_lens']} cus={cu_count(device)}", flush=True)
+    plain = _prefill(b, split_blocks=0)
+    outs = [_prefill(b, split_blocks=PREFILL_BALANCED) for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs:
+        d = float((o - plain).abs().max())
+        print(f"  vs unbalanced: max diff {d:.2e}", flush=True)
+        assert d <= 5e-3
+        assert torch.equal(o, outs[0])  # the same pieces merge in the same order every call
+    for r in (0, 6):
+        _check_large_request(b, outs[-1], r, 2e-2)
+
+
+@pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
+def test_balanced_ragged_requests(device, io_dtype):
+    """6 requests x 32 heads, T = 300 (three tiles, the last one partial): an empty request, a
+    request of 3 new tokens behind a 4000-token context (one long pair cut over many gangs), rows
+    padded past short chunks; every request against the oracle, the whole batch against the
+    unbalanced launch, twice in a row."""
+    ctx = [0, 37, 4000, 16, 0, 1200]
+    curs = [300, 150, 3, 90, 0, 300]
+    b = make_prefill(device, 41, ctx, curs, T=300, H=32, Hd=128, kv_dtype=torch.bfloat16)
+    assert _balanced_applies(b)
+    q = b.q.to(io_dtype)
+    print(f"balanced ragged io={io_dtype}", flush=True)
+    plain = _prefill(b, q=q, split_blocks=0)
+    got = _prefill(b, q=q, split_blocks=PREFILL_BALANCED)
+    again = _prefill(b, q=q, split_blocks=PREFILL_BALANCED)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
+    tol_plain, tol = (5e-3, 2e-2) if io_dtype == torch.float32 else (2e-2, 3e-2)
+    d = float((got.float() - plain.float()).abs().max())
+    want = oracle.paged_attention(q.float().cpu(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists, b.seq_lens,
+                                  b.cur_lens, nthreads=NTHREADS)
+    err = max_err(got, want)
+    print(f"  max err vs oracle {err:.2e}, vs unbalanced {d:.2e}", flush=True)
+    assert d <= tol_plain
+    assert err <= tol
+    assert float(got[4].abs().max()) == 0.0  # the empty request
+
+
+def test_balanced_many_heads_and_one_long_request(device):
+    """64 heads (8 pairs per die and request), one 6000-token context among three short ones (its
+    pairs are cut over several gangs each), -1 page entries inside cut tiles: against the
+    unbalanced launch everywhere and the oracle on the long request."""
+    ctx = [6000, 100, 300]
+    curs = [512, 512, 200]
+    b = make_prefill(device, 42, ctx, curs, T=512, H=64, Hd=128, kv_dtype=torch.bfloat16)
+    assert _balanced_applies(b)
+    pt = b.page_table.clone()
+    pt[0, [5, 130, 131, 300]] = -1
+    print("balanced 64 heads, one long request", flush=True)
+    plain = _prefill(b, page_table=pt, split_blocks=0)
+    got = _prefill(b, page_table=pt, split_blocks=PREFILL_BALANCED)
+    torch.cuda.synchronize()
+    d = float((got - plain).abs().max())
+    print(f"  vs unbalanced: max diff {d:.2e}", flush=True)
+    assert d <= 5e-3
+    full = _prefill(b, split_blocks=PREFILL_BALANCED)
+    assert float((got[0] - full[0]).abs().max()) > 1e-2  # the skipped keys did matter
+    want = oracle.paged_attention(b.q[1:].cpu(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists[1:],
+                                  b.seq_lens[1:], b.cur_lens[1:], nthreads=NTHREADS)
+    assert max_err(full[1:], want) <= 2e-2
+
+
+def test_balanced_needs_its_workspace(device):
+    """Asked for the balanced launch with a workspace smaller than pa_prefill_workspace_size, the
+    call fails on the host with PA_ERR_WORKSPACE and launches nothing."""
+    b = workloads.large_prefill(seed=0, device=device, batch=5, ctx_lo=1024, ctx_hi=1024)
+    B, H, T, Hd = b.q.shape
+    lib = _lib.load()
+    need = lib.pa_prefill_workspace_size(B, H, T, Hd, b.page_table.shape[1], PREFILL_BALANCED)
+    if need == 0:
+        pytest.skip("the balanced launch does not apply on this device at 5 x 32 x 4 tiles")
+    ws = torch.zeros(need // 2, dtype=torch.uint8, device=device)
+    out = torch.empty_like(b.q)
+    st = lib.pa_prefill(b.q.data_ptr(), b.q.stride(0), b.q.stride(1), b.q.stride(2),
+                        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _lib.dtype_code(b.q.dtype),
+                        b.k_pool.data_ptr(), b.v_pool.data_ptr(), _lib.dtype_code(b.k_pool.dtype),
+                        b.k_pool.shape[0], b.page_table.data_ptr(), b.page_table.stride(0),
+                        b.page_table.shape[1], b.seq_lens_t.data_ptr(), b.cur_lens_t.data_ptr(),
+                        B, H, T, Hd, 16, float(Hd) ** -0.5, PREFILL_BALANCED, ws.data_ptr(), need // 2, 0)
+    assert st == _lib.PA_ERR_WORKSPACE
+    assert "workspace" in lib.pa_last_error_message().decode()
