@@ -218,8 +218,11 @@ __device__ __forceinline__ void load_record_hi(const float* p, f32x4 (&v)[8]) {
       : "memory");
 }
 
+// The balanced launch (BAL) needs three workgroups per compute unit (its grid is the slots the
+// CUs hold at once): at most 168 registers per lane.
 template <typename IO, int HD, int NSUB, int NST, bool BAL>
-__device__ __forceinline__ void prefill_wide_body(const AttnArgs& a) {
+__global__ __launch_bounds__(kWideWaves * kWave) __attribute__((amdgpu_waves_per_eu(BAL ? 3 : 1)))
+void prefill_wide_kernel(const AttnArgs a) {
   constexpr int NW = kWideWaves;
   constexpr int KS = 32 * NSUB;          // keys per step
   constexpr int NBS = KS / 16;           // KV blocks per step
@@ -690,19 +693,6 @@ __device__ __forceinline__ void prefill_wide_body(const AttnArgs& a) {
       }
     }
   }  // pieces
-}
-
-template <typename IO, int HD, int NSUB, int NST>
-__global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_kernel(const AttnArgs a) {
-  prefill_wide_body<IO, HD, NSUB, NST, false>(a);
-}
-
-// The balanced launch needs three workgroups per compute unit (its grid is the slots the CUs
-// hold at once): at most 168 registers per lane.
-template <typename IO>
-__global__ __launch_bounds__(kWideWaves * kWave) __attribute__((amdgpu_waves_per_eu(3)))
-void prefill_balanced_kernel(const AttnArgs a) {
-  prefill_wide_body<IO, 128, 1, 2, true>(a);
 }
 
 // fp32 KV: the same workgroup layout, LDS staging and online softmax, on v_mfma_f32_32x32x2_f32
@@ -1274,9 +1264,9 @@ static int balanced_slots_per_cu() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
   if (cached[dev] == 0) {
     int nf = 0, nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_balanced_kernel<float>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_kernel<float, 128, 1, 2, true>,
                                                      kWideWaves * kWave, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_balanced_kernel<uint16_t>,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_kernel<uint16_t, 128, 1, 2, true>,
                                                      kWideWaves * kWave, 0) != hipSuccess)
       nf = nb = 0;
     cached[dev] = (nf < nb ? nf : nb) > 0 ? (nf < nb ? nf : nb) : -1;
@@ -1316,8 +1306,8 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
     const dim3 grid((unsigned)g);
     AttnArgs ab = a;
     ab.die_cus = pa_host::device_cu_count() / kXcds > 0 ? pa_host::device_cu_count() / kXcds : 1;
-    if (io_dtype == PA_DTYPE_F32) prefill_balanced_kernel<float><<<grid, block, 0, stream>>>(ab);
-    else prefill_balanced_kernel<uint16_t><<<grid, block, 0, stream>>>(ab);
+    if (io_dtype == PA_DTYPE_F32) prefill_wide_kernel<float, 128, 1, 2, true><<<grid, block, 0, stream>>>(ab);
+    else prefill_wide_kernel<uint16_t, 128, 1, 2, true><<<grid, block, 0, stream>>>(ab);
     PA_CHECK_LAUNCH("balanced wide prefill kernel");
     return PA_OK;
   }
@@ -1331,13 +1321,13 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
       else prefill_wide_f32_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
     }
   } else if (io_dtype == PA_DTYPE_F32) {
-    if (a.head_dim == 64) prefill_wide_kernel<float, 64, kWideNsub64, kWideStages64><<<grid, block, 0, stream>>>(a);
-    else if (wide128_pair(units)) prefill_wide_kernel<float, 128, 2, 2><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<float, 128, 1, 2><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<float, 64, kWideNsub64, kWideStages64, false><<<grid, block, 0, stream>>>(a);
+    else if (wide128_pair(units)) prefill_wide_kernel<float, 128, 2, 2, false><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<float, 128, 1, 2, false><<<grid, block, 0, stream>>>(a);
   } else {
-    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64, kWideNsub64, kWideStages64><<<grid, block, 0, stream>>>(a);
-    else if (wide128_pair(units)) prefill_wide_kernel<uint16_t, 128, 2, 2><<<grid, block, 0, stream>>>(a);
-    else prefill_wide_kernel<uint16_t, 128, 1, 2><<<grid, block, 0, stream>>>(a);
+    if (a.head_dim == 64) prefill_wide_kernel<uint16_t, 64, kWideNsub64, kWideStages64, false><<<grid, block, 0, stream>>>(a);
+    else if (wide128_pair(units)) prefill_wide_kernel<uint16_t, 128, 2, 2, false><<<grid, block, 0, stream>>>(a);
+    else prefill_wide_kernel<uint16_t, 128, 1, 2, false><<<grid, block, 0, stream>>>(a);
   }
   PA_CHECK_LAUNCH("wide prefill kernel");
   return PA_OK;
