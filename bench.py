@@ -560,7 +560,7 @@ def _large_prefill(res, device, steps):
     import torch
 
     from src import workloads
-    from src.kernels.hip_paged_attention import paged_attention_prefill_hip
+    from src.kernels.hip_paged_attention import PREFILL_BALANCED, paged_attention_prefill_hip
 
     for kv_dtype, tag in ((torch.bfloat16, "bf16kv"), (torch.float32, "fp32")):
         b = workloads.large_prefill(seed=0, device=device, kv_dtype=kv_dtype)
@@ -584,6 +584,13 @@ def _large_prefill(res, device, steps):
             "mfma_peak_TFLOPs": peak, "mfma_frac": round(tfs / peak, 4),
             "mfma_frac_graph": round(flops / (graph_ms * 1e-3) / 1e12 / peak, 4),
         }
+        if tag == "bf16kv":
+            # The opt-in balanced launch (one resident grid, KV steps dealt out evenly, cut tiles
+            # merged in the launch) timed beside the default one on the same batch.
+            bal = lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t,
+                                                      b.cur_lens_t, split_blocks=PREFILL_BALANCED)
+            bal_ms = time_call(bal, max(3, steps // 2))
+            res[f"large_prefill_{tag}"]["attention_us_balanced_launch"] = round(1e3 * bal_ms, 1)
         del b
         torch.cuda.empty_cache()
 
