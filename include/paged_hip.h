@@ -135,7 +135,8 @@ int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * per slot the compute units hold at once, the tiles' KV steps dealt out evenly among them, and
  * a tile cut between workgroups merged by the one that finishes it last, in the same launch;
  * other calls run as with 0. Every prefill workspace starts with PA_PREFILL_COUNTER_BYTES of
- * arrival counters that must be zero before its first use; every call leaves them zero.
+ * arrival counters that must be zero before its first use; every call leaves them zero. Calls that
+ * share a workspace must not run concurrently (e.g. on different streams).
  */
 int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
                void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
