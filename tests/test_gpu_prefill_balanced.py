@@ -122,3 +122,32 @@ def test_balanced_needs_its_workspace(device):
                         B, H, T, Hd, 16, float(Hd) ** -0.5, PREFILL_BALANCED, ws.data_ptr(), need // 2, 0)
     assert st == _lib.PA_ERR_WORKSPACE
     assert "workspace" in lib.pa_last_error_message().decode()
+
+
+def test_balanced_launch_in_a_graph(device):
+    """The balanced launch captured in a HIP graph (its counters are reset by the kernel, no memset
+    in the graph): three replays, each after eager calls of the same launch on other inputs, each
+    bit-identical to the eager result on the graph's inputs."""
+    b = workloads.large_prefill(seed=0, device=device, batch=5, ctx_lo=1024, ctx_hi=2048)
+    other = workloads.large_prefill(seed=9, device=device, batch=5, ctx_lo=1024, ctx_hi=2048)
+    assert _balanced_applies(b) and _balanced_applies(other)
+    print("balanced launch in a graph", flush=True)
+    out = torch.empty_like(b.q)
+    call = lambda: _prefill(b, split_blocks=PREFILL_BALANCED, out=out)
+    want = _prefill(b, split_blocks=PREFILL_BALANCED).clone()  # eager; allocates the workspace
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for r in range(3):
+        _prefill(other, split_blocks=PREFILL_BALANCED)  # eager work between the replays
+        torch.cuda.synchronize()
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {r}"
