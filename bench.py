@@ -363,7 +363,8 @@ def time_graph_call(fn, calls: int = 20, replays: int = 5) -> float:
     return e0.elapsed_time(e1) / (replays * calls)
 
 
-SECONDARY = ("single_decode", "ragged_decode", "chunked_prefill", "large_prefill", "mid_prefill")
+SECONDARY = ("single_decode", "ragged_decode", "chunked_prefill", "large_prefill", "mid_prefill",
+             "long_prompt_prefill")
 
 
 def secondary_workloads(device, steps: int, with_cpu: bool = True, only=SECONDARY) -> dict:
@@ -381,6 +382,8 @@ def secondary_workloads(device, steps: int, with_cpu: bool = True, only=SECONDAR
         _large_prefill(res, device, steps)
     if "mid_prefill" in only:
         _mid_prefill(res, device, steps)
+    if "long_prompt_prefill" in only:
+        _long_prompt_prefill(res, device, steps)
     return res
 
 
@@ -439,17 +442,22 @@ def _ragged_decode(res, device, steps, with_cpu):
 
 
 @contextlib.contextmanager
-def _forced_prefill_kernel(name):
-    """Force pa_prefill's kernel choice (tile | split | wide) for the calls inside the block."""
-    prev = os.environ.get("PAGED_HIP_PREFILL_KERNEL")
-    os.environ["PAGED_HIP_PREFILL_KERNEL"] = name
+def _env(var, value):
+    """Set an environment variable the library reads at each call for the calls inside the block."""
+    prev = os.environ.get(var)
+    os.environ[var] = value
     try:
         yield
     finally:
         if prev is None:
-            del os.environ["PAGED_HIP_PREFILL_KERNEL"]
+            del os.environ[var]
         else:
-            os.environ["PAGED_HIP_PREFILL_KERNEL"] = prev
+            os.environ[var] = prev
+
+
+def _forced_prefill_kernel(name):
+    """Force pa_prefill's kernel choice (tile | split | wide) for the calls inside the block."""
+    return _env("PAGED_HIP_PREFILL_KERNEL", name)
 
 
 def _chunked_prefill(res, device, steps, with_cpu):
@@ -585,14 +593,44 @@ def _large_prefill(res, device, steps):
             "mfma_frac_graph": round(flops / (graph_ms * 1e-3) / 1e12 / peak, 4),
         }
         if tag == "bf16kv":
-            # The opt-in balanced launch (one resident grid, KV steps dealt out evenly, cut tiles
-            # merged in the launch) timed beside the default one on the same batch.
+            # The balanced launch (a resident grid, KV steps dealt out evenly, cut tiles merged in
+            # the launch), which the library's policy does not take at this size, forced and timed
+            # beside the default one on the same batch.
             bal = lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t,
                                                       b.cur_lens_t, split_blocks=PREFILL_BALANCED)
-            bal_ms = time_call(bal, max(3, steps // 2))
+            with _env("PAGED_HIP_PREFILL_BALANCE", "force"):
+                bal_ms = time_call(bal, max(3, steps // 2))
             res[f"large_prefill_{tag}"]["attention_us_balanced_launch"] = round(1e3 * bal_ms, 1)
         del b
         torch.cuda.empty_cache()
+
+
+def _long_prompt_prefill(res, device, steps):
+    import torch
+
+    from src import workloads
+    from src.kernels.hip_paged_attention import paged_attention_prefill_hip
+
+    # One long prompt: 1 request x 32 heads x 128, a 512-token chunk over an 8k context (128
+    # tiles of 128 rows, half a tile per CU). The default call takes the balanced launch here; the
+    # unbalanced dispatch (the 16-row kernel at this tile count) is timed beside it.
+    b = workloads.large_prefill(seed=16, device=device, batch=1, chunk=512, ctx_lo=8192, ctx_hi=8192)
+    H, Hd = b.q.shape[1], b.q.shape[3]
+    flops = workloads.prefill_flops(b.extra["prev_lens"], b.cur_lens, H, Hd)
+    call = lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
+    ms = time_call(call, steps)
+    with _env("PAGED_HIP_PREFILL_BALANCE", "off"):
+        ms_plain = time_call(call, steps)
+    tfs = flops / (ms * 1e-3) / 1e12
+    res["long_prompt_prefill_bf16kv"] = {
+        "workload": f"1 request, {H} heads x {Hd}, context {b.extra['prev_lens'][0]} + chunk 512, bf16 KV, fp32 q/out "
+                    "(default dispatch: the balanced launch, two workgroups per CU)",
+        "attention_us": round(1e3 * ms, 1), "attention_us_unbalanced": round(1e3 * ms_plain, 1),
+        "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1), "mfma_peak_TFLOPs": 2500.0,
+        "mfma_frac": round(tfs / 2500.0, 4),
+    }
+    del b
+    torch.cuda.empty_cache()
 
 
 def _mid_prefill(res, device, steps):

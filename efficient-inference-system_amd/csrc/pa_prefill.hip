@@ -732,20 +732,20 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   a.num_splits = 1; a.split_blocks = 0; a.ws = nullptr;
 
   if (!prefill_fast_shape(head_dim, block_size)) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
-  if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
-      use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len)) {
-    if (split_blocks < 0 && kv_dtype == PA_DTYPE_BF16) {
-      const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages);
-      if (grid > 0) {
-        const size_t need = PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid);
-        if (workspace == nullptr || workspace_bytes < need)
-          PA_FAIL(PA_ERR_WORKSPACE, "prefill workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
-        a.counters = static_cast<int32_t*>(workspace);
-        a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + PA_PREFILL_COUNTER_BYTES);
-      }
+  if (split_blocks < 0 && kv_dtype == PA_DTYPE_BF16 && prefill_wide_supported(kv_dtype, head_dim, block_size)) {
+    const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages);
+    if (grid > 0) {
+      const size_t need = PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid);
+      if (workspace == nullptr || workspace_bytes < need)
+        PA_FAIL(PA_ERR_WORKSPACE, "prefill workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
+      a.counters = static_cast<int32_t*>(workspace);
+      a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + PA_PREFILL_COUNTER_BYTES);
+      return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
     }
-    return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
   }
+  if (split_blocks <= 0 && prefill_wide_supported(kv_dtype, head_dim, block_size) &&
+      use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len))
+    return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
   if (split_blocks <= 0 && prefill_split_supported(kv_dtype, head_dim, block_size) &&
       use_split_prefill(batch, num_heads, query_len))
     return launch_prefill_split(a, io_dtype, stream);

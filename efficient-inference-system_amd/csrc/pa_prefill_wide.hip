@@ -30,6 +30,8 @@
 //
 // The file also holds the split-step kernel (prefill_split_kernel, below): the same bf16 step on
 // 32-row tiles for short chunks, with a tile's steps split over 8 wavefronts instead of its rows.
+#include <string.h>
+
 #include "pa_attention.h"
 
 namespace pa {
@@ -1281,8 +1283,33 @@ int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_le
     return 0;
   const int64_t ntiles = (query_len + kWideRows - 1) / kWideRows;
   const int64_t units = (int64_t)batch * num_heads * ntiles;
-  if (wide128_pair(units) || units * (int64_t)sizeof(int32_t) > (int64_t)PA_PREFILL_COUNTER_BYTES) return 0;
-  const int64_t gangs = (int64_t)balanced_slots_per_cu() * pa_host::device_cu_count() / (kXcds * ntiles);
+  if (units * (int64_t)sizeof(int32_t) > (int64_t)PA_PREFILL_COUNTER_BYTES) return 0;
+  const int slots = balanced_slots_per_cu();
+  const int64_t cus = pa_host::device_cu_count();
+  // Where it pays (MI355X, bf16 KV, head_dim 128, graph-free eager timings; default launch ->
+  // balanced): few tiles over long contexts, where the default launch leaves CUs idle or each
+  // tile walks hundreds of steps alone: 1 x 32 heads, 512-token chunk over 8k 159 -> 96 us, over
+  // 3k 81 -> 59 us; 2 x 32, 256-token chunks over 8k 208 -> 103 us; 1 x 32, 128-token chunk over
+  // 16k 130 -> 86 us. It loses on short contexts (1 x 32, 128-token chunk over 4k 31 -> 38 us;
+  // 256 over 2k 28 -> 34 us) and on grids of two or more tiles per CU (8 x 32 heads, 512-token
+  // chunks: 237 -> 250 us), and ties in between (256 tiles: 0 to -5%). So: at most half a tile
+  // per CU and at least 8192 tile-steps (tiles x the longest tile's 32-key steps, from the page
+  // table's width), two workgroups per CU unless that cuts a tile more than 8 ways (then one).
+  const int64_t steps = ((int64_t)max_pages + 1) / 2;
+  bool pays = 2 * units <= cus && units * steps >= 8192;
+  int per_cu = 4 * units >= cus ? 2 : 1;  // two per CU cut each tile into 2 cus / units pieces
+  if (!pays && units > 2 * cus) per_cu = slots;
+  if (const char* env = getenv("PAGED_HIP_PREFILL_BALANCE")) {
+    if (strcmp(env, "force") == 0) pays = true;
+    if (strcmp(env, "off") == 0) pays = false;
+  }
+  if (!pays) return 0;
+  if (const char* env = getenv("PAGED_HIP_BALANCED_PER_CU")) {
+    const int v = atoi(env);
+    if (v >= 1) per_cu = v;
+  }
+  per_cu = per_cu < slots ? per_cu : slots;
+  const int64_t gangs = (int64_t)per_cu * cus / (kXcds * ntiles);
   if (gangs < 1) return 0;
   // The kernel's list positions are int: a die's work W (steps of at most max_pages / 2 + 1 per
   // pair, at least 1) stays below 2^31 / 64; its share table holds gangs + 1 entries.

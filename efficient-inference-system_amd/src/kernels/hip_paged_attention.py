@@ -89,18 +89,22 @@ def default_split_blocks(batch: int, num_heads: int, max_pages: int, device: tor
     return 0 if blocks >= max_pages else blocks
 
 
-# split_blocks value asking pa_prefill for its balanced launch (bf16 KV, head_dim 128, more than
-# two (request, head, 128-row tile) units per compute unit; other calls run unsplit).
+# split_blocks value asking pa_prefill for its balanced launch where the library's policy finds it
+# faster (bf16 KV, head_dim 128, heads a multiple of 8: few 128-row tiles over long contexts); other
+# calls run unsplit. PAGED_HIP_PREFILL_BALANCE=force / off overrides the policy.
 PREFILL_BALANCED = -1
 
 
 def default_prefill_split_blocks(batch: int, num_heads: int, query_len: int, max_pages: int,
-                                 device: torch.device) -> int:
-    """KV blocks per prefill split-K workgroup. Always 0: measured on MI355X, the second (merge)
-    launch costs more than the load balance it buys, from the chunked-prefill workload (4 x 8
-    heads, 16-row tiles over up to 58 blocks: 24.5 us unsplit, 32-95 us split) up to 8 x 32
-    heads with 512-token chunks. Callers may still pass split_blocks explicitly."""
-    return 0
+                                 device: torch.device, kv_dtype: torch.dtype | None = None) -> int:
+    """split_blocks for a prefill call: PREFILL_BALANCED for bf16 KV pools (the library takes the
+    balanced launch where it measured faster on MI355X: 1 x 32 heads x 128, 512-token chunk over an
+    8k context 159 -> 96 us; 2 x 32, 256-token chunks over 8k 208 -> 103 us), otherwise 0. Fixed
+    split-K (split_blocks > 0) is never the default: its second (merge) launch costs more than the
+    load balance it buys, from the chunked-prefill workload (4 x 8 heads, 16-row tiles over up to 58
+    blocks: 24.5 us unsplit, 32-95 us split) up to 8 x 32 heads with 512-token chunks. Callers may
+    still pass split_blocks explicitly."""
+    return PREFILL_BALANCED if kv_dtype == torch.bfloat16 else 0
 
 
 def _check_out(name: str, out: torch.Tensor, q: torch.Tensor) -> None:
@@ -187,7 +191,7 @@ def paged_attention_prefill_hip(
 ) -> torch.Tensor:
     """Chunked causal prefill attention for q [B, H, T, Hd]; returns a tensor shaped like q.
     split_blocks: KV blocks per split-K workgroup (0: none; PREFILL_BALANCED: the balanced launch
-    where it applies; None: default_prefill_split_blocks)."""
+    where the library finds it faster; None: default_prefill_split_blocks)."""
     _require_gpu("paged_attention_prefill_hip", q, k_pool, v_pool, page_table, seq_lens, current_lengths)
     _check_pool("paged_attention_prefill_hip", k_pool, v_pool)
     B, H, T, Hd = q.shape
@@ -205,7 +209,7 @@ def paged_attention_prefill_hip(
     max_pages = page_table.shape[1] if page_table.dim() == 2 else 0
     pt_stride = page_table.stride(0) if page_table.dim() == 2 and B > 0 else max_pages
     if split_blocks is None:
-        split_blocks = default_prefill_split_blocks(B, H, T, max_pages, q.device)
+        split_blocks = default_prefill_split_blocks(B, H, T, max_pages, q.device, k_pool.dtype)
     lib = _lib.load()
     ws_bytes = lib.pa_prefill_workspace_size(B, H, T, Hd, max_pages, split_blocks) if bs == 16 else 0
     ws_ptr = _workspace(q.device, ws_bytes, "prefill").data_ptr() if ws_bytes else None

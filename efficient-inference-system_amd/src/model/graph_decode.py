@@ -326,7 +326,7 @@ class _Captured:
             self.split_blocks = default_split_blocks(B, H, pages, device)
             ws_bytes = lib.pa_decode_workspace_size(B, H, Hd, pages, self.split_blocks)
         else:
-            self.split_blocks = default_prefill_split_blocks(B, H, Tb, pages, device)
+            self.split_blocks = default_prefill_split_blocks(B, H, Tb, pages, device, pools[0].dtype)
             ws_bytes = lib.pa_prefill_workspace_size(B, H, Tb, Hd, pages, self.split_blocks)
         # Allocated outside the capture and referenced here, so the address the graph records
         # stays valid for the graph's lifetime.

@@ -130,11 +130,14 @@ int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * KV blocks are also cut into ranges of split_blocks blocks, one workgroup each, whose partial
  * results a second kernel merges through a workspace of pa_prefill_workspace_size() bytes.
  * split_blocks == 0 means no split and no workspace. split_blocks < 0 (PA_PREFILL_BALANCED) asks
- * for the balanced launch where it applies (bf16 KV, head_dim 128, more than two (request, head,
- * 128-row tile) units per compute unit, num_heads a multiple of 8, batch <= 255): one workgroup
- * per slot the compute units hold at once, the tiles' KV steps dealt out evenly among them, and
- * a tile cut between workgroups merged by the one that finishes it last, in the same launch;
- * other calls run as with 0. Every prefill workspace starts with PA_PREFILL_COUNTER_BYTES of
+ * for the balanced launch where the library finds it faster: bf16 KV, head_dim 128, num_heads a
+ * multiple of 8, batch <= 255, at most one (request, head, 128-row tile) unit per two compute
+ * units and at least 8192 unit-steps (units x ceil(max_pages / 2)), i.e. few tiles over long
+ * contexts. It runs a grid of one or two workgroups per compute unit, deals the tiles' KV steps out
+ * evenly among them and merges a tile cut between workgroups in the same launch (the one that
+ * finishes it last). Other calls run as with 0. The environment variable
+ * PAGED_HIP_PREFILL_BALANCE=force takes it wherever it can run (three workgroups per compute unit
+ * on larger grids), =off never. Every prefill workspace starts with PA_PREFILL_COUNTER_BYTES of
  * arrival counters that must be zero before its first use; every call leaves them zero. Calls that
  * share a workspace must not run concurrently (e.g. on different streams).
  */

@@ -1,6 +1,6 @@
 """The balanced launch of the wide bf16 prefill kernel (head_dim 128; split_blocks < 0): the
-tiles' KV steps dealt out evenly over the workgroups the GPU holds at once, tiles cut between
-workgroups merged in the same launch by the piece that finishes last. Checked against the oracle
+tiles' KV steps dealt out evenly over a grid of resident workgroups, tiles cut between workgroups
+merged in the same launch by the piece that finishes last; the library's policy for when to take it. Checked against the oracle
 on the same bf16 KV values (2e-2, the bf16 tolerance) and against the unbalanced wide kernel,
 on repeated calls (the arrival counters must be left at zero) and ragged shapes whose tiles are
 cut into many pieces."""
@@ -20,6 +20,13 @@ pytestmark = pytest.mark.gpu
 NTHREADS = min(16, os.cpu_count() or 1)
 
 
+@pytest.fixture
+def forced(monkeypatch):
+    """The balanced launch wherever it can run, also where the library's policy would not take it
+    (these tests use large grids to cut tiles into many pieces)."""
+    monkeypatch.setenv("PAGED_HIP_PREFILL_BALANCE", "force")
+
+
 def _prefill(b, q=None, page_table=None, **kw):
     q = b.q if q is None else q
     pt = b.page_table if page_table is None else page_table
@@ -31,7 +38,7 @@ def _balanced_applies(b):
     return _lib.load().pa_prefill_workspace_size(B, H, T, Hd, b.page_table.shape[1], PREFILL_BALANCED) > 0
 
 
-def test_balanced_large_prefill(device):
+def test_balanced_large_prefill(device, forced):
     """The large-prefill workload (8 x 32 heads x 128, chunk 512 over 1-4k contexts): three calls
     in a row agree with each other up to the pieces' summation order and with the unbalanced
     launch; requests 0 (shortest) and 6 (longest, its tiles cut between workgroups) against the
@@ -52,7 +59,7 @@ def test_balanced_large_prefill(device):
 
 
 @pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
-def test_balanced_ragged_requests(device, io_dtype):
+def test_balanced_ragged_requests(device, forced, io_dtype):
     """6 requests x 32 heads, T = 300 (three tiles, the last one partial): an empty request, a
     request of 3 new tokens behind a 4000-token context (one long pair cut over many gangs), rows
     padded past short chunks; every request against the oracle, the whole batch against the
@@ -79,7 +86,7 @@ def test_balanced_ragged_requests(device, io_dtype):
     assert float(got[4].abs().max()) == 0.0  # the empty request
 
 
-def test_balanced_many_heads_and_one_long_request(device):
+def test_balanced_many_heads_and_one_long_request(device, forced):
     """64 heads (8 pairs per die and request), one 6000-token context among three short ones (its
     pairs are cut over several gangs each), -1 page entries inside cut tiles: against the
     unbalanced launch everywhere and the oracle on the long request."""
@@ -103,7 +110,7 @@ def test_balanced_many_heads_and_one_long_request(device):
     assert max_err(full[1:], want) <= 2e-2
 
 
-def test_balanced_needs_its_workspace(device):
+def test_balanced_needs_its_workspace(device, forced):
     """Asked for the balanced launch with a workspace smaller than pa_prefill_workspace_size, the
     call fails on the host with PA_ERR_WORKSPACE and launches nothing."""
     b = workloads.large_prefill(seed=0, device=device, batch=5, ctx_lo=1024, ctx_hi=1024)
@@ -124,7 +131,7 @@ def test_balanced_needs_its_workspace(device):
     assert "workspace" in lib.pa_last_error_message().decode()
 
 
-def test_balanced_launch_in_a_graph(device):
+def test_balanced_launch_in_a_graph(device, forced):
     """The balanced launch captured in a HIP graph (its counters are reset by the kernel, no memset
     in the graph): three replays, each after eager calls of the same launch on other inputs, each
     bit-identical to the eager result on the graph's inputs."""
@@ -151,3 +158,37 @@ def test_balanced_launch_in_a_graph(device):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {r}"
+
+
+def test_policy_takes_the_balanced_launch_on_a_long_context(device, monkeypatch):
+    """One request x 32 heads x 128, a 512-token chunk over an 8k context (128 tiles, half a tile
+    per CU): the default call takes the balanced launch (two workgroups per CU) and matches the
+    oracle on every head and the unbalanced launch; PAGED_HIP_PREFILL_BALANCE=off declines it."""
+    b = workloads.large_prefill(seed=16, device=device, batch=1, chunk=512, ctx_lo=8192, ctx_hi=8192)
+    if 2 * 128 > cu_count(device):
+        pytest.skip("fewer than 256 compute units")
+    assert _balanced_applies(b)
+    print("policy: balanced launch on 1 x 32 heads, chunk 512 over 8k", flush=True)
+    got = _prefill(b)  # default split_blocks: PREFILL_BALANCED for bf16 KV
+    monkeypatch.setenv("PAGED_HIP_PREFILL_BALANCE", "off")
+    assert not _balanced_applies(b)
+    plain = _prefill(b)
+    torch.cuda.synchronize()
+    d = float((got - plain).abs().max())
+    print(f"  vs unbalanced: max diff {d:.2e}", flush=True)
+    assert d <= 5e-3
+    _check_large_request(b, got, 0, 2e-2)
+
+
+def test_policy_declines_short_contexts_and_sizes_its_grid(device, monkeypatch):
+    """A 128-token chunk over 4k (32 tiles x 132 steps, under 8192 tile-steps): no balanced launch.
+    Over 16k it is taken with one workgroup per CU (two would cut each tile 16 ways)."""
+    monkeypatch.delenv("PAGED_HIP_PREFILL_BALANCE", raising=False)
+    lib = _lib.load()
+    cus = cu_count(device)
+    assert lib.pa_prefill_workspace_size(1, 32, 128, 128, (4096 + 128 + 15) // 16, PREFILL_BALANCED) == 0
+    need = lib.pa_prefill_workspace_size(1, 32, 128, 128, (16384 + 128 + 15) // 16, PREFILL_BALANCED)
+    if 2 * 32 > cus or 4 * 32 >= cus:
+        pytest.skip("the per-CU rule differs at this CU count")
+    record = 4 * 17 * 64 * 4 * 4  # four wavefronts x 17 groups x 64 lanes x 16 bytes
+    assert need == (64 << 10) + cus * 2 * record  # grid = one workgroup per CU
