@@ -343,6 +343,38 @@ __device__ __forceinline__ void merge_pair(const AttnArgs& a, int bh, int nact, 
   const int HD = a.head_dim;
   const int64_t R = HD + 2;
   const float* base = a.ws + (int64_t)bh * a.num_splits * R;
+  IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+  if (nact <= 8 && HD <= 2 * kWave) {
+    // At most 8 splits and two head_dim elements per lane: every word this lane needs (its
+    // elements from every split and, on lane s < nact, split s's m and l) in one batch of loads
+    // issued before any of them is used, so the merge waits for memory once. Indices past the
+    // last split read its record again and get weight 0.
+    const int d0 = lane < HD ? lane : HD - 1, d1 = lane + kWave < HD ? lane + kWave : HD - 1;
+    const int sl = lane < nact ? lane : nact - 1;
+    float x0[8], x1[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) x0[jj] = rec_load<COH>(base + (jj < nact ? jj : nact - 1) * R + 2 + d0);
+    if (HD > kWave) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) x1[jj] = rec_load<COH>(base + (jj < nact ? jj : nact - 1) * R + 2 + d1);
+    }
+    const float mr = rec_load<COH>(base + sl * R), lr = rec_load<COH>(base + sl * R + 1);
+    const float m0 = lane < nact ? mr : kNegBig;
+    const float M = wave_max(m0);
+    const float f0 = lane < nact ? fast_exp2(m0 - M) : 0.f;  // weight of split `lane`
+    const float lsum = wave_sum(lane < nact ? lr * f0 : 0.f);
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    float A0 = 0.f, A1 = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f0), jj));
+      A0 = fmaf(x0[jj], f, A0);
+      if (HD > kWave) A1 = fmaf(x1[jj], f, A1);
+    }
+    if (lane < HD) Elem<IO>::store(op + lane, A0 * inv);
+    if (lane + kWave < HD) Elem<IO>::store(op + lane + kWave, A1 * inv);
+    return;
+  }
   // Lane s holds split s's (m, l) for the first 64 splits; more splits are read in further passes.
   float m0 = kNegBig, l0 = 0.f;
   if (lane < nact) {
@@ -357,7 +389,6 @@ __device__ __forceinline__ void merge_pair(const AttnArgs& a, int bh, int nact, 
   for (int s = lane + kWave; s < nact; s += kWave) lsum = fmaf(rec_load<COH>(base + s * R + 1), fast_exp2(rec_load<COH>(base + s * R) - M), lsum);
   lsum = wave_sum(lsum);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
   for (int d = lane; d - lane < HD; d += kWave) {
     const int dd = d < HD ? d : HD - 1;  // every lane takes part in the broadcasts
     float A = 0.f;
