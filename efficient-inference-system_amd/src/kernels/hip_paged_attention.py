@@ -21,6 +21,7 @@ import torch
 from src.kernels import _lib
 
 _workspaces: dict[tuple[int, str], torch.Tensor] = {}
+_retired_workspaces: list[torch.Tensor] = []
 _cu_counts: dict[int, int] = {}
 
 
@@ -56,12 +57,15 @@ def cu_count(device: torch.device) -> int:
 
 def _workspace(device: torch.device, nbytes: int, kind: str) -> torch.Tensor:
     """The device's split-K workspace for `kind` ("decode" or "prefill"), at least `nbytes` long.
-    Decode workspaces start with the arrival counters of the in-launch merge, which must be zero
-    before first use and stay zero between calls: they are zero-filled when allocated and never
-    shared with prefill calls, whose records would overwrite them."""
+    Both kinds start with arrival counters of the in-launch merges, which must be zero before first
+    use and stay zero between calls: workspaces are zero-filled when allocated, and the two kinds
+    are kept apart (their layouts differ). A workspace replaced by a larger one stays allocated
+    for the life of the process: a HIP graph a caller captured may hold its address."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     ws = _workspaces.get((idx, kind))
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _retired_workspaces.append(ws)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[(idx, kind)] = ws
     return ws

@@ -9,6 +9,7 @@ import torch
 
 import oracle
 from src import workloads
+from src.kernels import _lib
 from src.kernels.hip_paged_attention import paged_attention_decode_hip
 
 pytestmark = pytest.mark.gpu
@@ -282,3 +283,43 @@ def test_in_launch_split_merge_shares_one_workspace_across_shapes_and_graph_repl
         assert max_err(run(b2, split_blocks=split2), wants[1 + rep % 2]) <= 1e-4
         torch.cuda.synchronize()
         assert counters_zero()
+
+
+def test_captured_graph_keeps_its_workspace_when_a_larger_one_is_needed(device):
+    """A graph captured with a split decode records its workspace's address; a later call that
+    needs a larger workspace makes the wrapper allocate a new one, and the old one must stay
+    allocated: after fresh allocations are filled with other data, the graph still replays to the
+    oracle's result and leaves its counters at zero."""
+    from src.kernels import hip_paged_attention as hpa
+
+    small = make_batch(device, 41, [300, 900, 650, 128], [1] * 4, H=8, Hd=64)
+    big = make_batch(device, 42, [3000, 2900, 2800, 2700, 2600, 2500, 2400, 2300], [1] * 8, H=32, Hd=128,
+                     kv_dtype=torch.bfloat16)
+    want_small = oracle_out(small)
+    idx = device.index if device.index is not None else 0
+    prev = hpa._workspaces.pop((idx, "decode"), None)  # start from a fresh (1 MiB) workspace
+    if prev is not None:
+        hpa._retired_workspaces.append(prev)
+    out = torch.empty_like(small.q)
+    call = lambda: run(small, split_blocks=16, out=out)
+    call()  # allocates the workspace this graph records
+    torch.cuda.synchronize()
+    old = hpa._workspaces[(idx, "decode")]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    need = _lib.load().pa_decode_workspace_size(8, 32, 128, big.page_table.shape[1], 16)
+    assert need > old.numel()  # the big call grows the workspace
+    print(f"workspace {old.numel()} -> {need} bytes", flush=True)
+    assert max_err(run(big, split_blocks=16), oracle_out(big)) <= 2e-2
+    torch.cuda.synchronize()
+    assert hpa._workspaces[(idx, "decode")].data_ptr() != old.data_ptr()
+    filler = [torch.full((old.numel() // 4,), 7.0, device=device) for _ in range(4)]  # reuses freed memory, if any
+    torch.cuda.synchronize()
+    for rep in range(2):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert max_err(out, want_small) <= 1e-4, rep
+        assert int(old[:256 << 10].view(torch.int32).abs().sum()) == 0
+    del filler
