@@ -687,8 +687,10 @@ using namespace pa;
 extern "C" size_t pa_prefill_workspace_size(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                                             int32_t max_pages, int32_t split_blocks) {
   if (batch <= 0 || num_heads <= 0 || query_len <= 0 || !prefill_fast_shape(head_dim, 16)) return 0;
-  if (split_blocks < 0) {
-    const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages);
+  if (split_blocks < 0) {  // the larger of the bf16 and fp32 KV launches' needs
+    const int64_t gb = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages, PA_DTYPE_BF16);
+    const int64_t gf = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages, PA_DTYPE_F32);
+    const int64_t grid = gb > gf ? gb : gf;
     return grid > 0 ? PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid) : 0;
   }
   const int s = prefill_num_splits(max_pages, split_blocks);
@@ -732,8 +734,8 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   a.num_splits = 1; a.split_blocks = 0; a.ws = nullptr;
 
   if (!prefill_fast_shape(head_dim, block_size)) return launch_generic_attention(a, io_dtype, kv_dtype, stream);
-  if (split_blocks < 0 && kv_dtype == PA_DTYPE_BF16 && prefill_wide_supported(kv_dtype, head_dim, block_size)) {
-    const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages);
+  if (split_blocks < 0 && prefill_wide_supported(kv_dtype, head_dim, block_size)) {
+    const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages, kv_dtype);
     if (grid > 0) {
       const size_t need = PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid);
       if (workspace == nullptr || workspace_bytes < need)

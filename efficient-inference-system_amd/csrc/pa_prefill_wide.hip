@@ -707,7 +707,7 @@ void prefill_wide_kernel(const AttnArgs a) {
 //                    tile d, row c) and B = its softmax weight, exactly as held.
 // Per 32-key step a wavefront issues HD MFMAs of 32x32x2 (HD/2 for QK^T, HD/2 for PV), so the
 // per-step costs are small next to the matrix work.
-template <typename IO, int HD>
+template <typename IO, int HD, bool BAL>
 __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(const AttnArgs a) {
   constexpr int NW = kWideWaves;
   constexpr int KS = 32;                 // keys per step (two 16-token blocks)
@@ -718,6 +718,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   constexpr int RPC = HD / 4;            // 16-byte chunks per key row
   constexpr int CPT = KS * RPC / (NW * kWave);
   static_assert(CPT >= 1 && KS * RPC == CPT * NW * kWave, "tile split");
+  static_assert(!BAL || HD == 128, "balanced launch shape");
 
   __shared__ __attribute__((aligned(16))) float sk[2][KS * RS];
   __shared__ __attribute__((aligned(16))) float sv[2][KS * RS];
@@ -728,11 +729,98 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   const int c = lane & 31;
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
-  int bh, qt;
-  static_assert(sizeof(sk) >= (kOrderMax + 1) * sizeof(int), "order scratch");
-  if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(&sk[0][0]), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
-  const int h = bh % a.H;
-  const int b = bh / a.H;
+  // Steps of 32 keys that tile qt of request b walks (the valid keys of its last row).
+  auto tile_steps = [&](int rb, int rqt) {
+    const int last = (rqt * kWideRows + kWideRows - 1) < (a.T - 1) ? (rqt * kWideRows + kWideRows - 1) : (a.T - 1);
+    int nbb = (valid_keys(a.seq_lens[rb], a.cur_lens[rb], last) + 15) / 16;  // nondecreasing in the row
+    nbb = nbb < a.max_pages ? nbb : a.max_pages;
+    return (nbb + NBS - 1) / NBS;
+  };
+  int bh = 0, qt = 0;
+  // BAL (as in prefill_wide_kernel): this workgroup's share [lo, hi) of its die's pair list, the
+  // pair it has reached (request pb, head k + 8 hh), that pair's list position Sb and work P.
+  int k = 0, gang = 0, NG = 1, HP = 1, pb = 0, hh = 0, P = 1;
+  int W = 1, lo = 0, hi = 0, Sb = 0;
+  __shared__ int sm_last;                     // BAL: this piece arrived last
+  __shared__ int sP[kWideWaves * kWave];      // BAL: pair work per request
+  __shared__ int sS[kWideWaves * kWave];      // BAL: its prefix sums
+  __shared__ int sCw[kWideWaves * kWave];     // BAL: prefix sums of the gangs' share weights
+  __shared__ int sLo[kWideWaves * kWave];     // BAL: the gangs' shares: [sLo[g], sLo[g + 1])
+  auto gang_of = [&](int pos) {
+    int lg = 0, ug = NG - 1;
+    while (lg < ug) {
+      const int mid = (lg + ug + 1) / 2;
+      if (__builtin_amdgcn_readfirstlane(sLo[mid]) <= pos) lg = mid;
+      else ug = mid - 1;
+    }
+    return lg;
+  };
+  if constexpr (!BAL) {
+    static_assert(sizeof(sk) >= (kOrderMax + 1) * sizeof(int), "order scratch");
+    if (!wide_lpt_unit(a, ntiles, reinterpret_cast<int*>(&sk[0][0]), bh, qt)) wide_unit(blockIdx.x, a.B * a.H, ntiles, bh, qt);
+  } else {
+    k = blockIdx.x % kXcds;
+    const int jx = blockIdx.x / kXcds;
+    gang = jx / ntiles;
+    qt = jx - gang * ntiles;
+    NG = gridDim.x / (kXcds * ntiles);
+    HP = a.H / kXcds;
+    if (threadIdx.x < a.B) {
+      const int p = tile_steps(threadIdx.x, ntiles - 1);
+      sP[threadIdx.x] = p > 1 ? p : 1;
+    }
+    __syncthreads();
+    if (threadIdx.x <= a.B) {
+      int s = 0;
+      for (int r = 0; r < (int)threadIdx.x; ++r) s += sP[r];
+      sS[threadIdx.x] = s;
+    }
+    if (threadIdx.x <= NG) {
+      int s = 0;
+      for (int gg = 0; gg < (int)threadIdx.x; ++gg) s += share_weight(gg * ntiles / a.die_cus);
+      sCw[threadIdx.x] = s;
+    }
+    __syncthreads();
+    W = HP * __builtin_amdgcn_readfirstlane(sS[a.B]);
+    if (threadIdx.x <= NG) sLo[threadIdx.x] = (int)((int64_t)W * sCw[threadIdx.x] / sCw[NG]);
+    __syncthreads();
+    lo = __builtin_amdgcn_readfirstlane(sLo[gang]);
+    hi = __builtin_amdgcn_readfirstlane(sLo[gang + 1]);
+    int lb = 0, ub = a.B - 1;
+    while (lb < ub) {
+      const int mid = (lb + ub + 1) / 2;
+      if (HP * __builtin_amdgcn_readfirstlane(sS[mid]) <= lo) lb = mid;
+      else ub = mid - 1;
+    }
+    pb = lb;
+    Sb = __builtin_amdgcn_readfirstlane(sS[pb]);
+    P = __builtin_amdgcn_readfirstlane(sS[pb + 1]) - Sb;
+    hh = (int)((lo - HP * Sb) / P);
+  }
+  for (bool first = true;; first = false) {
+  int b, h, s_hi = 0x7fffffff;
+  int s_lo = 0, np = 1, g0 = 0, rec_slot = 0;
+  int tile_start = 0;
+  if constexpr (!BAL) {
+    h = bh % a.H;
+    b = bh / a.H;
+  } else {
+    tile_start = HP * Sb + hh * P;
+    if (lo >= hi || pb >= a.B || tile_start >= hi) break;
+    s_lo = lo > tile_start ? lo - tile_start : 0;
+    s_hi = hi - tile_start < P ? hi - tile_start : P;
+    const int nt = tile_steps(pb, qt);
+    const int ntp = nt > 1 ? nt : 1;
+    np = 0;  // no piece of this tile when the share starts past its steps
+    if (lo < tile_start + ntp) {
+      g0 = gang_of(tile_start);
+      np = gang_of(tile_start + ntp - 1) - g0 + 1;
+      rec_slot = lo >= tile_start ? 0 : 1;
+    }
+    b = pb;
+    h = k + kXcds * hh;
+    if (!first) __syncthreads();  // every wavefront is done with the previous piece's LDS tiles
+  }
   const int i0 = qt * kWideRows;
   const int iw = i0 + 32 * w;
   const int i = iw + c;
@@ -740,11 +828,15 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   const int L = a.seq_lens[b];
   const int C = a.cur_lens[b];
   const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
-  const int last_wg = (i0 + kWideRows - 1) < (a.T - 1) ? (i0 + kWideRows - 1) : (a.T - 1);
+  // Blocks the walk loads: up to the last row of the tile (BAL: of the pair's last tile, so that
+  // a gang's workgroups walk the same steps).
+  const int last_row = BAL ? ntiles * kWideRows - 1 : i0 + kWideRows - 1;
+  const int last_wg = last_row < (a.T - 1) ? last_row : (a.T - 1);
   const int n_wg = valid_keys(L, C, last_wg);
   int nb = (n_wg + 15) / 16;
   nb = nb < a.max_pages ? nb : a.max_pages;
-  const int nsteps = (nb + NBS - 1) / NBS;
+  int nsteps = (nb + NBS - 1) / NBS;
+  nsteps = nsteps < s_hi ? nsteps : s_hi;
   int wsteps = 0;
   if (iw < a.T) {
     const int last_w = (iw + 31) < (a.T - 1) ? (iw + 31) : (a.T - 1);
@@ -880,23 +972,92 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
     __builtin_amdgcn_s_setprio(0);
   };
 
-  if (nsteps > 0) {
+  if (s_lo < nsteps) {
     int cur[NBS], nxt[NBS];
-    gload(0, cur);
+    gload(s_lo, cur);
     lstore(0);
     __syncthreads();
-    for (int st = 0; st < nsteps; ++st) {
+    for (int st = s_lo; st < nsteps; ++st) {
       const bool more = st + 1 < nsteps;
       if (more) gload(st + 1, nxt);
-      if (st < wsteps) compute(st & 1, st, cur);
-      if (more) lstore((st + 1) & 1);
+      if (st < wsteps) compute((st - s_lo) & 1, st, cur);
+      if (more) lstore((st + 1 - s_lo) & 1);
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < NBS; ++j) cur[j] = nxt[j];
     }
   }
 
-  if (i >= a.T) return;
+  bool store = true;
+  if constexpr (BAL) {
+    if (np == 0) {
+      store = false;
+    } else if (np > 1) {
+      // Cut tile: the record and merge protocol of prefill_wide_kernel (same accumulator layout).
+      int32_t* cnt = a.counters + ((int64_t)b * a.H + h) * ntiles + qt;
+      constexpr int WREC = kWideRecGroups * kWave * 4;  // a wavefront's floats in a record
+      bool last = false;
+      if (gang == g0) {
+        if (threadIdx.x == 0) sm_last = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
+        __syncthreads();
+        last = __builtin_amdgcn_readfirstlane(sm_last);
+      }
+      if (!last) {
+        float* rp = a.ws + ((int64_t)blockIdx.x * 2 + rec_slot) * kWideRecFloats<HD> + w * WREC + 4 * lane;
+        store_record_group(rp, f32x4{m, l, 0.f, 0.f});
+#pragma unroll
+        for (int d = 0; d < DU; ++d)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            store_record_group(rp + (1 + 4 * d + q4) * 4 * kWave,
+                               f32x4{oacc[d][4 * q4], oacc[d][4 * q4 + 1], oacc[d][4 * q4 + 2], oacc[d][4 * q4 + 3]});
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+          sm_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
+        __syncthreads();
+        last = __builtin_amdgcn_readfirstlane(sm_last);
+      }
+      store = last;
+      if (last) {
+        if (threadIdx.x == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (gang != g0) {
+          m = kNegBig;
+          l = 0.f;
+        }
+        for (int gg = gang == g0 ? g0 + 1 : g0; gg < g0 + np; ++gg) {
+          const int slot = __builtin_amdgcn_readfirstlane(sLo[gg]) >= tile_start ? 0 : 1;
+          const int64_t x = (int64_t)kXcds * ((int64_t)gg * ntiles + qt) + k;
+          const float* rq = a.ws + (x * 2 + slot) * kWideRecFloats<HD> + w * WREC + 4 * lane;
+          f32x4 lo4[9];
+          load_record_lo(rq, lo4);
+          const float mr = lo4[0][0], lr = lo4[0][1];
+          const float mn = fmaxf(m, mr);
+          const float fa = gg == g0 ? 0.f : fast_exp2(m - mn), fr = fast_exp2(mr - mn);
+          l = l * fa + lr * fr;
+          m = mn;
+#pragma unroll
+          for (int gi = 1; gi < 9; ++gi)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
+              oacc[d][r] = oacc[d][r] * fa + lo4[gi][e] * fr;
+            }
+          f32x4 hi4[8];
+          load_record_hi(rq, hi4);
+#pragma unroll
+          for (int gi = 9; gi < 17; ++gi)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
+              oacc[d][r] = oacc[d][r] * fa + hi4[gi - 9][e] * fr;
+            }
+        }
+      }
+    }
+  }
+
+  if (store && i < a.T) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
   IO* op = static_cast<IO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_st;
 #pragma unroll
@@ -907,6 +1068,19 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
 #pragma unroll
       for (int d = 0; d < DU; ++d) Elem<IO>::store(op + R * DU + d, oacc[d][4 * j + r] * inv);
     }
+  }
+  if constexpr (!BAL) {
+    break;
+  } else {
+    if (++hh == HP) {
+      hh = 0;
+      if (++pb < a.B) {
+        Sb = __builtin_amdgcn_readfirstlane(sS[pb]);
+        P = __builtin_amdgcn_readfirstlane(sS[pb + 1]) - Sb;
+      }
+    }
+  }
+  }  // pieces
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1257,46 +1431,59 @@ int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len) 
   return (int64_t)batch * num_heads * ((query_len + kWideRows - 1) / kWideRows);
 }
 
-// Workgroups of the balanced kernel one compute unit holds at once (the smaller of its two
-// output types), per device.
-static int balanced_slots_per_cu() {
+// Workgroups of the balanced kernel for `kv_dtype` one compute unit holds at once (the smaller
+// of its two output types), per device.
+static int balanced_slots_per_cu(int kv_dtype) {
   constexpr int kMaxDevices = 64;
-  static int cached[kMaxDevices] = {0};
+  static int cached[2][kMaxDevices] = {};
+  const int kind = kv_dtype == PA_DTYPE_F32 ? 1 : 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  if (cached[dev] == 0) {
+  if (cached[kind][dev] == 0) {
     int nf = 0, nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_kernel<float, 128, 1, 2, true>,
-                                                     kWideWaves * kWave, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_kernel<uint16_t, 128, 1, 2, true>,
-                                                     kWideWaves * kWave, 0) != hipSuccess)
-      nf = nb = 0;
-    cached[dev] = (nf < nb ? nf : nb) > 0 ? (nf < nb ? nf : nb) : -1;
+    hipError_t e1, e2;
+    if (kind == 1) {
+      e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_f32_kernel<float, 128, true>,
+                                                        kWideWaves * kWave, 0);
+      e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_f32_kernel<uint16_t, 128, true>,
+                                                        kWideWaves * kWave, 0);
+    } else {
+      e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_kernel<float, 128, 1, 2, true>,
+                                                        kWideWaves * kWave, 0);
+      e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_kernel<uint16_t, 128, 1, 2, true>,
+                                                        kWideWaves * kWave, 0);
+    }
+    if (e1 != hipSuccess || e2 != hipSuccess) nf = nb = 0;
+    cached[kind][dev] = (nf < nb ? nf : nb) > 0 ? (nf < nb ? nf : nb) : -1;
   }
-  return cached[dev] > 0 ? cached[dev] : 0;
+  return cached[kind][dev] > 0 ? cached[kind][dev] : 0;
 }
 
 int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
-                              int32_t max_pages) {
+                              int32_t max_pages, int kv_dtype) {
   if (head_dim != 128 || batch < 1 || batch > 255 || num_heads < kXcds || num_heads % kXcds != 0 ||
       query_len < 1 || max_pages < 0)
     return 0;
   const int64_t ntiles = (query_len + kWideRows - 1) / kWideRows;
   const int64_t units = (int64_t)batch * num_heads * ntiles;
   if (units * (int64_t)sizeof(int32_t) > (int64_t)PA_PREFILL_COUNTER_BYTES) return 0;
-  const int slots = balanced_slots_per_cu();
+  const int slots = balanced_slots_per_cu(kv_dtype);
   const int64_t cus = pa_host::device_cu_count();
-  // Where it pays (MI355X, bf16 KV, head_dim 128, graph-free eager timings; default launch ->
-  // balanced): few tiles over long contexts, where the default launch leaves CUs idle or each
-  // tile walks hundreds of steps alone: 1 x 32 heads, 512-token chunk over 8k 159 -> 96 us, over
-  // 3k 81 -> 59 us; 2 x 32, 256-token chunks over 8k 208 -> 103 us; 1 x 32, 128-token chunk over
-  // 16k 130 -> 86 us. It loses on short contexts (1 x 32, 128-token chunk over 4k 31 -> 38 us;
-  // 256 over 2k 28 -> 34 us) and on grids of two or more tiles per CU (8 x 32 heads, 512-token
-  // chunks: 237 -> 250 us), and ties in between (256 tiles: 0 to -5%). So: at most half a tile
-  // per CU and at least 8192 tile-steps (tiles x the longest tile's 32-key steps, from the page
-  // table's width), two workgroups per CU unless that cuts a tile more than 8 ways (then one).
+  // Where it pays (MI355X, head_dim 128, graph-free eager timings; default launch -> balanced):
+  // few tiles over long contexts, where the default launch leaves CUs idle or each tile walks
+  // hundreds of steps alone. bf16 KV: 1 x 32 heads, 512-token chunk over 8k 159 -> 96 us, over 3k
+  // 81 -> 59 us; 2 x 32, 256-token chunks over 8k 208 -> 103 us; 1 x 32, 128-token chunk over 16k
+  // 130 -> 86 us; it loses on short contexts (1 x 32, 128-token chunk over 4k 31 -> 38 us; 256
+  // over 2k 28 -> 34 us) and on grids of two or more tiles per CU (8 x 32 heads, 512-token chunks:
+  // 237 -> 250 us), and ties in between (256 tiles: 0 to -5%). fp32 KV (a step costs more, so
+  // cutting pays sooner): 1 x 32, 512-token chunk over 8k 807 -> 574 us, over 1k 144 -> 126 us;
+  // 256-token chunk over 2k 109 -> 105 us; 128-token chunk over 16k 356 -> 321 us, over 4k 92 ->
+  // 108 us (loses). So: at most half a tile per CU and at least 8192 tile-steps (tiles x the
+  // longest tile's 32-key steps, from the page table's width), 4096 for fp32 KV from a quarter
+  // tile per CU; two workgroups per CU unless that cuts a tile more than 8 ways (then one).
   const int64_t steps = ((int64_t)max_pages + 1) / 2;
-  bool pays = 2 * units <= cus && units * steps >= 8192;
+  const int64_t min_steps = kv_dtype == PA_DTYPE_F32 && 4 * units >= cus ? 4096 : 8192;
+  bool pays = 2 * units <= cus && units * steps >= min_steps;
   int per_cu = 4 * units >= cus ? 2 : 1;  // two per CU cut each tile into 2 cus / units pieces
   if (!pays && units > 2 * cus) per_cu = slots;
   if (const char* env = getenv("PAGED_HIP_PREFILL_BALANCE")) {
@@ -1328,24 +1515,30 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
   const dim3 block(kWideWaves * kWave);
   if (a.counters != nullptr) {
     // Balanced launch: the caller checked prefill_balanced_grid > 0 and sized the workspace.
-    const int64_t g = prefill_balanced_grid(a.B, a.H, a.T, a.head_dim, a.max_pages);
-    if (g <= 0 || kv_dtype != PA_DTYPE_BF16) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "balanced prefill does not apply");
+    const int64_t g = prefill_balanced_grid(a.B, a.H, a.T, a.head_dim, a.max_pages, kv_dtype);
+    if (g <= 0) PA_FAIL(PA_ERR_INVALID_ARGUMENT, "balanced prefill does not apply");
     const dim3 grid((unsigned)g);
     AttnArgs ab = a;
     ab.die_cus = pa_host::device_cu_count() / kXcds > 0 ? pa_host::device_cu_count() / kXcds : 1;
-    if (io_dtype == PA_DTYPE_F32) prefill_wide_kernel<float, 128, 1, 2, true><<<grid, block, 0, stream>>>(ab);
-    else prefill_wide_kernel<uint16_t, 128, 1, 2, true><<<grid, block, 0, stream>>>(ab);
+    if (kv_dtype == PA_DTYPE_F32) {
+      if (io_dtype == PA_DTYPE_F32) prefill_wide_f32_kernel<float, 128, true><<<grid, block, 0, stream>>>(ab);
+      else prefill_wide_f32_kernel<uint16_t, 128, true><<<grid, block, 0, stream>>>(ab);
+    } else if (io_dtype == PA_DTYPE_F32) {
+      prefill_wide_kernel<float, 128, 1, 2, true><<<grid, block, 0, stream>>>(ab);
+    } else {
+      prefill_wide_kernel<uint16_t, 128, 1, 2, true><<<grid, block, 0, stream>>>(ab);
+    }
     PA_CHECK_LAUNCH("balanced wide prefill kernel");
     return PA_OK;
   }
   const dim3 grid((unsigned)units);
   if (kv_dtype == PA_DTYPE_F32) {
     if (io_dtype == PA_DTYPE_F32) {
-      if (a.head_dim == 64) prefill_wide_f32_kernel<float, 64><<<grid, block, 0, stream>>>(a);
-      else prefill_wide_f32_kernel<float, 128><<<grid, block, 0, stream>>>(a);
+      if (a.head_dim == 64) prefill_wide_f32_kernel<float, 64, false><<<grid, block, 0, stream>>>(a);
+      else prefill_wide_f32_kernel<float, 128, false><<<grid, block, 0, stream>>>(a);
     } else {
-      if (a.head_dim == 64) prefill_wide_f32_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
-      else prefill_wide_f32_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
+      if (a.head_dim == 64) prefill_wide_f32_kernel<uint16_t, 64, false><<<grid, block, 0, stream>>>(a);
+      else prefill_wide_f32_kernel<uint16_t, 128, false><<<grid, block, 0, stream>>>(a);
     }
   } else if (io_dtype == PA_DTYPE_F32) {
     if (a.head_dim == 64) prefill_wide_kernel<float, 64, kWideNsub64, kWideStages64, false><<<grid, block, 0, stream>>>(a);

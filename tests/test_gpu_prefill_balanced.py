@@ -1,9 +1,9 @@
-"""The balanced launch of the wide bf16 prefill kernel (head_dim 128; split_blocks < 0): the
-tiles' KV steps dealt out evenly over a grid of resident workgroups, tiles cut between workgroups
-merged in the same launch by the piece that finishes last; the library's policy for when to take it. Checked against the oracle
-on the same bf16 KV values (2e-2, the bf16 tolerance) and against the unbalanced wide kernel,
-on repeated calls (the arrival counters must be left at zero) and ragged shapes whose tiles are
-cut into many pieces."""
+"""The balanced launch of the wide prefill kernels (bf16 and fp32 KV, head_dim 128; split_blocks
+< 0): the tiles' KV steps dealt out evenly over a grid of resident workgroups, tiles cut between
+workgroups merged in the same launch by the piece that finishes last; and the library's policy
+for when to take it. Checked against the oracle on the same KV values (bf16 KV 2e-2, fp32 KV
+1e-4) and against the unbalanced launch, on repeated calls (the arrival counters must be left at
+zero), in a HIP graph, and on ragged shapes whose tiles are cut into many pieces."""
 import os
 
 import numpy as np
@@ -58,24 +58,29 @@ def test_balanced_large_prefill(device, forced):
         _check_large_request(b, outs[-1], r, 2e-2)
 
 
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
-def test_balanced_ragged_requests(device, forced, io_dtype):
+def test_balanced_ragged_requests(device, forced, io_dtype, kv_dtype):
     """6 requests x 32 heads, T = 300 (three tiles, the last one partial): an empty request, a
     request of 3 new tokens behind a 4000-token context (one long pair cut over many gangs), rows
     padded past short chunks; every request against the oracle, the whole batch against the
     unbalanced launch, twice in a row."""
     ctx = [0, 37, 4000, 16, 0, 1200]
     curs = [300, 150, 3, 90, 0, 300]
-    b = make_prefill(device, 41, ctx, curs, T=300, H=32, Hd=128, kv_dtype=torch.bfloat16)
+    b = make_prefill(device, 41, ctx, curs, T=300, H=32, Hd=128, kv_dtype=kv_dtype)
     assert _balanced_applies(b)
     q = b.q.to(io_dtype)
-    print(f"balanced ragged io={io_dtype}", flush=True)
+    print(f"balanced ragged io={io_dtype} kv={kv_dtype}", flush=True)
     plain = _prefill(b, q=q, split_blocks=0)
     got = _prefill(b, q=q, split_blocks=PREFILL_BALANCED)
     again = _prefill(b, q=q, split_blocks=PREFILL_BALANCED)
     torch.cuda.synchronize()
     assert torch.equal(got, again)
-    tol_plain, tol = (5e-3, 2e-2) if io_dtype == torch.float32 else (2e-2, 3e-2)
+    if kv_dtype == torch.float32:
+        # bf16 output: half an ulp of outputs up to ~4 is ~1.6e-2 against the fp64 oracle
+        tol_plain, tol = (2e-5, 1e-4) if io_dtype == torch.float32 else (1e-2, 3e-2)
+    else:
+        tol_plain, tol = (5e-3, 2e-2) if io_dtype == torch.float32 else (2e-2, 3e-2)
     d = float((got.float() - plain.float()).abs().max())
     want = oracle.paged_attention(q.float().cpu(), b.k_pool.cpu(), b.v_pool.cpu(), b.block_lists, b.seq_lens,
                                   b.cur_lens, nthreads=NTHREADS)
@@ -160,24 +165,26 @@ def test_balanced_launch_in_a_graph(device, forced):
         assert torch.equal(out, want), f"replay {r}"
 
 
-def test_policy_takes_the_balanced_launch_on_a_long_context(device, monkeypatch):
+@pytest.mark.parametrize("kv_dtype,tol_plain,tol", [(torch.bfloat16, 5e-3, 2e-2), (torch.float32, 2e-5, 1e-4)])
+def test_policy_takes_the_balanced_launch_on_a_long_context(device, monkeypatch, kv_dtype, tol_plain, tol):
     """One request x 32 heads x 128, a 512-token chunk over an 8k context (128 tiles, half a tile
     per CU): the default call takes the balanced launch (two workgroups per CU) and matches the
     oracle on every head and the unbalanced launch; PAGED_HIP_PREFILL_BALANCE=off declines it."""
-    b = workloads.large_prefill(seed=16, device=device, batch=1, chunk=512, ctx_lo=8192, ctx_hi=8192)
+    b = workloads.large_prefill(seed=16, device=device, batch=1, chunk=512, ctx_lo=8192, ctx_hi=8192,
+                                kv_dtype=kv_dtype)
     if 2 * 128 > cu_count(device):
         pytest.skip("fewer than 256 compute units")
     assert _balanced_applies(b)
-    print("policy: balanced launch on 1 x 32 heads, chunk 512 over 8k", flush=True)
-    got = _prefill(b)  # default split_blocks: PREFILL_BALANCED for bf16 KV
+    print(f"policy: balanced launch on 1 x 32 heads, chunk 512 over 8k, kv={kv_dtype}", flush=True)
+    got = _prefill(b)  # default split_blocks: PREFILL_BALANCED
     monkeypatch.setenv("PAGED_HIP_PREFILL_BALANCE", "off")
     assert not _balanced_applies(b)
     plain = _prefill(b)
     torch.cuda.synchronize()
     d = float((got - plain).abs().max())
     print(f"  vs unbalanced: max diff {d:.2e}", flush=True)
-    assert d <= 5e-3
-    _check_large_request(b, got, 0, 2e-2)
+    assert d <= tol_plain
+    _check_large_request(b, got, 0, tol)
 
 
 def test_policy_declines_short_contexts_and_sizes_its_grid(device, monkeypatch):
@@ -186,7 +193,7 @@ def test_policy_declines_short_contexts_and_sizes_its_grid(device, monkeypatch):
     monkeypatch.delenv("PAGED_HIP_PREFILL_BALANCE", raising=False)
     lib = _lib.load()
     cus = cu_count(device)
-    assert lib.pa_prefill_workspace_size(1, 32, 128, 128, (4096 + 128 + 15) // 16, PREFILL_BALANCED) == 0
+    assert lib.pa_prefill_workspace_size(1, 32, 128, 128, (4096 + 128 + 15) // 16, PREFILL_BALANCED) == 0  # both dtypes
     need = lib.pa_prefill_workspace_size(1, 32, 128, 128, (16384 + 128 + 15) // 16, PREFILL_BALANCED)
     if 2 * 32 > cus or 4 * 32 >= cus:
         pytest.skip("the per-CU rule differs at this CU count")
