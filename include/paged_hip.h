@@ -130,14 +130,14 @@ int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * KV blocks are also cut into ranges of split_blocks blocks, one workgroup each, whose partial
  * results a second kernel merges through a workspace of pa_prefill_workspace_size() bytes.
  * split_blocks == 0 means no split and no workspace. split_blocks < 0 (PA_PREFILL_BALANCED) asks
- * for the balanced launch where the library finds it faster: bf16 KV, head_dim 128, num_heads a
- * multiple of 8, batch <= 255, at most one (request, head, 128-row tile) unit per two compute
- * units and at least 8192 unit-steps (units x ceil(max_pages / 2)), i.e. few tiles over long
- * contexts. It runs a grid of one or two workgroups per compute unit, deals the tiles' KV steps out
+ * for the balanced launch where the library finds it faster: head_dim 128, num_heads a multiple of
+ * 8, batch <= 255, at most one (request, head, 128-row tile) unit per two compute units and at
+ * least 8192 unit-steps (units x ceil(max_pages / 2); fp32 KV: 4096 from one unit per four
+ * compute units), i.e. few tiles over long contexts. It runs a grid of one or two workgroups per compute unit, deals the tiles' KV steps out
  * evenly among them and merges a tile cut between workgroups in the same launch (the one that
  * finishes it last). Other calls run as with 0. The environment variable
- * PAGED_HIP_PREFILL_BALANCE=force takes it wherever it can run (three workgroups per compute unit
- * on larger grids), =off never. Every prefill workspace starts with PA_PREFILL_COUNTER_BYTES of
+ * PAGED_HIP_PREFILL_BALANCE=force takes it wherever it can run (as many workgroups per compute
+ * unit as fit on larger grids), =off never. Every prefill workspace starts with PA_PREFILL_COUNTER_BYTES of
  * arrival counters that must be zero before its first use; every call leaves them zero. Calls that
  * share a workspace must not run concurrently (e.g. on different streams).
  */
@@ -152,8 +152,8 @@ int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_
                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of workspace pa_prefill needs for these sizes (0 when neither a split nor the balanced
- * launch applies; the balanced launch's size is given whatever the KV dtype, and fp32 KV calls
- * leave that workspace unused). No reference counterpart: the Triton prefill path has no split-K. */
+ * launch applies; for the balanced launch the larger of its bf16 and fp32 KV needs). No reference
+ * counterpart: the Triton prefill path has no split-K. */
 size_t pa_prefill_workspace_size(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                                  int32_t max_pages, int32_t split_blocks);
 
