@@ -612,23 +612,27 @@ def _long_prompt_prefill(res, device, steps):
     from src.kernels.hip_paged_attention import paged_attention_prefill_hip
 
     # One long prompt: 1 request x 32 heads x 128, a 512-token chunk over an 8k context (128
-    # tiles of 128 rows, half a tile per CU), bf16 and fp32 KV. The default call takes the balanced
-    # launch here; the unbalanced dispatch (the 16-row kernel at this tile count) is timed beside it.
-    for kv_dtype, tag, peak in ((torch.bfloat16, "bf16kv", 2500.0), (torch.float32, "fp32", 157.3)):
-        b = workloads.large_prefill(seed=16, device=device, batch=1, chunk=512, ctx_lo=8192, ctx_hi=8192,
-                                    kv_dtype=kv_dtype)
-        H, Hd = b.q.shape[1], b.q.shape[3]
+    # tiles of 128 rows, half a tile per CU), bf16 and fp32 KV; and the benchmark model's head
+    # shape (8 heads x 64), a 128-token chunk over a 32k context (8 tiles), bf16 KV. The default
+    # call takes the balanced launch on each; the unbalanced dispatch (the 16-row kernel on the
+    # first two, the split-step kernel on the third) is timed beside it.
+    for kv_dtype, tag, peak, H, Hd, chunk, ctx, per_cu in (
+            (torch.bfloat16, "bf16kv", 2500.0, 32, 128, 512, 8192, "two workgroups"),
+            (torch.float32, "fp32", 157.3, 32, 128, 512, 8192, "two workgroups"),
+            (torch.bfloat16, "bf16kv_head_dim_64", 2500.0, 8, 64, 128, 32768, "one workgroup")):
+        b = workloads.large_prefill(seed=16, device=device, batch=1, heads=H, head_dim=Hd, chunk=chunk,
+                                    ctx_lo=ctx, ctx_hi=ctx, kv_dtype=kv_dtype)
         flops = workloads.prefill_flops(b.extra["prev_lens"], b.cur_lens, H, Hd)
         call = lambda: paged_attention_prefill_hip(b.q, b.k_pool, b.v_pool, b.page_table, b.seq_lens_t, b.cur_lens_t)
-        reps = steps if tag == "bf16kv" else max(3, steps // 4)
+        reps = steps if kv_dtype == torch.bfloat16 else max(3, steps // 4)
         ms = time_call(call, reps)
         with _env("PAGED_HIP_PREFILL_BALANCE", "off"):
             ms_plain = time_call(call, reps)
         tfs = flops / (ms * 1e-3) / 1e12
         res[f"long_prompt_prefill_{tag}"] = {
-            "workload": f"1 request, {H} heads x {Hd}, context {b.extra['prev_lens'][0]} + chunk 512, "
-                        f"{'bf16' if tag == 'bf16kv' else 'fp32'} KV, fp32 q/out "
-                        "(default dispatch: the balanced launch, two workgroups per CU)",
+            "workload": f"1 request, {H} heads x {Hd}, context {b.extra['prev_lens'][0]} + chunk {chunk}, "
+                        f"{'bf16' if kv_dtype == torch.bfloat16 else 'fp32'} KV, fp32 q/out "
+                        f"(default dispatch: the balanced launch, {per_cu} per CU)",
             "attention_us": round(1e3 * ms, 1), "attention_us_unbalanced": round(1e3 * ms_plain, 1),
             "useful_gflop": round(flops / 1e9, 2), "TFLOPs": round(tfs, 1), "mfma_peak_TFLOPs": peak,
             "mfma_frac": round(tfs / peak, 4),

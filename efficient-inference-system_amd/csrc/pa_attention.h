@@ -60,7 +60,7 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
 // the bytes of its split records. launch_prefill_wide takes it when a.counters is set.
 int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                               int32_t max_pages, int kv_dtype);
-size_t prefill_balanced_record_bytes(int64_t grid);
+size_t prefill_balanced_record_bytes(int64_t grid, int32_t head_dim);
 
 // Split-step prefill (32 query rows per workgroup, 8 wavefronts splitting the KV steps; bf16 KV
 // at head_dim 64). Defined in pa_prefill_wide.hip.

@@ -662,17 +662,22 @@ static bool use_wide_prefill(int kv_dtype, int32_t head_dim, int32_t batch, int3
 
 // Split-step kernel (32-row tiles, 8 wavefronts splitting the KV steps; bf16 KV at head_dim 64)
 // instead of the 16-row kernel, by its unit count U = B * H * ceil(T / 32) (one workgroup per CU
-// at most): it is taken from half the CUs to the CU count for chunks longer than 64 rows, where it
-// measured faster on MI355X; below half the CUs or for short chunks the 16-row kernel's extra
-// workgroups win. PAGED_HIP_PREFILL_KERNEL=split forces it where it applies (tile forces the
-// 16-row kernel).
-static bool use_split_prefill(int32_t batch, int32_t num_heads, int32_t query_len) {
+// at most) and the page-table width: it is taken for chunks longer than 64 rows from half the CUs
+// to the CU count, and up to twice the CU count (two rounds) once the widest request spans 96
+// pages, where it measured faster on MI355X (its 32-row tiles read each KV step half as often as
+// the 16-row kernel's, which pays once the context outweighs the second round's tail: at 512
+// units 0.96-1.02x of the 16-row time at 48-64 pages, 0.74-0.87x from 96 pages; at 384 units a
+// tie at 88-96 pages, 0.92-0.97x from 120); below half the CUs or for short chunks the 16-row
+// kernel's extra workgroups win. PAGED_HIP_PREFILL_KERNEL=split forces it where it applies (tile
+// forces the 16-row kernel).
+static bool use_split_prefill(int32_t batch, int32_t num_heads, int32_t query_len, int32_t max_pages) {
   const char* env = getenv("PAGED_HIP_PREFILL_KERNEL");
   if (env != nullptr && strcmp(env, "split") == 0) return true;
   if (env != nullptr && strcmp(env, "tile") == 0) return false;
   const int64_t units = prefill_split_units(batch, num_heads, query_len);
   const int64_t cus = pa_host::device_cu_count();
-  return query_len > 64 && 2 * units >= cus && units <= cus;
+  if (query_len <= 64 || 2 * units < cus) return false;
+  return units <= cus || (units <= 2 * cus && max_pages >= 96);
 }
 
 static int prefill_num_splits(int32_t max_pages, int32_t split_blocks) {
@@ -691,7 +696,7 @@ extern "C" size_t pa_prefill_workspace_size(int32_t batch, int32_t num_heads, in
     const int64_t gb = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages, PA_DTYPE_BF16);
     const int64_t gf = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages, PA_DTYPE_F32);
     const int64_t grid = gb > gf ? gb : gf;
-    return grid > 0 ? PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid) : 0;
+    return grid > 0 ? PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid, head_dim) : 0;
   }
   const int s = prefill_num_splits(max_pages, split_blocks);
   if (s <= 1) return 0;
@@ -737,7 +742,7 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   if (split_blocks < 0 && prefill_wide_supported(kv_dtype, head_dim, block_size)) {
     const int64_t grid = prefill_balanced_grid(batch, num_heads, query_len, head_dim, max_pages, kv_dtype);
     if (grid > 0) {
-      const size_t need = PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid);
+      const size_t need = PA_PREFILL_COUNTER_BYTES + prefill_balanced_record_bytes(grid, head_dim);
       if (workspace == nullptr || workspace_bytes < need)
         PA_FAIL(PA_ERR_WORKSPACE, "prefill workspace too small: need %zu bytes, have %zu", need, workspace_bytes);
       a.counters = static_cast<int32_t*>(workspace);
@@ -749,7 +754,7 @@ extern "C" int pa_prefill(const void* q, int64_t q_stride_b, int64_t q_stride_h,
       use_wide_prefill(kv_dtype, head_dim, batch, num_heads, query_len))
     return launch_prefill_wide(a, io_dtype, kv_dtype, stream);
   if (split_blocks <= 0 && prefill_split_supported(kv_dtype, head_dim, block_size) &&
-      use_split_prefill(batch, num_heads, query_len))
+      use_split_prefill(batch, num_heads, query_len, max_pages))
     return launch_prefill_split(a, io_dtype, stream);
 
   const int64_t units = (int64_t)batch * num_heads * ((query_len + 15) / 16);

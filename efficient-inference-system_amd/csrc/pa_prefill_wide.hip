@@ -143,7 +143,8 @@ constexpr int kWideStages64 = WIDE_NST64;
 // round of workgroups needs the CU slots it holds.
 static bool wide128_pair(int64_t units) { return units <= 2 * (int64_t)pa_host::device_cu_count(); }
 
-// Balanced launch (BAL; head_dim 128 bf16 KV, one 32-key sub-tile per step, 2 stages): the grid
+// Balanced launch (BAL; bf16 KV at head_dim 128 with one 32-key sub-tile per step or at head_dim
+// 64 with two, fp32 KV at head_dim 128; 2 stages): the grid
 // is the workgroups the compute units hold at once (three per CU), and the KV steps of all tiles are
 // dealt out evenly instead of one workgroup per tile. Die k (workgroups x = k mod 8) takes the
 // (request, head) pairs with head = k mod 8, listed by request, then head; a pair's work is the
@@ -157,11 +158,12 @@ static bool wide128_pair(int64_t units) { return units <= 2 * (int64_t)pa_host::
 // share's first and last pair; pairs inside a share are never cut), and the piece that arrives
 // last (per-tile arrival counter, reset to zero by that piece) merges them in gang order.
 // Workspace: a.counters holds one arrival counter per (request, head, tile), zero between calls;
-// a.ws the records, slot s of workgroup x at a.ws + (2 x + s) * kWideRecFloats. A wavefront's
-// part is 17 groups of 16 bytes per lane, lane-minor (group j of lane L at float 4 (64 j + L), so
-// each group is one coalesced 1 KB block): group 0 holds m and l, group 1 + 4d + q the
-// accumulators oacc[d][4q .. 4q + 3].
-constexpr int kWideRecGroups = 17;
+// a.ws the records, slot s of workgroup x at a.ws + (2 x + s) * kWideRecFloats<HD>. A wavefront's
+// part is 1 + HD / 8 groups of 16 bytes per lane (17 at head_dim 128, 9 at 64), lane-minor (group
+// j of lane L at float 4 (64 j + L), so each group is one coalesced 1 KB block): group 0 holds m
+// and l, group 1 + 4d + q the accumulators oacc[d][4q .. 4q + 3].
+template <int HD>
+constexpr int kWideRecGroups = 1 + HD / 32 * 16 / 4;
 // Share weight of the gangs whose workgroups are the s-th to reach their compute units (s = 0, 1, 2
 // at three workgroups per CU). Measured on MI355X with equal shares (8 x 32 heads x 128, chunk
 // 512 over 1.8-3.7k contexts): the first, second and third workgroup of each CU finished at 197,
@@ -169,11 +171,12 @@ constexpr int kWideRecGroups = 17;
 __device__ __forceinline__ int share_weight(int s) { return s < 2 ? 22 - s : 20; }
 
 template <int HD>
-constexpr int kWideRecFloats = kWideWaves * kWideRecGroups * kWave * 4;
-static_assert(kWideRecGroups == 1 + 128 / 32 * 16 / 4, "record groups at head_dim 128");
+constexpr int kWideRecFloats = kWideWaves * kWideRecGroups<HD> * kWave * 4;
+static_assert(kWideRecGroups<128> == 17 && kWideRecGroups<64> == 9, "record groups");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-// Groups 0-8 and 9-16 of a record (p: the lane's group 0; groups 1 KB apart), read with the
+// Groups 0-8 and 9-16 of a record (p: the lane's group 0; groups 1 KB apart; a head_dim 64 record
+// is groups 0-8 only), read with the
 // device-scope coherence bit (sc1) that relaxed agent-scope atomic loads use, nine and eight
 // loads in flight, each batch waited for inside its assembly block. (As atomic loads the compiler
 // issues them one at a time, waiting for each: 66 memory round trips per record.)
@@ -239,7 +242,7 @@ void prefill_wide_kernel(const AttnArgs a) {
   constexpr int TILE = KS * HD;          // elements per K (or V) tile
 
   static_assert(NST == 2 || NST == 3, "stages");
-  static_assert(!BAL || (HD == 128 && NSUB == 1 && NST == 2), "balanced launch shape");
+  static_assert(!BAL || (NST == 2 && NSUB == (HD == 128 ? 1 : 2)), "balanced launch shape");
   // Stage s: K tile at sbuf + 2 * s * TILE, V tile right after it (one array addressed through
   // per-stage pointers takes fewer registers than one array per tile).
   __shared__ __attribute__((aligned(16))) uint16_t sbuf[NST * 2 * TILE];
@@ -608,7 +611,7 @@ void prefill_wide_kernel(const AttnArgs a) {
         // is gang g0 (the values its record would hold), so the result does not depend on which
         // piece arrives last.
         int32_t* cnt = a.counters + ((int64_t)b * a.H + h) * ntiles + qt;
-        constexpr int WREC = kWideRecGroups * kWave * 4;  // a wavefront's floats in a record
+        constexpr int WREC = kWideRecGroups<HD> * kWave * 4;  // a wavefront's floats in a record
         bool last = false;
         if (gang == g0) {
           if (threadIdx.x == 0) sm_last = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
@@ -658,15 +661,17 @@ void prefill_wide_kernel(const AttnArgs a) {
                 const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
                 oacc[d][r] = oacc[d][r] * fa + lo[gi][e] * fr;
               }
-            f32x4 hi[8];
-            load_record_hi(rq, hi);
+            if constexpr (HD == 128) {
+              f32x4 hi[8];
+              load_record_hi(rq, hi);
 #pragma unroll
-            for (int gi = 9; gi < 17; ++gi)
+              for (int gi = 9; gi < 17; ++gi)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
-                oacc[d][r] = oacc[d][r] * fa + hi[gi - 9][e] * fr;
-              }
+                for (int e = 0; e < 4; ++e) {
+                  const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
+                  oacc[d][r] = oacc[d][r] * fa + hi[gi - 9][e] * fr;
+                }
+            }
           }
         }
       }
@@ -995,7 +1000,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
     } else if (np > 1) {
       // Cut tile: the record and merge protocol of prefill_wide_kernel (same accumulator layout).
       int32_t* cnt = a.counters + ((int64_t)b * a.H + h) * ntiles + qt;
-      constexpr int WREC = kWideRecGroups * kWave * 4;  // a wavefront's floats in a record
+      constexpr int WREC = kWideRecGroups<HD> * kWave * 4;  // a wavefront's floats in a record
       bool last = false;
       if (gang == g0) {
         if (threadIdx.x == 0) sm_last = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
@@ -1431,12 +1436,12 @@ int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len) 
   return (int64_t)batch * num_heads * ((query_len + kWideRows - 1) / kWideRows);
 }
 
-// Workgroups of the balanced kernel for `kv_dtype` one compute unit holds at once (the smaller
-// of its two output types), per device.
-static int balanced_slots_per_cu(int kv_dtype) {
+// Workgroups of the balanced kernel for `kv_dtype` and `head_dim` one compute unit holds at once
+// (the smaller of its two output types), per device.
+static int balanced_slots_per_cu(int kv_dtype, int head_dim) {
   constexpr int kMaxDevices = 64;
-  static int cached[2][kMaxDevices] = {};
-  const int kind = kv_dtype == PA_DTYPE_F32 ? 1 : 0;
+  static int cached[3][kMaxDevices] = {};
+  const int kind = kv_dtype == PA_DTYPE_F32 ? 1 : head_dim == 64 ? 2 : 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
   if (cached[kind][dev] == 0) {
@@ -1446,6 +1451,11 @@ static int balanced_slots_per_cu(int kv_dtype) {
       e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_f32_kernel<float, 128, true>,
                                                         kWideWaves * kWave, 0);
       e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_f32_kernel<uint16_t, 128, true>,
+                                                        kWideWaves * kWave, 0);
+    } else if (kind == 2) {
+      e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_kernel<float, 64, kWideNsub64, 2, true>,
+                                                        kWideWaves * kWave, 0);
+      e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_kernel<uint16_t, 64, kWideNsub64, 2, true>,
                                                         kWideWaves * kWave, 0);
     } else {
       e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_kernel<float, 128, 1, 2, true>,
@@ -1461,13 +1471,16 @@ static int balanced_slots_per_cu(int kv_dtype) {
 
 int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                               int32_t max_pages, int kv_dtype) {
-  if (head_dim != 128 || batch < 1 || batch > 255 || num_heads < kXcds || num_heads % kXcds != 0 ||
-      query_len < 1 || max_pages < 0)
+  if (!(head_dim == 128 || (head_dim == 64 && kv_dtype == PA_DTYPE_BF16)) || batch < 1 || batch > 255 ||
+      num_heads < kXcds || num_heads % kXcds != 0 || query_len < 1 || max_pages < 0)
     return 0;
   const int64_t ntiles = (query_len + kWideRows - 1) / kWideRows;
   const int64_t units = (int64_t)batch * num_heads * ntiles;
   if (units * (int64_t)sizeof(int32_t) > (int64_t)PA_PREFILL_COUNTER_BYTES) return 0;
-  const int slots = balanced_slots_per_cu(kv_dtype);
+  const int slots = balanced_slots_per_cu(kv_dtype, head_dim);
+  // KV blocks per step: 32-key steps at head_dim 128, 64-key steps at 64 (the same products per
+  // query row).
+  const int nbs = head_dim == 128 ? 2 : 2 * kWideNsub64;
   const int64_t cus = pa_host::device_cu_count();
   // Where it pays (MI355X, head_dim 128, graph-free eager timings; default launch -> balanced):
   // few tiles over long contexts, where the default launch leaves CUs idle or each tile walks
@@ -1481,9 +1494,16 @@ int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_le
   // 108 us (loses). So: at most half a tile per CU and at least 8192 tile-steps (tiles x the
   // longest tile's 32-key steps, from the page table's width), 4096 for fp32 KV from a quarter
   // tile per CU; two workgroups per CU unless that cuts a tile more than 8 ways (then one).
-  const int64_t steps = ((int64_t)max_pages + 1) / 2;
+  const int64_t steps = ((int64_t)max_pages + nbs - 1) / nbs;
   const int64_t min_steps = kv_dtype == PA_DTYPE_F32 && 4 * units >= cus ? 4096 : 8192;
   bool pays = 2 * units <= cus && units * steps >= min_steps;
+  // Head_dim 64 (bf16 KV, 64-key steps: twice the softmax work per matrix product of a head_dim 128
+  // step, and the split-step kernel as the alternative): 1 x 32 heads, 512-token chunk over 8k
+  // 64.6 -> 56.9 us, 2 x 32, 256 over 8k 63.8 -> 57.3 us, 1 x 32, 128 over 16k 52.8 -> 46.8 us;
+  // ties at 1 x 32, 512 over 4k (38.8 / 38.1) and 1 x 8, 512 over 8k (32.2 / 31.4); loses at
+  // 1 x 16, 512 over 8k (33.1 -> 38.1), 4 x 8, 256 over 4k (19.3 -> 28.5) and 1 x 32, 512 over 2k
+  // (25.1 -> 28.8). So at least 16384 tile-steps, or 256 steps (16k keys) per tile.
+  if (head_dim == 64) pays = 2 * units <= cus && (units * steps >= 16384 || steps >= 256);
   int per_cu = 4 * units >= cus ? 2 : 1;  // two per CU cut each tile into 2 cus / units pieces
   if (!pays && units > 2 * cus) per_cu = slots;
   if (const char* env = getenv("PAGED_HIP_PREFILL_BALANCE")) {
@@ -1498,15 +1518,15 @@ int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_le
   per_cu = per_cu < slots ? per_cu : slots;
   const int64_t gangs = (int64_t)per_cu * cus / (kXcds * ntiles);
   if (gangs < 1) return 0;
-  // The kernel's list positions are int: a die's work W (steps of at most max_pages / 2 + 1 per
+  // The kernel's list positions are int: a die's work W (steps of at most max_pages / nbs + 1 per
   // pair, at least 1) stays below 2^31 / 64; its share table holds gangs + 1 entries.
-  const int64_t w = (int64_t)(num_heads / kXcds) * batch * ((int64_t)max_pages / 2 + 1);
+  const int64_t w = (int64_t)(num_heads / kXcds) * batch * ((int64_t)max_pages / nbs + 1);
   if (w >= (0x7fffffffLL >> 6) || gangs + 1 > kWideWaves * kWave) return 0;
   return gangs * kXcds * ntiles;
 }
 
-size_t prefill_balanced_record_bytes(int64_t grid) {
-  return (size_t)grid * 2 * kWideRecFloats<128> * sizeof(float);
+size_t prefill_balanced_record_bytes(int64_t grid, int32_t head_dim) {
+  return (size_t)grid * 2 * (head_dim == 64 ? kWideRecFloats<64> : kWideRecFloats<128>) * sizeof(float);
 }
 
 int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream) {
@@ -1523,6 +1543,9 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
     if (kv_dtype == PA_DTYPE_F32) {
       if (io_dtype == PA_DTYPE_F32) prefill_wide_f32_kernel<float, 128, true><<<grid, block, 0, stream>>>(ab);
       else prefill_wide_f32_kernel<uint16_t, 128, true><<<grid, block, 0, stream>>>(ab);
+    } else if (a.head_dim == 64) {
+      if (io_dtype == PA_DTYPE_F32) prefill_wide_kernel<float, 64, kWideNsub64, 2, true><<<grid, block, 0, stream>>>(ab);
+      else prefill_wide_kernel<uint16_t, 64, kWideNsub64, 2, true><<<grid, block, 0, stream>>>(ab);
     } else if (io_dtype == PA_DTYPE_F32) {
       prefill_wide_kernel<float, 128, 1, 2, true><<<grid, block, 0, stream>>>(ab);
     } else {

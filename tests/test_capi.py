@@ -67,8 +67,10 @@ def test_host_only_entry_points(lib):
     assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 58, 16) == (64 << 10) + 4 * 8 * 16 * 4 * 16 * (64 + 2) * 4
     assert lib.pa_prefill_workspace_size(4, 8, 256, 64, 16, 16) == 0
     assert lib.pa_prefill_workspace_size(4, 8, 256, 96, 58, 16) == 0  # no tuned kernel: no split
-    # the balanced launch applies to head_dim 128 only (and needs a device to size its grid)
+    # the balanced launch sizes its grid from the device's compute units (none here: no workspace);
+    # it never applies to other head_dims or to head counts that are not a multiple of 8
     assert lib.pa_prefill_workspace_size(8, 32, 512, 64, 300, -1) == 0
+    assert lib.pa_prefill_workspace_size(8, 32, 512, 96, 300, -1) == 0
     assert lib.pa_prefill_workspace_size(8, 12, 512, 128, 300, -1) == 0  # heads not a multiple of 8
 
 

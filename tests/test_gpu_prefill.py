@@ -454,3 +454,23 @@ def test_large_prefill_parity(device):
     assert 8 * 32 * 4 >= 2 * cu_count(device)  # the wide kernel's grid rule holds at this size
     for r in (0, 5):
         _check_large_request(b, out, r, 2e-2)
+
+
+@pytest.mark.parametrize("ctx,kernel", [(2048, "split"), (256, "tile")])
+def test_split_step_kernel_two_rounds_by_context(device, monkeypatch, ctx, kernel):
+    """4 requests x 8 heads x 64, 512-token chunks, bf16 KV: 512 split-step units (two per CU on
+    MI355X). The default dispatch takes the split-step kernel for two rounds once the widest
+    request spans 96 pages (a 2k context), the 16-row kernel below that: its output equals the
+    forced kernel's bit for bit, and two requests match the oracle."""
+    from src.kernels.hip_paged_attention import cu_count
+    b = workloads.large_prefill(seed=7, device=device, batch=4, heads=8, head_dim=64, chunk=512,
+                                ctx_lo=ctx, ctx_hi=ctx)
+    units, cus = 4 * 8 * (512 // 32), cu_count(device)
+    if not cus < units <= 2 * cus:
+        pytest.skip(f"{units} units is not one to two rounds on {cus} CUs")
+    print(f"split-step two rounds ctx={ctx} pages={b.page_table.shape[1]} expect {kernel}", flush=True)
+    out = run(b)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_KERNEL", kernel)
+    assert torch.equal(out, run(b))
+    for r in (0, 3):
+        _check_large_request(b, out, r, 2e-2)

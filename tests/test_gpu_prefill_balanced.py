@@ -1,5 +1,5 @@
-"""The balanced launch of the wide prefill kernels (bf16 and fp32 KV, head_dim 128; split_blocks
-< 0): the tiles' KV steps dealt out evenly over a grid of resident workgroups, tiles cut between
+"""The balanced launch of the wide prefill kernels (bf16 KV at head_dim 128 and 64, fp32 KV at
+head_dim 128; split_blocks < 0): the tiles' KV steps dealt out evenly over a grid of resident workgroups, tiles cut between
 workgroups merged in the same launch by the piece that finishes last; and the library's policy
 for when to take it. Checked against the oracle on the same KV values (bf16 KV 2e-2, fp32 KV
 1e-4) and against the unbalanced launch, on repeated calls (the arrival counters must be left at
@@ -58,19 +58,38 @@ def test_balanced_large_prefill(device, forced):
         _check_large_request(b, outs[-1], r, 2e-2)
 
 
-@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float32])
+def test_balanced_large_prefill_head_dim_64(device, forced):
+    """8 requests x 32 heads x 64, chunk 512 over 1-4k contexts, bf16 KV (64-key steps): three
+    calls bit-identical, within 5e-3 of the unbalanced launch, requests 0 and 6 against the oracle
+    on every head."""
+    b = workloads.large_prefill(seed=3, device=device, head_dim=64)
+    assert _balanced_applies(b)
+    print(f"balanced large prefill head_dim 64 ctx={b.extra['prev_lens']}", flush=True)
+    plain = _prefill(b, split_blocks=0)
+    outs = [_prefill(b, split_blocks=PREFILL_BALANCED) for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs:
+        d = float((o - plain).abs().max())
+        print(f"  vs unbalanced: max diff {d:.2e}", flush=True)
+        assert d <= 5e-3
+        assert torch.equal(o, outs[0])
+    for r in (0, 6):
+        _check_large_request(b, outs[-1], r, 2e-2)
+
+
+@pytest.mark.parametrize("kv_dtype,Hd", [(torch.bfloat16, 128), (torch.float32, 128), (torch.bfloat16, 64)])
 @pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
-def test_balanced_ragged_requests(device, forced, io_dtype, kv_dtype):
+def test_balanced_ragged_requests(device, forced, io_dtype, kv_dtype, Hd):
     """6 requests x 32 heads, T = 300 (three tiles, the last one partial): an empty request, a
     request of 3 new tokens behind a 4000-token context (one long pair cut over many gangs), rows
     padded past short chunks; every request against the oracle, the whole batch against the
     unbalanced launch, twice in a row."""
     ctx = [0, 37, 4000, 16, 0, 1200]
     curs = [300, 150, 3, 90, 0, 300]
-    b = make_prefill(device, 41, ctx, curs, T=300, H=32, Hd=128, kv_dtype=kv_dtype)
+    b = make_prefill(device, 41, ctx, curs, T=300, H=32, Hd=Hd, kv_dtype=kv_dtype)
     assert _balanced_applies(b)
     q = b.q.to(io_dtype)
-    print(f"balanced ragged io={io_dtype} kv={kv_dtype}", flush=True)
+    print(f"balanced ragged io={io_dtype} kv={kv_dtype} head_dim={Hd}", flush=True)
     plain = _prefill(b, q=q, split_blocks=0)
     got = _prefill(b, q=q, split_blocks=PREFILL_BALANCED)
     again = _prefill(b, q=q, split_blocks=PREFILL_BALANCED)
@@ -91,17 +110,18 @@ def test_balanced_ragged_requests(device, forced, io_dtype, kv_dtype):
     assert float(got[4].abs().max()) == 0.0  # the empty request
 
 
-def test_balanced_many_heads_and_one_long_request(device, forced):
+@pytest.mark.parametrize("Hd", [128, 64])
+def test_balanced_many_heads_and_one_long_request(device, forced, Hd):
     """64 heads (8 pairs per die and request), one 6000-token context among three short ones (its
     pairs are cut over several gangs each), -1 page entries inside cut tiles: against the
-    unbalanced launch everywhere and the oracle on the long request."""
+    unbalanced launch everywhere and the oracle on the short requests."""
     ctx = [6000, 100, 300]
     curs = [512, 512, 200]
-    b = make_prefill(device, 42, ctx, curs, T=512, H=64, Hd=128, kv_dtype=torch.bfloat16)
+    b = make_prefill(device, 42, ctx, curs, T=512, H=64, Hd=Hd, kv_dtype=torch.bfloat16)
     assert _balanced_applies(b)
     pt = b.page_table.clone()
     pt[0, [5, 130, 131, 300]] = -1
-    print("balanced 64 heads, one long request", flush=True)
+    print(f"balanced 64 heads, one long request, head_dim {Hd}", flush=True)
     plain = _prefill(b, page_table=pt, split_blocks=0)
     got = _prefill(b, page_table=pt, split_blocks=PREFILL_BALANCED)
     torch.cuda.synchronize()
@@ -136,14 +156,15 @@ def test_balanced_needs_its_workspace(device, forced):
     assert "workspace" in lib.pa_last_error_message().decode()
 
 
-def test_balanced_launch_in_a_graph(device, forced):
+@pytest.mark.parametrize("Hd", [128, 64])
+def test_balanced_launch_in_a_graph(device, forced, Hd):
     """The balanced launch captured in a HIP graph (its counters are reset by the kernel, no memset
     in the graph): three replays, each after eager calls of the same launch on other inputs, each
     bit-identical to the eager result on the graph's inputs."""
-    b = workloads.large_prefill(seed=0, device=device, batch=5, ctx_lo=1024, ctx_hi=2048)
-    other = workloads.large_prefill(seed=9, device=device, batch=5, ctx_lo=1024, ctx_hi=2048)
+    b = workloads.large_prefill(seed=0, device=device, batch=5, head_dim=Hd, ctx_lo=1024, ctx_hi=2048)
+    other = workloads.large_prefill(seed=9, device=device, batch=5, head_dim=Hd, ctx_lo=1024, ctx_hi=2048)
     assert _balanced_applies(b) and _balanced_applies(other)
-    print("balanced launch in a graph", flush=True)
+    print(f"balanced launch in a graph, head_dim {Hd}", flush=True)
     out = torch.empty_like(b.q)
     call = lambda: _prefill(b, split_blocks=PREFILL_BALANCED, out=out)
     want = _prefill(b, split_blocks=PREFILL_BALANCED).clone()  # eager; allocates the workspace
@@ -199,3 +220,27 @@ def test_policy_declines_short_contexts_and_sizes_its_grid(device, monkeypatch):
         pytest.skip("the per-CU rule differs at this CU count")
     record = 4 * 17 * 64 * 4 * 4  # four wavefronts x 17 groups x 64 lanes x 16 bytes
     assert need == (64 << 10) + cus * 2 * record  # grid = one workgroup per CU
+
+
+def test_policy_takes_the_balanced_launch_at_head_dim_64(device, monkeypatch):
+    """One request x 8 heads x 64, a 128-token chunk over a 32k context, bf16 KV (8 tiles of 514
+    64-key steps each): the default call takes the balanced launch and matches the unbalanced
+    launch and the oracle on every head; a 512-token chunk over 4k (128 tiles x 68 steps) does not
+    take it."""
+    monkeypatch.delenv("PAGED_HIP_PREFILL_BALANCE", raising=False)
+    b = workloads.large_prefill(seed=17, device=device, batch=1, heads=8, head_dim=64, chunk=128,
+                                ctx_lo=32768, ctx_hi=32768)
+    if 2 * 8 > cu_count(device):
+        pytest.skip("fewer than 16 compute units")
+    assert _balanced_applies(b)
+    lib = _lib.load()
+    assert lib.pa_prefill_workspace_size(1, 32, 512, 64, (4096 + 512) // 16, PREFILL_BALANCED) == 0
+    print("policy: balanced launch on 1 x 8 heads x 64, chunk 128 over 32k", flush=True)
+    got = _prefill(b)
+    monkeypatch.setenv("PAGED_HIP_PREFILL_BALANCE", "off")
+    plain = _prefill(b)
+    torch.cuda.synchronize()
+    d = float((got - plain).abs().max())
+    print(f"  vs unbalanced: max diff {d:.2e}", flush=True)
+    assert d <= 5e-3
+    _check_large_request(b, got, 0, 2e-2)
