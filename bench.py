@@ -614,8 +614,8 @@ def _long_prompt_prefill(res, device, steps):
     # One long prompt: 1 request x 32 heads x 128, a 512-token chunk over an 8k context (128
     # tiles of 128 rows, half a tile per CU), bf16 and fp32 KV; and the benchmark model's head
     # shape (8 heads x 64), a 128-token chunk over a 32k context (8 tiles), bf16 KV. The default
-    # call takes the balanced launch on each; the unbalanced dispatch (the 16-row kernel on the
-    # first two, the split-step kernel on the third) is timed beside it.
+    # call takes the balanced launch on each; the unbalanced dispatch (the 16-row kernel at these
+    # tile counts) is timed beside it.
     for kv_dtype, tag, peak, H, Hd, chunk, ctx, per_cu in (
             (torch.bfloat16, "bf16kv", 2500.0, 32, 128, 512, 8192, "two workgroups"),
             (torch.float32, "fp32", 157.3, 32, 128, 512, 8192, "two workgroups"),
