@@ -613,13 +613,14 @@ def _long_prompt_prefill(res, device, steps):
 
     # One long prompt: 1 request x 32 heads x 128, a 512-token chunk over an 8k context (128
     # tiles of 128 rows, half a tile per CU), bf16 and fp32 KV; and the benchmark model's head
-    # shape (8 heads x 64), a 128-token chunk over a 32k context (8 tiles), bf16 KV. The default
+    # shape (8 heads x 64), a 128-token chunk over a 32k context (8 tiles), bf16 and fp32 KV. The default
     # call takes the balanced launch on each; the unbalanced dispatch (the 16-row kernel at these
     # tile counts) is timed beside it.
     for kv_dtype, tag, peak, H, Hd, chunk, ctx, per_cu in (
             (torch.bfloat16, "bf16kv", 2500.0, 32, 128, 512, 8192, "two workgroups"),
             (torch.float32, "fp32", 157.3, 32, 128, 512, 8192, "two workgroups"),
-            (torch.bfloat16, "bf16kv_head_dim_64", 2500.0, 8, 64, 128, 32768, "one workgroup")):
+            (torch.bfloat16, "bf16kv_head_dim_64", 2500.0, 8, 64, 128, 32768, "one workgroup"),
+            (torch.float32, "fp32_head_dim_64", 157.3, 8, 64, 128, 32768, "one workgroup")):
         b = workloads.large_prefill(seed=16, device=device, batch=1, heads=H, head_dim=Hd, chunk=chunk,
                                     ctx_lo=ctx, ctx_hi=ctx, kv_dtype=kv_dtype)
         flops = workloads.prefill_flops(b.extra["prev_lens"], b.cur_lens, H, Hd)

@@ -723,7 +723,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   constexpr int RPC = HD / 4;            // 16-byte chunks per key row
   constexpr int CPT = KS * RPC / (NW * kWave);
   static_assert(CPT >= 1 && KS * RPC == CPT * NW * kWave, "tile split");
-  static_assert(!BAL || HD == 128, "balanced launch shape");
+  static_assert(!BAL || HD == 128 || HD == 64, "balanced launch shape");
 
   __shared__ __attribute__((aligned(16))) float sk[2][KS * RS];
   __shared__ __attribute__((aligned(16))) float sv[2][KS * RS];
@@ -1048,15 +1048,17 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
               const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
               oacc[d][r] = oacc[d][r] * fa + lo4[gi][e] * fr;
             }
-          f32x4 hi4[8];
-          load_record_hi(rq, hi4);
+          if constexpr (HD == 128) {
+            f32x4 hi4[8];
+            load_record_hi(rq, hi4);
 #pragma unroll
-          for (int gi = 9; gi < 17; ++gi)
+            for (int gi = 9; gi < 17; ++gi)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
-              oacc[d][r] = oacc[d][r] * fa + hi4[gi - 9][e] * fr;
-            }
+              for (int e = 0; e < 4; ++e) {
+                const int d = (gi - 1) / 4, r = 4 * ((gi - 1) % 4) + e;
+                oacc[d][r] = oacc[d][r] * fa + hi4[gi - 9][e] * fr;
+              }
+          }
         }
       }
     }
@@ -1440,8 +1442,8 @@ int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len) 
 // (the smaller of its two output types), per device.
 static int balanced_slots_per_cu(int kv_dtype, int head_dim) {
   constexpr int kMaxDevices = 64;
-  static int cached[3][kMaxDevices] = {};
-  const int kind = kv_dtype == PA_DTYPE_F32 ? 1 : head_dim == 64 ? 2 : 0;
+  static int cached[4][kMaxDevices] = {};
+  const int kind = (kv_dtype == PA_DTYPE_F32 ? 1 : 0) + (head_dim == 64 ? 2 : 0);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
   if (cached[kind][dev] == 0) {
@@ -1451,6 +1453,11 @@ static int balanced_slots_per_cu(int kv_dtype, int head_dim) {
       e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_f32_kernel<float, 128, true>,
                                                         kWideWaves * kWave, 0);
       e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_f32_kernel<uint16_t, 128, true>,
+                                                        kWideWaves * kWave, 0);
+    } else if (kind == 3) {
+      e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_f32_kernel<float, 64, true>,
+                                                        kWideWaves * kWave, 0);
+      e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, prefill_wide_f32_kernel<uint16_t, 64, true>,
                                                         kWideWaves * kWave, 0);
     } else if (kind == 2) {
       e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nf, prefill_wide_kernel<float, 64, kWideNsub64, 2, true>,
@@ -1471,16 +1478,16 @@ static int balanced_slots_per_cu(int kv_dtype, int head_dim) {
 
 int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                               int32_t max_pages, int kv_dtype) {
-  if (!(head_dim == 128 || (head_dim == 64 && kv_dtype == PA_DTYPE_BF16)) || batch < 1 || batch > 255 ||
-      num_heads < kXcds || num_heads % kXcds != 0 || query_len < 1 || max_pages < 0)
+  if ((head_dim != 128 && head_dim != 64) || batch < 1 || batch > 255 || num_heads < kXcds ||
+      num_heads % kXcds != 0 || query_len < 1 || max_pages < 0)
     return 0;
   const int64_t ntiles = (query_len + kWideRows - 1) / kWideRows;
   const int64_t units = (int64_t)batch * num_heads * ntiles;
   if (units * (int64_t)sizeof(int32_t) > (int64_t)PA_PREFILL_COUNTER_BYTES) return 0;
   const int slots = balanced_slots_per_cu(kv_dtype, head_dim);
-  // KV blocks per step: 32-key steps at head_dim 128, 64-key steps at 64 (the same products per
-  // query row).
-  const int nbs = head_dim == 128 ? 2 : 2 * kWideNsub64;
+  // KV blocks per step: 32-key steps, except 64-key steps for bf16 KV at head_dim 64 (the same
+  // products per query row as a 32-key step at 128).
+  const int nbs = head_dim == 64 && kv_dtype == PA_DTYPE_BF16 ? 2 * kWideNsub64 : 2;
   const int64_t cus = pa_host::device_cu_count();
   // Where it pays (MI355X, head_dim 128, graph-free eager timings; default launch -> balanced):
   // few tiles over long contexts, where the default launch leaves CUs idle or each tile walks
@@ -1503,8 +1510,29 @@ int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_le
   // ties at 1 x 32, 512 over 4k (38.8 / 38.1) and 1 x 8, 512 over 8k (32.2 / 31.4); loses at
   // 1 x 16, 512 over 8k (33.1 -> 38.1), 4 x 8, 256 over 4k (19.3 -> 28.5) and 1 x 32, 512 over 2k
   // (25.1 -> 28.8). So at least 16384 tile-steps, or 256 steps (16k keys) per tile.
-  if (head_dim == 64) pays = 2 * units <= cus && (units * steps >= 16384 || steps >= 256);
+  if (head_dim == 64 && kv_dtype == PA_DTYPE_BF16) pays = 2 * units <= cus && (units * steps >= 16384 || steps >= 256);
   int per_cu = 4 * units >= cus ? 2 : 1;  // two per CU cut each tile into 2 cus / units pieces
+  // Head_dim 64, fp32 KV (32-key steps; the alternative is the 16-row kernel, whose B * H *
+  // ceil(T / 16) workgroups leave CUs idle when tiles are few): 1 x 8 heads, 128-token chunk over
+  // 32k 369.6 -> 126.2 us, over 8k 94.5 -> 54.7 us (one workgroup per CU); 512 over 16k 209.2 ->
+  // 173.3 us, 1 x 32, 128 over 16k 190.8 -> 169.8 us, 1 x 32, 512 over 8k 351.7 -> 307.1 us,
+  // 2 x 32, 256 over 8k 354.1 -> 306.6 us (two per CU); ties at 1 x 16, 256 over 8k (98.0 / 98.2)
+  // and 1 x 8, 512 over 8k (113.0 / 104.9); loses at 4 x 8, 256 over 4k (79.9 -> 97.1), 2 x 8,
+  // 512 over 4k (83.7 -> 96.6), 1 x 32, 512 over 2k (99.6 -> 102.6) and 4 x 8, 256 over 768
+  // (23.4 -> 33.9). Checked on further shapes: 1 x 8, 256 over 16k 187.6 -> 107.9 us, 2 x 8, 128
+  // over 16k 186.2 -> 109.6 us, 1 x 8, 512 over 32k 371.0 -> 302.5 us, 2 x 16, 512 over 8k 340.0 ->
+  // 307.5 us, 1 x 32, 512 over 4k 180.4 -> 171.6 us; but 1 x 32, 256 over 8k 151.1 -> 165.9 us and
+  // 1 x 64, 128 over 8k 153.2 -> 176.7 us lose: there the 16-row kernel has two workgroups per
+  // CU, its LDS-staged build at its best. So at least 16384 tile-steps unless the 16-row grid
+  // holds one to two workgroups per CU, or 256 steps per tile at most one tile per 16 CUs; two
+  // workgroups per CU from one tile per 8 CUs.
+  if (head_dim == 64 && kv_dtype == PA_DTYPE_F32) {
+    const int64_t rows16 = (int64_t)batch * num_heads * ((query_len + 15) / 16);
+    const bool rows16_at_best = rows16 > cus && rows16 <= 2 * cus;
+    pays = 2 * units <= cus &&
+           ((units * steps >= 16384 && !rows16_at_best) || (steps >= 256 && 16 * units <= cus));
+    per_cu = 8 * units >= cus ? 2 : 1;
+  }
   if (!pays && units > 2 * cus) per_cu = slots;
   if (const char* env = getenv("PAGED_HIP_PREFILL_BALANCE")) {
     if (strcmp(env, "force") == 0) pays = true;
@@ -1540,7 +1568,10 @@ int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream
     const dim3 grid((unsigned)g);
     AttnArgs ab = a;
     ab.die_cus = pa_host::device_cu_count() / kXcds > 0 ? pa_host::device_cu_count() / kXcds : 1;
-    if (kv_dtype == PA_DTYPE_F32) {
+    if (kv_dtype == PA_DTYPE_F32 && a.head_dim == 64) {
+      if (io_dtype == PA_DTYPE_F32) prefill_wide_f32_kernel<float, 64, true><<<grid, block, 0, stream>>>(ab);
+      else prefill_wide_f32_kernel<uint16_t, 64, true><<<grid, block, 0, stream>>>(ab);
+    } else if (kv_dtype == PA_DTYPE_F32) {
       if (io_dtype == PA_DTYPE_F32) prefill_wide_f32_kernel<float, 128, true><<<grid, block, 0, stream>>>(ab);
       else prefill_wide_f32_kernel<uint16_t, 128, true><<<grid, block, 0, stream>>>(ab);
     } else if (a.head_dim == 64) {

@@ -1,5 +1,5 @@
-"""The balanced launch of the wide prefill kernels (bf16 KV at head_dim 128 and 64, fp32 KV at
-head_dim 128; split_blocks < 0): the tiles' KV steps dealt out evenly over a grid of resident workgroups, tiles cut between
+"""The balanced launch of the wide prefill kernels (bf16 and fp32 KV, head_dim 128 and 64;
+split_blocks < 0): the tiles' KV steps dealt out evenly over a grid of resident workgroups, tiles cut between
 workgroups merged in the same launch by the piece that finishes last; and the library's policy
 for when to take it. Checked against the oracle on the same KV values (bf16 KV 2e-2, fp32 KV
 1e-4) and against the unbalanced launch, on repeated calls (the arrival counters must be left at
@@ -77,7 +77,8 @@ def test_balanced_large_prefill_head_dim_64(device, forced):
         _check_large_request(b, outs[-1], r, 2e-2)
 
 
-@pytest.mark.parametrize("kv_dtype,Hd", [(torch.bfloat16, 128), (torch.float32, 128), (torch.bfloat16, 64)])
+@pytest.mark.parametrize("kv_dtype,Hd", [(torch.bfloat16, 128), (torch.float32, 128), (torch.bfloat16, 64),
+                                         (torch.float32, 64)])
 @pytest.mark.parametrize("io_dtype", [torch.float32, torch.bfloat16])
 def test_balanced_ragged_requests(device, forced, io_dtype, kv_dtype, Hd):
     """6 requests x 32 heads, T = 300 (three tiles, the last one partial): an empty request, a
@@ -222,25 +223,26 @@ def test_policy_declines_short_contexts_and_sizes_its_grid(device, monkeypatch):
     assert need == (64 << 10) + cus * 2 * record  # grid = one workgroup per CU
 
 
-def test_policy_takes_the_balanced_launch_at_head_dim_64(device, monkeypatch):
-    """One request x 8 heads x 64, a 128-token chunk over a 32k context, bf16 KV (8 tiles of 514
-    64-key steps each): the default call takes the balanced launch and matches the unbalanced
-    launch and the oracle on every head; a 512-token chunk over 4k (128 tiles x 68 steps) does not
-    take it."""
+@pytest.mark.parametrize("kv_dtype,tol_plain,tol", [(torch.bfloat16, 5e-3, 2e-2), (torch.float32, 2e-5, 1e-4)])
+def test_policy_takes_the_balanced_launch_at_head_dim_64(device, monkeypatch, kv_dtype, tol_plain, tol):
+    """One request x 8 heads x 64, a 128-token chunk over a 32k context (8 tiles of 514 64-key
+    steps with bf16 KV, 1028 32-key steps with fp32 KV): the default call takes the balanced launch
+    and matches the unbalanced launch and the oracle on every head; 32 heads with a 512-token chunk
+    over 2k (128 tiles x 40 or 80 steps) do not take it with either KV dtype."""
     monkeypatch.delenv("PAGED_HIP_PREFILL_BALANCE", raising=False)
     b = workloads.large_prefill(seed=17, device=device, batch=1, heads=8, head_dim=64, chunk=128,
-                                ctx_lo=32768, ctx_hi=32768)
+                                ctx_lo=32768, ctx_hi=32768, kv_dtype=kv_dtype)
     if 2 * 8 > cu_count(device):
         pytest.skip("fewer than 16 compute units")
     assert _balanced_applies(b)
     lib = _lib.load()
-    assert lib.pa_prefill_workspace_size(1, 32, 512, 64, (4096 + 512) // 16, PREFILL_BALANCED) == 0
-    print("policy: balanced launch on 1 x 8 heads x 64, chunk 128 over 32k", flush=True)
+    assert lib.pa_prefill_workspace_size(1, 32, 512, 64, (2048 + 512) // 16, PREFILL_BALANCED) == 0
+    print(f"policy: balanced launch on 1 x 8 heads x 64, chunk 128 over 32k, kv={kv_dtype}", flush=True)
     got = _prefill(b)
     monkeypatch.setenv("PAGED_HIP_PREFILL_BALANCE", "off")
     plain = _prefill(b)
     torch.cuda.synchronize()
     d = float((got - plain).abs().max())
     print(f"  vs unbalanced: max diff {d:.2e}", flush=True)
-    assert d <= 5e-3
-    _check_large_request(b, got, 0, 2e-2)
+    assert d <= tol_plain
+    _check_large_request(b, got, 0, tol)
