@@ -144,8 +144,8 @@ constexpr int kWideStages64 = WIDE_NST64;
 static bool wide128_pair(int64_t units) { return units <= 2 * (int64_t)pa_host::device_cu_count(); }
 
 // Balanced launch (BAL; bf16 KV at head_dim 128 with one 32-key sub-tile per step or at head_dim
-// 64 with two, fp32 KV at head_dim 128; 2 stages): the grid
-// is the workgroups the compute units hold at once (three per CU), and the KV steps of all tiles are
+// 64 with two, fp32 KV at head_dim 128 and 64 with 32-key steps; 2 stages): the grid
+// is one to three workgroups per CU (no more than the CUs hold at once), and the KV steps of all tiles are
 // dealt out evenly instead of one workgroup per tile. Die k (workgroups x = k mod 8) takes the
 // (request, head) pairs with head = k mod 8, listed by request, then head; a pair's work is the
 // step count of its last (longest) tile, at least 1. The die's workgroups form gangs of ntiles
