@@ -94,7 +94,7 @@ def default_split_blocks(batch: int, num_heads: int, max_pages: int, device: tor
 
 
 # split_blocks value asking pa_prefill for its balanced launch where the library's policy finds it
-# faster (head_dim 128, heads a multiple of 8: few 128-row tiles over long contexts); other calls
+# faster (head_dim 128 or 64, heads a multiple of 8: few 128-row tiles over long contexts); other calls
 # run unsplit. PAGED_HIP_PREFILL_BALANCE=force / off overrides the policy.
 PREFILL_BALANCED = -1
 
@@ -103,7 +103,8 @@ def default_prefill_split_blocks(batch: int, num_heads: int, query_len: int, max
                                  device: torch.device, kv_dtype: torch.dtype | None = None) -> int:
     """split_blocks for a prefill call: PREFILL_BALANCED, so that the library takes the balanced
     launch where it measured faster on MI355X (1 x 32 heads x 128, 512-token chunk over an 8k
-    context: bf16 KV 159 -> 96 us, fp32 KV 807 -> 574 us) and runs unsplit elsewhere. Fixed split-K
+    context: bf16 KV 159 -> 96 us, fp32 KV 807 -> 574 us; 1 x 8 heads x 64, 128-token chunk over
+    32k: bf16 KV 147 -> 47 us, fp32 KV 365 -> 123 us) and runs unsplit elsewhere. Fixed split-K
     (split_blocks > 0) is never the default: its second (merge) launch costs more than the load
     balance it buys, from the chunked-prefill workload (4 x 8 heads, 16-row tiles over up to 58
     blocks: 24.5 us unsplit, 32-95 us split) up to 8 x 32 heads with 512-token chunks. Callers may

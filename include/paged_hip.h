@@ -130,10 +130,13 @@ int pa_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * KV blocks are also cut into ranges of split_blocks blocks, one workgroup each, whose partial
  * results a second kernel merges through a workspace of pa_prefill_workspace_size() bytes.
  * split_blocks == 0 means no split and no workspace. split_blocks < 0 (PA_PREFILL_BALANCED) asks
- * for the balanced launch where the library finds it faster: head_dim 128, num_heads a multiple of
- * 8, batch <= 255, at most one (request, head, 128-row tile) unit per two compute units and at
- * least 8192 unit-steps (units x ceil(max_pages / 2); fp32 KV: 4096 from one unit per four
- * compute units), i.e. few tiles over long contexts. It runs a grid of one or two workgroups per compute unit, deals the tiles' KV steps out
+ * for the balanced launch where the library finds it faster: head_dim 128 or 64, num_heads a
+ * multiple of 8, batch <= 255, at most one (request, head, 128-row tile) unit per two compute units
+ * and at head_dim 128 at least 8192 unit-steps (units x ceil(max_pages / 2); fp32 KV: 4096 from one
+ * unit per four compute units); at head_dim 64 at least 16384 unit-steps (steps of 64 keys for bf16
+ * KV, 32 for fp32 KV) or 256 steps per unit (fp32 KV: at most one unit per 16 compute units), for
+ * fp32 KV not where the 16-row kernel would run one to two workgroups per compute unit; i.e. few
+ * tiles over long contexts. It runs a grid of one or two workgroups per compute unit, deals the tiles' KV steps out
  * evenly among them and merges a tile cut between workgroups in the same launch (the one that
  * finishes it last). Other calls run as with 0. The environment variable
  * PAGED_HIP_PREFILL_BALANCE=force takes it wherever it can run (as many workgroups per compute
