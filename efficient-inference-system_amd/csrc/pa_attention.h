@@ -56,8 +56,9 @@ __device__ __forceinline__ float sum_xor32(float x) {
 bool prefill_wide_supported(int kv_dtype, int head_dim, int block_size);
 int64_t prefill_wide_units(int32_t batch, int32_t num_heads, int32_t query_len);
 int launch_prefill_wide(const AttnArgs& a, int io_dtype, int kv_dtype, hipStream_t stream);
-// Balanced launch of the head_dim 128 bf16 wide kernel: its grid (0 when it does not apply) and
-// the bytes of its split records. launch_prefill_wide takes it when a.counters is set.
+// Balanced launch of the wide kernels (bf16 or fp32 KV, head_dim 128 or 64): its grid (0 when the
+// policy declines or it does not apply) and the bytes of its split records at that grid and
+// head_dim. launch_prefill_wide takes it when a.counters is set.
 int64_t prefill_balanced_grid(int32_t batch, int32_t num_heads, int32_t query_len, int32_t head_dim,
                               int32_t max_pages, int kv_dtype);
 size_t prefill_balanced_record_bytes(int64_t grid, int32_t head_dim);
