@@ -688,10 +688,13 @@ def calibration_copy(device, nbytes: int = 1 << 32) -> None:
 
 
 def box_bandwidth(device, nbytes: int = 4 << 30, reps: int = 10) -> dict:
-    """What this box's HBM delivers, measured in the same process right after the decode timing:
-    a streaming read of `nbytes` with the decode kernel's 16-byte non-temporal loads
-    (pa_hbm_read_probe; the best of five grid sizes) and torch's device copy of nbytes / 2
-    (counted as read + write bytes). HIP events on the stream the kernels run on."""
+    """What this box's HBM delivers, measured in the same process right after the decode timing,
+    with the decode kernel's 16-byte non-temporal loads: a streaming read of `nbytes`
+    (pa_hbm_read_probe, the best over 4 grid sizes x 3 workgroup sizes x 1, 4 or 8 loads in
+    flight per lane), the same bytes as 4 KB chunks in a random order, as a paged KV pool is read
+    (pa_hbm_chunk_read_probe, the best over 4 grid sizes x 1, 2 or 4 chunks in flight per
+    workgroup), and torch's device copy of nbytes / 2 (counted as read + write bytes). HIP events
+    on the stream the kernels run on."""
     import torch
 
     from src.kernels import _lib
@@ -700,15 +703,30 @@ def box_bandwidth(device, nbytes: int = 4 << 30, reps: int = 10) -> dict:
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     stream = torch.cuda.current_stream(device)
     buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-    best = (0.0, 0)
-    for per_cu in (1, 2, 4, 8, 16):
-        wgs = cus * per_cu
-        sink = torch.zeros(wgs, dtype=torch.int32, device=device)
-        call = lambda: _lib.check(lib.pa_hbm_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), wgs,
-                                                        stream.cuda_stream), "pa_hbm_read_probe")
-        ms = time_call(call, reps)
-        best = max(best, (nbytes / (ms * 1e-3) / 1e9, wgs))
-    del buf
+    sink = torch.zeros(16 * cus, dtype=torch.int32, device=device)
+    best = (0.0, "")
+    for per_cu in (1, 2, 4, 8):
+        for threads in (256, 512, 1024):
+            for depth in (1, 4, 8):
+                wgs = cus * per_cu
+                call = lambda: _lib.check(lib.pa_hbm_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), wgs, threads,
+                                                                depth, stream.cuda_stream), "pa_hbm_read_probe")
+                ms = time_call(call, reps)
+                best = max(best, (nbytes / (ms * 1e-3) / 1e9,
+                                  f"{wgs} workgroups of {threads}, {depth} loads in flight per lane"))
+    chunks = nbytes // 4096
+    order = torch.randperm(chunks, generator=torch.Generator().manual_seed(4096)).to(torch.int32).to(device)
+    best_chunk = (0.0, "")
+    for per_cu in (2, 4, 8, 16):
+        for depth in (1, 2, 4):
+            wgs = cus * per_cu
+            call = lambda: _lib.check(lib.pa_hbm_chunk_read_probe(buf.data_ptr(), order.data_ptr(), chunks,
+                                                                  sink.data_ptr(), wgs, depth, stream.cuda_stream),
+                                      "pa_hbm_chunk_read_probe")
+            ms = time_call(call, reps)
+            best_chunk = max(best_chunk, (chunks * 4096 / (ms * 1e-3) / 1e9,
+                                          f"{wgs} workgroups of 256, {depth} chunks in flight per workgroup"))
+    del buf, order, sink
     half = nbytes // 2
     a = torch.zeros(half, dtype=torch.uint8, device=device)
     b = torch.empty_like(a)
@@ -716,7 +734,8 @@ def box_bandwidth(device, nbytes: int = 4 << 30, reps: int = 10) -> dict:
     copy = 2 * half / (ms * 1e-3) / 1e9
     del a, b
     torch.cuda.empty_cache()
-    return {"read_probe_GBps": round(best[0], 1), "read_probe_workgroups": best[1],
+    return {"read_probe_GBps": round(best[0], 1), "read_probe_shape": best[1],
+            "paged_read_probe_GBps": round(best_chunk[0], 1), "paged_read_probe_shape": best_chunk[1],
             "copy_GBps": round(copy, 1), "bytes": nbytes}
 
 
@@ -898,7 +917,8 @@ def main() -> int:
         box = None
         if not args.no_box_calibration:
             box = box_bandwidth(dev)
-            log(f"box: read probe {box['read_probe_GBps']} GB/s, copy {box['copy_GBps']} GB/s")
+            log(f"box: read probe {box['read_probe_GBps']} GB/s, 4 KB chunks in random order "
+                f"{box['paged_read_probe_GBps']} GB/s, copy {box['copy_GBps']} GB/s")
         result.update({
             "value": round(gbs, 2),
             "ms_per_step": round(ms, 4),
@@ -920,15 +940,19 @@ def main() -> int:
             },
         })
         if box is not None:
-            # the same kernel against what this box's HBM delivers to a plain read and a copy, so a
-            # slower box and a slower kernel can be told apart
+            # the same kernel against what this box's HBM delivers to a streaming read, to the
+            # paged pool's access pattern (4 KB slabs in random order) and to a copy, so a slower
+            # box and a slower kernel can be told apart
             result["roofline"].update({
                 "hbm_read_probe_GBps": box["read_probe_GBps"],
                 "frac_vs_read_probe": round(gbs / box["read_probe_GBps"], 4),
+                "hbm_paged_read_probe_GBps": box["paged_read_probe_GBps"],
+                "frac_vs_paged_read_probe": round(gbs / box["paged_read_probe_GBps"], 4),
                 "hbm_copy_GBps": box["copy_GBps"],
                 "frac_vs_copy": round(gbs / box["copy_GBps"], 4),
-                "calibration": f"read probe: {box['bytes']} bytes read once with 16-byte non-temporal loads "
-                               f"({box['read_probe_workgroups']} workgroups of 512, best of 5 grid sizes); "
+                "calibration": f"read probe: {box['bytes']} bytes read once in order with 16-byte non-temporal loads, "
+                               f"best of 36 shapes ({box['read_probe_shape']}); paged read probe: the same bytes as "
+                               f"4 KB chunks in a random order, best of 12 shapes ({box['paged_read_probe_shape']}); "
                                f"copy: torch copy of {box['bytes'] // 2} bytes, read + write counted",
             })
         if not args.no_cpu_baseline:

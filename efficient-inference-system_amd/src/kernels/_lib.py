@@ -138,7 +138,8 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _i64, _i32, _i32,  # logits, row stride, batch, rows per request
          _c_void_p, _i32, _int, _c_void_p, _c_void_p],  # row index, vocab, dtype, tokens, stream
     ),
-    "pa_hbm_read_probe": (_int, [_c_void_p, _size_t, _c_void_p, _i32, _c_void_p]),
+    "pa_hbm_read_probe": (_int, [_c_void_p, _size_t, _c_void_p, _i32, _i32, _i32, _c_void_p]),
+    "pa_hbm_chunk_read_probe": (_int, [_c_void_p, _c_void_p, _i32, _c_void_p, _i32, _i32, _c_void_p]),
     "pa_zero_blocks": (
         _int,
         [_c_void_p, _c_void_p, _int, _i64, _i32, _i32, _i32, _c_void_p, _i32, _c_void_p],

@@ -351,14 +351,27 @@ int pa_mlp_rows(const void* x, int64_t x_stride, int32_t rows, int32_t d_model,
                 void* out, int64_t out_stride, int dtype, void* stream);
 
 /*
- * pa_hbm_read_probe: reads `bytes` (a multiple of 16) of device memory at `src` once, with the
- * 16-byte non-temporal vector loads pa_decode streams KV tiles with, over `workgroups`
- * workgroups of 512 threads; `sink` is a device buffer of `workgroups` uint32 words, which the
- * probe may write for a non-zero buffer (a buffer of zeros leaves it untouched). No counterpart
- * in the reference: it lets a benchmark state the read bandwidth the box delivers beside the
- * decode kernel's, separating the box from the kernel.
+ * pa_hbm_read_probe: reads `bytes` (a multiple of 16) of device memory at `src` once, in order,
+ * with the 16-byte non-temporal vector loads pa_decode streams KV tiles with, over `workgroups`
+ * workgroups of `threads` (256, 512 or 1024) threads, each lane keeping `depth` (1, 4 or 8) loads
+ * in flight; `sink` is a device buffer of `workgroups` uint32 words, which the probe may write
+ * for a non-zero buffer (a buffer of zeros leaves it untouched). No counterpart in the reference:
+ * it lets a benchmark state the read bandwidth the box delivers beside the decode kernel's,
+ * separating the box from the kernel (the best of a sweep over the three shape arguments).
  */
-int pa_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, int32_t workgroups, void* stream);
+int pa_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, int32_t workgroups, int32_t threads,
+                      int32_t depth, void* stream);
+
+/*
+ * pa_hbm_chunk_read_probe: reads `chunks` 4 KB chunks of device memory at `src` (which holds at
+ * least chunks x 4096 bytes) once each, in the order the device array `order` gives (chunk ids in
+ * [0, chunks); other ids are skipped), with the same loads, over `workgroups` workgroups of 256
+ * threads that keep `depth` (1, 2 or 4) chunks in flight; `sink` as for pa_hbm_read_probe. A
+ * random order reads memory as a paged KV pool is read: one (block, head) slab of 16 tokens x 128
+ * values x 2 bytes is one 4 KB chunk. No counterpart in the reference.
+ */
+int pa_hbm_chunk_read_probe(const void* src, const int32_t* order, int32_t chunks, uint32_t* sink,
+                            int32_t workgroups, int32_t depth, void* stream);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,7 @@ def lib():
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
         "pa_argmax_rows", "pa_decode", "pa_decode_noalloc", "pa_decode_workspace_size", "pa_embed_rows",
-        "pa_hbm_read_probe", "pa_kv_append", "pa_last_error_message",
+        "pa_hbm_chunk_read_probe", "pa_hbm_read_probe", "pa_kv_append", "pa_last_error_message",
         "pa_linear_rows", "pa_linear_select_rows", "pa_mlp_rows",
         "pa_pack_metadata", "pa_pack_metadata_mirror", "pa_prefill", "pa_prefill_workspace_size", "pa_qkv_append", "pa_version",
         "pa_zero_blocks",
@@ -82,11 +82,18 @@ def test_argument_errors_are_reported_without_a_device(lib):
     assert b"bad sizes" in lib.pa_last_error_message()
     st = lib.pa_kv_append(None, None, 0, 0, 0, 7, None, None, 0, 0, None, 1, 1, 1, 1, 1, None)
     assert st == _lib.PA_ERR_INVALID_ARGUMENT
-    # the read probe: whole 16-byte vectors only, at least one workgroup; nothing to read is a no-op
-    assert lib.pa_hbm_read_probe(0x10000, 24, 0x10000, 8, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # the read probes: whole 16-byte vectors only, at least one workgroup, the shapes they build;
+    # nothing to read is a no-op (these calls launch nothing)
+    assert lib.pa_hbm_read_probe(0x10000, 24, 0x10000, 8, 512, 8, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert b"multiple of 16" in lib.pa_last_error_message()
-    assert lib.pa_hbm_read_probe(0x10000, 32, 0x10000, 0, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert lib.pa_hbm_read_probe(0x10000, 0, 0x10000, 8, None) == _lib.PA_OK
+    assert lib.pa_hbm_read_probe(0x10000, 32, 0x10000, 0, 512, 8, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_hbm_read_probe(0x10000, 32, 0x10000, 8, 128, 8, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_hbm_read_probe(0x10000, 32, 0x10000, 8, 512, 2, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_hbm_read_probe(0x10000, 0, 0x10000, 8, 512, 8, None) == _lib.PA_OK
+    assert lib.pa_hbm_chunk_read_probe(0x10000, None, 4, 0x10000, 8, 1, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_hbm_chunk_read_probe(0x10000, 0x10000, -1, 0x10000, 8, 1, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_hbm_chunk_read_probe(0x10000, 0x10000, 4, 0x10000, 8, 8, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_hbm_chunk_read_probe(0x10000, 0x10000, 0, 0x10000, 8, 1, None) == _lib.PA_OK
     # zero-sized work is a no-op success
     assert lib.pa_prefill(None, 0, 0, 0, None, 0, 0, 0, 0, None, None, 0, 0, None, 0, 0, None, None,
                           0, 8, 4, 64, 16, 1.0, 0, None, 0, None) == _lib.PA_OK
