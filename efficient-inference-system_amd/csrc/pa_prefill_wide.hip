@@ -260,9 +260,9 @@ void prefill_wide_kernel(const AttnArgs a) {
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
   // Steps of 32 * NSUB keys that tile qt of request b walks (the valid keys of its last row).
-  auto tile_steps = [&](int rb, int rqt) {
+  auto tile_steps = [&](int L, int C, int rqt) {
     const int last = (rqt * kWideRows + kWideRows - 1) < (a.T - 1) ? (rqt * kWideRows + kWideRows - 1) : (a.T - 1);
-    int nbb = (valid_keys(a.seq_lens[rb], a.cur_lens[rb], last) + 15) / 16;  // nondecreasing in the row
+    int nbb = (valid_keys(L, C, last) + 15) / 16;  // nondecreasing in the row
     nbb = nbb < a.max_pages ? nbb : a.max_pages;
     return (nbb + NBS - 1) / NBS;
   };
@@ -278,6 +278,8 @@ void prefill_wide_kernel(const AttnArgs a) {
   __shared__ int sS[kWideWaves * kWave];      // BAL: its prefix sums
   __shared__ int sCw[kWideWaves * kWave];     // BAL: prefix sums of the gangs' share weights
   __shared__ int sLo[kWideWaves * kWave];     // BAL: the gangs' shares: [sLo[g], sLo[g + 1])
+  __shared__ int sL[kWideWaves * kWave];      // BAL: each request's seq_lens and cur_lens, read once
+  __shared__ int sC[kWideWaves * kWave];
   // BAL: the gang whose share holds list position pos (the last g with sLo[g] <= pos).
   auto gang_of = [&](int pos) {
     int lg = 0, ug = NG - 1;
@@ -300,7 +302,10 @@ void prefill_wide_kernel(const AttnArgs a) {
     HP = a.H / kXcds;
     // S[r] = work of requests 0 .. r - 1 per head (at most 255 requests: one thread per entry).
     if (threadIdx.x < a.B) {
-      const int p = tile_steps(threadIdx.x, ntiles - 1);
+      const int L = a.seq_lens[threadIdx.x], C = a.cur_lens[threadIdx.x];
+      sL[threadIdx.x] = L;
+      sC[threadIdx.x] = C;
+      const int p = tile_steps(L, C, ntiles - 1);
       sP[threadIdx.x] = p > 1 ? p : 1;
     }
     __syncthreads();
@@ -314,9 +319,15 @@ void prefill_wide_kernel(const AttnArgs a) {
     // arrive later progress more slowly (the instruction arbiter favours older wavefronts), so
     // earlier gangs take proportionally more steps.
     if (threadIdx.x <= NG) {
-      int s = 0;
-      for (int gg = 0; gg < (int)threadIdx.x; ++gg) s += share_weight(gg * ntiles / a.die_cus);
-      sCw[threadIdx.x] = s;
+      // share_weight(g ntiles / die_cus) summed over g < n: its value is share_weight(0) while
+      // g ntiles < die_cus (g < n0), share_weight(1) while g ntiles < 2 die_cus (g < n1), then
+      // share_weight(2). (Summed in a loop, this table took ~2.5 us of a 48 us launch at 32 gangs
+      // per die; with it and the lengths kept in LDS: 4 x 32 heads x 128, 256-token chunks at two
+      // workgroups per CU 50.0 -> 47.9 us, 1 x 8 heads x 64 over 32k 48.0 -> 45.4 us.)
+      const int n = threadIdx.x;
+      const int n0 = (a.die_cus + ntiles - 1) / ntiles, n1 = (2 * a.die_cus + ntiles - 1) / ntiles;
+      const int c0 = n < n0 ? n : n0, c1 = n < n1 ? n : n1;
+      sCw[threadIdx.x] = share_weight(0) * c0 + share_weight(1) * (c1 - c0) + share_weight(2) * (n - c1);
     }
     __syncthreads();
     W = HP * __builtin_amdgcn_readfirstlane(sS[a.B]);
@@ -353,7 +364,7 @@ void prefill_wide_kernel(const AttnArgs a) {
       if (lo >= hi || pb >= a.B || tile_start >= hi) break;
       s_lo = lo > tile_start ? lo - tile_start : 0;
       s_hi = hi - tile_start < P ? hi - tile_start : P;
-      const int nt = tile_steps(pb, qt);
+      const int nt = tile_steps(__builtin_amdgcn_readfirstlane(sL[pb]), __builtin_amdgcn_readfirstlane(sC[pb]), qt);
       const int ntp = nt > 1 ? nt : 1;
       np = 0;  // no piece of this tile when the share starts past its steps
       if (lo < tile_start + ntp) {
@@ -369,8 +380,8 @@ void prefill_wide_kernel(const AttnArgs a) {
     const int iw = i0 + 32 * w;
     const int i = iw + c;
 
-    const int L = a.seq_lens[b];
-    const int C = a.cur_lens[b];
+    const int L = BAL ? __builtin_amdgcn_readfirstlane(sL[b]) : a.seq_lens[b];
+    const int C = BAL ? __builtin_amdgcn_readfirstlane(sC[b]) : a.cur_lens[b];
     const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
     // Blocks the walk loads: up to the last row of the tile (BAL: of the pair's last tile).
     const int last_row = BAL ? ntiles * kWideRows - 1 : i0 + kWideRows - 1;
@@ -735,9 +746,9 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
 
   const int ntiles = (a.T + kWideRows - 1) / kWideRows;
   // Steps of 32 keys that tile qt of request b walks (the valid keys of its last row).
-  auto tile_steps = [&](int rb, int rqt) {
+  auto tile_steps = [&](int L, int C, int rqt) {
     const int last = (rqt * kWideRows + kWideRows - 1) < (a.T - 1) ? (rqt * kWideRows + kWideRows - 1) : (a.T - 1);
-    int nbb = (valid_keys(a.seq_lens[rb], a.cur_lens[rb], last) + 15) / 16;  // nondecreasing in the row
+    int nbb = (valid_keys(L, C, last) + 15) / 16;  // nondecreasing in the row
     nbb = nbb < a.max_pages ? nbb : a.max_pages;
     return (nbb + NBS - 1) / NBS;
   };
@@ -751,6 +762,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   __shared__ int sS[kWideWaves * kWave];      // BAL: its prefix sums
   __shared__ int sCw[kWideWaves * kWave];     // BAL: prefix sums of the gangs' share weights
   __shared__ int sLo[kWideWaves * kWave];     // BAL: the gangs' shares: [sLo[g], sLo[g + 1])
+  __shared__ int sL[kWideWaves * kWave];      // BAL: each request's seq_lens and cur_lens, read once
+  __shared__ int sC[kWideWaves * kWave];
   auto gang_of = [&](int pos) {
     int lg = 0, ug = NG - 1;
     while (lg < ug) {
@@ -771,7 +784,10 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
     NG = gridDim.x / (kXcds * ntiles);
     HP = a.H / kXcds;
     if (threadIdx.x < a.B) {
-      const int p = tile_steps(threadIdx.x, ntiles - 1);
+      const int L = a.seq_lens[threadIdx.x], C = a.cur_lens[threadIdx.x];
+      sL[threadIdx.x] = L;
+      sC[threadIdx.x] = C;
+      const int p = tile_steps(L, C, ntiles - 1);
       sP[threadIdx.x] = p > 1 ? p : 1;
     }
     __syncthreads();
@@ -781,9 +797,13 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
       sS[threadIdx.x] = s;
     }
     if (threadIdx.x <= NG) {
-      int s = 0;
-      for (int gg = 0; gg < (int)threadIdx.x; ++gg) s += share_weight(gg * ntiles / a.die_cus);
-      sCw[threadIdx.x] = s;
+      // share_weight(g ntiles / die_cus) summed over g < n: its value is share_weight(0) while
+      // g ntiles < die_cus (g < n0), share_weight(1) while g ntiles < 2 die_cus (g < n1), then
+      // share_weight(2).
+      const int n = threadIdx.x;
+      const int n0 = (a.die_cus + ntiles - 1) / ntiles, n1 = (2 * a.die_cus + ntiles - 1) / ntiles;
+      const int c0 = n < n0 ? n : n0, c1 = n < n1 ? n : n1;
+      sCw[threadIdx.x] = share_weight(0) * c0 + share_weight(1) * (c1 - c0) + share_weight(2) * (n - c1);
     }
     __syncthreads();
     W = HP * __builtin_amdgcn_readfirstlane(sS[a.B]);
@@ -814,7 +834,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
     if (lo >= hi || pb >= a.B || tile_start >= hi) break;
     s_lo = lo > tile_start ? lo - tile_start : 0;
     s_hi = hi - tile_start < P ? hi - tile_start : P;
-    const int nt = tile_steps(pb, qt);
+    const int nt = tile_steps(__builtin_amdgcn_readfirstlane(sL[pb]), __builtin_amdgcn_readfirstlane(sC[pb]), qt);
     const int ntp = nt > 1 ? nt : 1;
     np = 0;  // no piece of this tile when the share starts past its steps
     if (lo < tile_start + ntp) {
@@ -830,8 +850,8 @@ __global__ __launch_bounds__(kWideWaves * kWave) void prefill_wide_f32_kernel(co
   const int iw = i0 + 32 * w;
   const int i = iw + c;
 
-  const int L = a.seq_lens[b];
-  const int C = a.cur_lens[b];
+  const int L = BAL ? __builtin_amdgcn_readfirstlane(sL[b]) : a.seq_lens[b];
+  const int C = BAL ? __builtin_amdgcn_readfirstlane(sC[b]) : a.cur_lens[b];
   const int n_c = i < a.T ? valid_keys(L, C, i) : 0;
   // Blocks the walk loads: up to the last row of the tile (BAL: of the pair's last tile, so that
   // a gang's workgroups walk the same steps).
