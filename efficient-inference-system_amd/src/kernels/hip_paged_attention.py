@@ -104,7 +104,7 @@ def default_prefill_split_blocks(batch: int, num_heads: int, query_len: int, max
     """split_blocks for a prefill call: PREFILL_BALANCED, so that the library takes the balanced
     launch where it measured faster on MI355X (1 x 32 heads x 128, 512-token chunk over an 8k
     context: bf16 KV 159 -> 96 us, fp32 KV 807 -> 574 us; 1 x 8 heads x 64, 128-token chunk over
-    32k: bf16 KV 147 -> 47 us, fp32 KV 365 -> 123 us) and runs unsplit elsewhere. Fixed split-K
+    32k: bf16 KV 147 -> 44-47 us, fp32 KV 365 -> 120-123 us) and runs unsplit elsewhere. Fixed split-K
     (split_blocks > 0) is never the default: its second (merge) launch costs more than the load
     balance it buys, from the chunked-prefill workload (4 x 8 heads, 16-row tiles over up to 58
     blocks: 24.5 us unsplit, 32-95 us split) up to 8 x 32 heads with 512-token chunks. Callers may
